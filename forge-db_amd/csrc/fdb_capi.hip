@@ -1,0 +1,272 @@
+// extern "C" boundary: the functions declared in include/forgedb_hip.h.
+// Every entry point catches C++ exceptions and turns them into an
+// fdb_status plus a thread-local message.
+#include <cmath>
+#include <cstring>
+#include <string>
+
+#include "fdb_format.hpp"
+#include "fdb_host.hpp"
+#include "fdb_ivfpq.hpp"
+#include "forgedb_hip.h"
+
+struct fdb_ivfpq {
+  fdb::IvfPqIndex* impl;
+};
+
+namespace fdb {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+
+template <class F>
+fdb_status guarded(F&& f) {
+  try {
+    f();
+    return FDB_OK;
+  } catch (const Error& e) {
+    set_last_error(e.what());
+    return e.status;
+  } catch (const std::bad_alloc&) {
+    set_last_error("host allocation failed");
+    return FDB_ERR_OUT_OF_MEMORY;
+  } catch (const std::exception& e) {
+    set_last_error(e.what());
+    return FDB_ERR_HIP;
+  }
+}
+
+void require_device() {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+    (void)hipGetLastError();
+    throw Error(FDB_ERR_NO_DEVICE, "no HIP device visible");
+  }
+}
+
+// Checks that flat artifacts describe a consistent index.
+void validate(const IvfPqArtifacts& a) {
+  if (a.nlist == 0 || a.dim == 0 || a.M == 0 || a.dim % a.M != 0)
+    throw Error(FDB_ERR_INVALID_ARGUMENT, "nlist, dim and M must be positive with M dividing dim");
+  if (a.metric > 4) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown metric");
+  if (a.offsets.size() != (size_t)a.nlist + 1 || a.offsets[0] != 0)
+    throw Error(FDB_ERR_INVALID_ARGUMENT, "list_offsets must have nlist+1 entries starting at 0");
+  for (uint32_t l = 0; l < a.nlist; ++l)
+    if (a.offsets[l + 1] < a.offsets[l]) throw Error(FDB_ERR_INVALID_ARGUMENT, "list_offsets decrease");
+  if (a.dim > 4096) throw Error(FDB_ERR_UNSUPPORTED, "dim above 4096");
+  if (a.M > 128) throw Error(FDB_ERR_UNSUPPORTED, "more than 128 subvectors");
+}
+
+fdb::IvfPqIndex* H(fdb_ivfpq* h) {
+  if (!h || !h->impl) throw Error(FDB_ERR_INVALID_ARGUMENT, "null index handle");
+  return h->impl;
+}
+const fdb::IvfPqIndex* H(const fdb_ivfpq* h) {
+  if (!h || !h->impl) throw Error(FDB_ERR_INVALID_ARGUMENT, "null index handle");
+  return h->impl;
+}
+
+fdb_ivfpq* wrap(IvfPqArtifacts&& a) {
+  validate(a);
+  auto* impl = new fdb::IvfPqIndex(std::move(a));
+  return new fdb_ivfpq{impl};
+}
+
+}  // namespace fdb
+
+using namespace fdb;
+
+extern "C" {
+
+const char* fdb_last_error(void) { return g_last_error.c_str(); }
+const char* fdb_version(void) { return "forgedb-hip 0.1 gfx950"; }
+
+fdb_status fdb_ivfpq_create(const float* centroids, uint32_t nlist, uint32_t dim,
+                            const float* codebooks, uint32_t M, const uint64_t* list_offsets,
+                            const uint64_t* ids, const uint8_t* codes, uint32_t metric,
+                            fdb_ivfpq** out) {
+  return guarded([&] {
+    if (!out || !centroids || !codebooks || !list_offsets)
+      throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (nlist == 0 || dim == 0 || M == 0 || dim % M != 0)
+      throw Error(FDB_ERR_INVALID_ARGUMENT, "nlist, dim and M must be positive with M dividing dim");
+    require_device();
+    IvfPqArtifacts a;
+    a.nlist = nlist;
+    a.dim = dim;
+    a.M = M;
+    a.dsub = dim / M;
+    a.metric = metric;
+    a.centroids.assign(centroids, centroids + (size_t)nlist * dim);
+    a.codebooks.assign(codebooks, codebooks + (size_t)M * 256 * a.dsub);
+    a.offsets.assign(list_offsets, list_offsets + nlist + 1);
+    const uint64_t n = a.offsets.back();
+    if (n && (!ids || !codes)) throw Error(FDB_ERR_INVALID_ARGUMENT, "null ids or codes");
+    if (n) {
+      a.ids.assign(ids, ids + n);
+      a.codes.assign(codes, codes + n * M);
+    }
+    *out = wrap(std::move(a));
+  });
+}
+
+fdb_status fdb_ivfpq_build(const float* vectors, const uint64_t* ids, uint64_t n, uint32_t dim,
+                           uint32_t n_clusters, uint32_t M, uint32_t metric, uint64_t seed,
+                           fdb_ivfpq** out) {
+  return guarded([&] {
+    if (!out || !vectors) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    require_device();
+    IvfPqArtifacts a = IvfPqIndex::build(vectors, ids, n, dim, n_clusters, M, metric, seed);
+    *out = wrap(std::move(a));
+  });
+}
+
+fdb_status fdb_ivfpq_load(const char* path, fdb_ivfpq** out) {
+  return guarded([&] {
+    if (!out || !path) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    std::vector<uint8_t> file;
+    IoResult r = read_file(path, file);
+    if (r.status) throw Error(r.status, r.message);
+    size_t off = 0;
+    r = verify_header(file, IndexType::IvfPq, off);
+    if (r.status) throw Error(r.status, r.message);
+    IvfPqArtifacts a;
+    r = decode_ivfpq(file.data() + off, file.size() - off, a);
+    if (r.status) throw Error(r.status, r.message);
+    require_device();
+    *out = wrap(std::move(a));
+  });
+}
+
+fdb_status fdb_ivfpq_save(const fdb_ivfpq* h, const char* path) {
+  return guarded([&] {
+    if (!path) throw Error(FDB_ERR_INVALID_ARGUMENT, "null path");
+    const IvfPqIndex* ix = H(h);
+    IvfPqArtifacts a = ix->artifacts();  // copy: nprobe reflects the live value
+    a.nprobe = ix->nprobe();
+    IoResult r = write_file(path, IndexType::IvfPq, encode_ivfpq(a));
+    if (r.status) throw Error(r.status, r.message);
+  });
+}
+
+void fdb_ivfpq_destroy(fdb_ivfpq* h) {
+  if (!h) return;
+  delete h->impl;
+  delete h;
+}
+
+void fdb_ivfpq_set_nprobe(fdb_ivfpq* h, uint64_t nprobe) {
+  if (h && h->impl) h->impl->set_nprobe(nprobe);
+}
+
+uint64_t fdb_ivfpq_nprobe(const fdb_ivfpq* h) { return (h && h->impl) ? h->impl->nprobe() : 0; }
+
+fdb_status fdb_ivfpq_describe(const fdb_ivfpq* h, fdb_ivfpq_desc* out) {
+  return guarded([&] {
+    if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    const IvfPqArtifacts& a = H(h)->artifacts();
+    out->nlist = a.nlist;
+    out->dim = a.dim;
+    out->n_subvectors = a.M;
+    out->subvector_dim = a.dsub;
+    out->n_vectors = a.ids.size();
+    out->metric = a.metric;
+    out->reranking = a.has_originals ? 1 : 0;
+    out->rerank_factor = a.rerank_factor;
+  });
+}
+
+fdb_status fdb_ivfpq_export(const fdb_ivfpq* h, float* centroids, float* codebooks,
+                            uint64_t* list_offsets, uint64_t* ids, uint8_t* codes) {
+  return guarded([&] {
+    const IvfPqArtifacts& a = H(h)->artifacts();
+    if (centroids) std::memcpy(centroids, a.centroids.data(), 4 * a.centroids.size());
+    if (codebooks) std::memcpy(codebooks, a.codebooks.data(), 4 * a.codebooks.size());
+    if (list_offsets) std::memcpy(list_offsets, a.offsets.data(), 8 * a.offsets.size());
+    if (ids) std::memcpy(ids, a.ids.data(), 8 * a.ids.size());
+    if (codes) std::memcpy(codes, a.codes.data(), a.codes.size());
+  });
+}
+
+fdb_status fdb_ivfpq_enable_reranking(fdb_ivfpq* h, const float* v, uint64_t factor) {
+  return guarded([&] {
+    if (!v) throw Error(FDB_ERR_INVALID_ARGUMENT, "null vectors");
+    H(h)->enable_reranking(v, factor);
+  });
+}
+
+fdb_status fdb_ivfpq_search(fdb_ivfpq* h, const float* query, uint32_t dim, uint32_t k,
+                            uint64_t* out_ids, float* out_dists, uint32_t* out_count) {
+  return guarded([&] {
+    IvfPqIndex* ix = H(h);
+    if (!query || !out_count || (k && (!out_ids || !out_dists)))
+      throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (dim != ix->dim()) throw Error(FDB_ERR_DIMENSION_MISMATCH, "query dimension does not match the index");
+    *out_count = ix->search(query, k, out_ids, out_dists);
+  });
+}
+
+fdb_status fdb_ivfpq_batch_search(fdb_ivfpq* h, const float* queries, uint64_t nq, uint32_t dim,
+                                  uint32_t k, uint64_t* out_ids, float* out_dists,
+                                  uint32_t* out_counts) {
+  return guarded([&] {
+    IvfPqIndex* ix = H(h);
+    if (nq && (!queries || !out_counts || (k && (!out_ids || !out_dists))))
+      throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (dim != ix->dim()) throw Error(FDB_ERR_DIMENSION_MISMATCH, "query dimension does not match the index");
+    ix->batch_search(queries, nq, k, out_ids, out_dists, out_counts);
+  });
+}
+
+fdb_status fdb_ivfpq_batch_search_device(fdb_ivfpq* h, const float* d_queries, uint64_t nq,
+                                         uint32_t k, uint64_t* d_out_ids, float* d_out_dists,
+                                         uint32_t* d_out_counts, void* stream) {
+  return guarded([&] {
+    H(h)->batch_search_device(d_queries, nq, k, d_out_ids, d_out_dists, d_out_counts,
+                              (hipStream_t)stream);
+  });
+}
+
+fdb_status fdb_ivfpq_batch_search_device_timed(fdb_ivfpq* h, const float* d_queries, uint64_t nq,
+                                               uint32_t k, uint64_t* d_out_ids, float* d_out_dists,
+                                               uint32_t* d_out_counts, void* stream,
+                                               float* coarse_ms, float* scan_ms) {
+  return guarded([&] {
+    float c = 0.0f, s = 0.0f;
+    H(h)->batch_search_device(d_queries, nq, k, d_out_ids, d_out_dists, d_out_counts,
+                              (hipStream_t)stream, &c, &s);
+    if (coarse_ms) *coarse_ms = c;
+    if (scan_ms) *scan_ms = s;
+  });
+}
+
+fdb_status fdb_ivfpq_sync(fdb_ivfpq* h, void* stream) {
+  return guarded([&] {
+    if (H(h)->sync((hipStream_t)stream)) throw Error(FDB_ERR_NAN, "NaN centroid distance (a query contains NaN)");
+  });
+}
+
+fdb_status fdb_ivfpq_probe(fdb_ivfpq* h, const float* queries, uint64_t nq, uint32_t dim,
+                           uint32_t nprobe, int32_t* out_lists, float* out_dists) {
+  return guarded([&] {
+    IvfPqIndex* ix = H(h);
+    if (nq && (!queries || !out_lists)) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (dim != ix->dim()) throw Error(FDB_ERR_DIMENSION_MISMATCH, "query dimension does not match the index");
+    ix->probe(queries, nq, nprobe, out_lists, out_dists);
+  });
+}
+
+fdb_status fdb_ivfpq_encode(fdb_ivfpq* h, const float* residuals, uint64_t nq, uint32_t dim,
+                            uint8_t* out_codes) {
+  return guarded([&] {
+    IvfPqIndex* ix = H(h);
+    if (nq && (!residuals || !out_codes)) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (dim != ix->dim()) throw Error(FDB_ERR_DIMENSION_MISMATCH, "vector dimension does not match the index");
+    ix->encode(residuals, nq, out_codes);
+  });
+}
+
+}  // extern "C"

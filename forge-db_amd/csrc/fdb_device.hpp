@@ -1,0 +1,254 @@
+// Device-side building blocks shared by the forge-db HIP kernels (gfx950,
+// wave64).  Everything here is compiled with -ffp-contract=off: a product
+// written as `a * b + c` stays a rounded multiply and a rounded add, and the
+// only fused operations are the explicit __builtin_fmaf calls, placed where
+// the reference's AVX2 kernels issue _mm256_fmadd_ps.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fdb {
+
+constexpr int kWave = 64;
+constexpr uint32_t kNoPos = 0xFFFFFFFFu;
+
+__device__ __forceinline__ float f_inf() { return __builtin_huge_valf(); }
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ uint32_t readlane_u(uint32_t v, int lane) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Squared L2 in the reference's AVX2 order (src/distance/simd.rs:335-366):
+// lane l = FMA chain over elements i = l (mod 8) of the full 8-blocks, lanes
+// summed left to right, then the tail i >= 8*floor(n/8) as `total += d*d`
+// (separate multiply and add).  `a` is read element by element, so it may
+// live in LDS (wave-uniform reads broadcast).
+// ---------------------------------------------------------------------------
+template <int N>
+__device__ __forceinline__ float l2sq_ref(const float* __restrict__ a, const float* __restrict__ b) {
+  constexpr int NB = N / 8;
+  float total;
+  if constexpr (NB > 0) {
+    float lane[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      float d = a[l] - b[l];
+      lane[l] = __builtin_fmaf(d, d, 0.0f);
+    }
+#pragma unroll
+    for (int i = 1; i < NB; ++i)
+#pragma unroll
+      for (int l = 0; l < 8; ++l) {
+        float d = a[8 * i + l] - b[8 * i + l];
+        lane[l] = __builtin_fmaf(d, d, lane[l]);
+      }
+    total = lane[0];
+#pragma unroll
+    for (int l = 1; l < 8; ++l) total = total + lane[l];
+  } else {
+    total = 0.0f;
+  }
+#pragma unroll
+  for (int i = 8 * NB; i < N; ++i) {
+    float d = a[i] - b[i];
+    total = total + d * d;
+  }
+  return total;
+}
+
+// Same order for a runtime length.
+__device__ __forceinline__ float l2sq_ref_rt(const float* __restrict__ a, const float* __restrict__ b,
+                                             int n) {
+  const int nb = n / 8;
+  float total = 0.0f;
+  if (nb > 0) {
+    float lane[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) lane[l] = 0.0f;
+    for (int i = 0; i < nb; ++i)
+#pragma unroll
+      for (int l = 0; l < 8; ++l) {
+        float d = a[8 * i + l] - b[8 * i + l];
+        lane[l] = __builtin_fmaf(d, d, lane[l]);
+      }
+    total = lane[0];
+#pragma unroll
+    for (int l = 1; l < 8; ++l) total = total + lane[l];
+  }
+  for (int i = 8 * nb; i < n; ++i) {
+    float d = a[i] - b[i];
+    total = total + d * d;
+  }
+  return total;
+}
+
+// ---------------------------------------------------------------------------
+// ADC summation orders over a flat LUT [M][256] (src/pq.rs).
+// ---------------------------------------------------------------------------
+enum AdcOrder : int {
+  kAdcLanes8 = 0,   // asymmetric_distance_simd_avx2 / batch_..._avx2, pq.rs:318-485
+  kAdcGroups4 = 1,  // asymmetric_distance_fast, pq.rs:218-245
+};
+
+template <int M>
+__device__ __forceinline__ uint32_t code_byte(const uint32_t (&w)[(M + 3) / 4], int m) {
+  return (w[m >> 2] >> (8 * (m & 3))) & 0xFFu;
+}
+
+template <int M, int ORDER>
+__device__ __forceinline__ float adc_sum(const float* __restrict__ lut, const uint32_t (&w)[(M + 3) / 4]) {
+  if constexpr (ORDER == kAdcLanes8) {
+    constexpr int MB = M / 8;
+    float total;
+    if constexpr (MB > 0) {
+      float lane[8];
+#pragma unroll
+      for (int l = 0; l < 8; ++l) lane[l] = lut[l * 256 + code_byte<M>(w, l)];
+#pragma unroll
+      for (int b = 1; b < MB; ++b)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) lane[l] = lane[l] + lut[(8 * b + l) * 256 + code_byte<M>(w, 8 * b + l)];
+      total = lane[0];
+#pragma unroll
+      for (int l = 1; l < 8; ++l) total = total + lane[l];
+    } else {
+      total = 0.0f;
+    }
+#pragma unroll
+    for (int m = 8 * MB; m < M; ++m) total = total + lut[m * 256 + code_byte<M>(w, m)];
+    return total;
+  } else {
+    float sum = 0.0f;
+    constexpr int MG = M / 4;
+#pragma unroll
+    for (int g = 0; g < MG; ++g) {
+      float t = lut[(4 * g) * 256 + code_byte<M>(w, 4 * g)] +
+                lut[(4 * g + 1) * 256 + code_byte<M>(w, 4 * g + 1)];
+      t = t + lut[(4 * g + 2) * 256 + code_byte<M>(w, 4 * g + 2)];
+      t = t + lut[(4 * g + 3) * 256 + code_byte<M>(w, 4 * g + 3)];
+      sum = sum + t;
+    }
+#pragma unroll
+    for (int m = 4 * MG; m < M; ++m) sum = sum + lut[m * 256 + code_byte<M>(w, m)];
+    return sum;
+  }
+}
+
+// Runtime-M versions reading bytes directly.
+template <int ORDER>
+__device__ __forceinline__ float adc_sum_rt(const float* __restrict__ lut, const uint8_t* __restrict__ c,
+                                            int M) {
+  if (ORDER == kAdcLanes8) {
+    const int mb = M / 8;
+    float total = 0.0f;
+    if (mb > 0) {
+      float lane[8];
+#pragma unroll
+      for (int l = 0; l < 8; ++l) lane[l] = lut[l * 256 + c[l]];
+      for (int b = 1; b < mb; ++b)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) lane[l] = lane[l] + lut[(8 * b + l) * 256 + c[8 * b + l]];
+      total = lane[0];
+#pragma unroll
+      for (int l = 1; l < 8; ++l) total = total + lane[l];
+    }
+    for (int m = 8 * mb; m < M; ++m) total = total + lut[m * 256 + c[m]];
+    return total;
+  } else {
+    float sum = 0.0f;
+    int m = 0;
+    for (; m + 4 <= M; m += 4) {
+      float t = lut[m * 256 + c[m]] + lut[(m + 1) * 256 + c[m + 1]];
+      t = t + lut[(m + 2) * 256 + c[m + 2]];
+      t = t + lut[(m + 3) * 256 + c[m + 3]];
+      sum = sum + t;
+    }
+    for (; m < M; ++m) sum = sum + lut[m * 256 + c[m]];
+    return sum;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 top-k.  One sorted list of 64*R (distance, position) pairs spread
+// over the wave: slot s = r*64 + lane lives in register r of that lane.  The
+// list keeps the k smallest values offered so far; a new value goes after
+// existing equal ones, so among exact ties the earliest offered wins.
+// ---------------------------------------------------------------------------
+template <int R>
+struct WaveTopK {
+  float d[R];
+  uint32_t p[R];
+  float tau;  // value in slot k-1 (wave-uniform); +inf until k values arrived
+  int k;
+
+  __device__ __forceinline__ void init(int kk) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      d[r] = f_inf();
+      p[r] = kNoPos;
+    }
+    k = kk;
+    tau = f_inf();
+  }
+
+  __device__ __forceinline__ float slot_value(int s) const {
+    const int rs = s >> 6;
+    float v = d[0];
+#pragma unroll
+    for (int r = 1; r < R; ++r)
+      if (r == rs) v = d[r];
+    return readlane_f(v, s & 63);
+  }
+
+  // Insert one wave-uniform pair.  Caller guarantees dn < tau.
+  __device__ __forceinline__ void insert(float dn, uint32_t pn) {
+    const int lane = lane_id();
+    int pos = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) pos += __popcll(__ballot(d[r] <= dn));
+#pragma unroll
+    for (int r = R - 1; r >= 0; --r) {
+      float up_d = __shfl_up(d[r], 1);
+      uint32_t up_p = __shfl_up(p[r], 1);
+      if (r > 0) {
+        float cd = readlane_f(d[r - 1], 63);
+        uint32_t cp = readlane_u(p[r - 1], 63);
+        if (lane == 0) {
+          up_d = cd;
+          up_p = cp;
+        }
+      }
+      const int s = r * 64 + lane;
+      if (s > pos) {
+        d[r] = up_d;
+        p[r] = up_p;
+      } else if (s == pos) {
+        d[r] = dn;
+        p[r] = pn;
+      }
+    }
+    tau = slot_value(k - 1);
+  }
+
+  // Every lane offers one pair (use +inf to offer nothing).  Lanes are taken
+  // in ascending order.
+  __device__ __forceinline__ void offer(float dist, uint32_t pos) {
+    uint64_t mask = __ballot(dist < tau);
+    while (mask) {
+      const int l = __ffsll((unsigned long long)mask) - 1;
+      mask &= mask - 1;
+      const float dn = readlane_f(dist, l);
+      const uint32_t pn = readlane_u(pos, l);
+      if (dn < tau) insert(dn, pn);
+    }
+  }
+};
+
+}  // namespace fdb

@@ -1,0 +1,65 @@
+// .fdb container and payload codecs (host side).
+//
+// Container (src/persistence/format.rs:82-184, src/persistence/mod.rs:77-94,
+// :169-188): 24-byte little-endian header "FORGEDB\0", version u32 (= 1),
+// index_type u32 (IvfPq 1, Hnsw 2, Ivf 3, BruteForce 4), flags u32,
+// CRC-32/IEEE of the payload u32, then the payload.
+//
+// IVF-PQ payload: bincode 1.x default encoding (fixed-width little-endian
+// integers, u64 sequence lengths, u32 enum variant index, u8 Option tag) of
+// SerializableIVFPQ (src/index/ivf_pq.rs:197-328).
+//
+// Brute-force payload (src/index/brute_force.rs:277-313): metric u8, n u64,
+// dim u64, ids [n] u64, data [n*dim] f32.
+#pragma once
+
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+namespace fdb {
+
+enum class IndexType : uint32_t { IvfPq = 1, Hnsw = 2, Ivf = 3, BruteForce = 4 };
+
+uint32_t crc32_ieee(const uint8_t* data, size_t n);
+
+// Flat form of an IVF-PQ index: the layout the device holds.
+struct IvfPqArtifacts {
+  uint32_t nlist = 0, dim = 0, M = 0, dsub = 0;
+  std::vector<float> centroids;     // [nlist][dim]
+  std::vector<float> codebooks;     // [M][256][dsub]
+  std::vector<uint64_t> offsets;    // [nlist+1]
+  std::vector<uint64_t> ids;        // [N]
+  std::vector<uint8_t> codes;       // [N][M]
+  uint64_t nprobe = 1;
+  uint32_t metric = 0;
+  bool has_originals = false;
+  std::vector<float> originals;     // [N][dim], list order, when has_originals
+  uint64_t rerank_factor = 1;
+};
+
+// Errors are reported as (status, message); status values are fdb_status.
+struct IoResult {
+  int status = 0;
+  std::string message;
+};
+
+IoResult read_file(const std::string& path, std::vector<uint8_t>& out);
+IoResult write_file(const std::string& path, IndexType type, const std::vector<uint8_t>& payload);
+// verify_header: returns the payload offset in `file` through payload_off.
+IoResult verify_header(const std::vector<uint8_t>& file, IndexType expected, size_t& payload_off);
+
+std::vector<uint8_t> encode_ivfpq(const IvfPqArtifacts& a);
+IoResult decode_ivfpq(const uint8_t* p, size_t n, IvfPqArtifacts& a);
+
+struct BruteForceArtifacts {
+  uint32_t metric = 0;
+  uint64_t n = 0, dim = 0;
+  std::vector<uint64_t> ids;
+  std::vector<float> data;
+};
+std::vector<uint8_t> encode_bf(const BruteForceArtifacts& a);
+IoResult decode_bf(const uint8_t* p, size_t n, BruteForceArtifacts& a);
+
+}  // namespace fdb

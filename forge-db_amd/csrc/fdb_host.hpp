@@ -1,0 +1,103 @@
+// Host-side helpers: error propagation, device buffers, and the scalar
+// reference-order distance used by host-side training steps.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cmath>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "forgedb_hip.h"
+
+namespace fdb {
+
+struct Error : std::runtime_error {
+  int status;
+  Error(int s, const std::string& m) : std::runtime_error(m), status(s) {}
+};
+
+void set_last_error(const std::string& msg);
+
+inline void hip_check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return;
+  (void)hipGetLastError();  // clear the sticky launch error
+  const int st = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? FDB_ERR_OUT_OF_MEMORY
+                                                                             : FDB_ERR_HIP;
+  throw Error(st, std::string(what) + ": " + hipGetErrorString(e));
+}
+#define FDB_HIP(expr) ::fdb::hip_check((expr), #expr)
+
+template <class T>
+struct DevBuf {
+  T* p = nullptr;
+  size_t n = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() { release(); }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+  // (re)allocate to hold at least cnt elements; contents are not kept
+  void reserve(size_t cnt) {
+    if (cnt <= n && p) return;
+    release();
+    if (cnt == 0) return;
+    FDB_HIP(hipMalloc((void**)&p, cnt * sizeof(T)));
+    n = cnt;
+  }
+  void upload(const T* src, size_t cnt, hipStream_t s) {
+    reserve(cnt);
+    if (cnt) FDB_HIP(hipMemcpyAsync(p, src, cnt * sizeof(T), hipMemcpyHostToDevice, s));
+  }
+};
+
+// Squared L2 in the reference's AVX2 order (src/distance/simd.rs:335-366),
+// scalar: 8 FMA lanes, lanes summed from -0.0 left to right, scalar tail.
+inline float host_l2sq_ref(const float* a, const float* b, int n) {
+  const int nb = n / 8;
+  float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int i = 0; i < nb; ++i)
+    for (int l = 0; l < 8; ++l) {
+      const float d = a[8 * i + l] - b[8 * i + l];
+      lane[l] = std::fma(d, d, lane[l]);
+    }
+  float total = -0.0f;
+  for (int l = 0; l < 8; ++l) total += lane[l];
+  for (int i = 8 * nb; i < n; ++i) {
+    const float d = a[i] - b[i];
+    total += d * d;
+  }
+  return total;
+}
+
+// SplitMix64: the i-th output for a seed is a pure function of (seed, i).
+inline uint64_t splitmix64_at(uint64_t seed, uint64_t i) {
+  uint64_t z = seed + (i + 1) * 0x9E3779B97F4A7C15ULL;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+  return z ^ (z >> 31);
+}
+
+struct Stream {
+  uint64_t seed, n = 0;
+  explicit Stream(uint64_t s) : seed(s) {}
+  uint64_t next() { return splitmix64_at(seed, n++); }
+  uint64_t index(uint64_t bound) { return (uint64_t)(((unsigned __int128)next() * bound) >> 64); }
+  float unit() { return (float)(next() >> 40) * (1.0f / 16777216.0f); }
+};
+
+// Fisher-Yates from the back (rand 0.8 SliceRandom::shuffle).
+inline void shuffle(Stream& rng, std::vector<uint64_t>& v) {
+  for (uint64_t i = v.size(); i > 1; --i) {
+    const uint64_t j = rng.index(i);
+    std::swap(v[i - 1], v[j]);
+  }
+}
+
+}  // namespace fdb

@@ -1,0 +1,548 @@
+// IVF-PQ index: device layout, search orchestration, GPU build.
+#include "fdb_ivfpq.hpp"
+
+#include <algorithm>
+#include <cstring>
+
+#include "fdb_device.hpp"
+#include "fdb_kernels.hpp"
+
+namespace fdb {
+
+namespace {
+
+__global__ void fill_empty_kernel(uint64_t n, uint32_t k, uint64_t* ids, float* dists,
+                                  uint32_t* counts) {
+  const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < n * k) {
+    ids[e] = ~0ull;
+    dists[e] = f_inf();
+  }
+  if (e < n) counts[e] = 0;
+}
+
+__global__ void iota_probes_kernel(uint64_t nq, uint32_t np, int32_t* probes) {
+  const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < nq * np) probes[e] = (int32_t)(e % np);
+}
+
+__global__ void clear_int_kernel(int* p) { *p = 0; }
+
+// Every list is probed (nprobe >= nlist): no selection runs, but a NaN query
+// still has to be reported as the reference's comparison would panic on it.
+__global__ void nan_check_kernel(const float* __restrict__ q, uint64_t n, int* err) {
+  const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < n && q[e] != q[e]) atomicOr(err, 1);
+}
+
+// rerank_results, ivf_pq.rs:556-582: candidates arrive sorted by ADC
+// distance; each gets sqrt of the exact reference-order squared L2 to its
+// original vector, and a stable ascending order of those (offered in ADC
+// order, ties keep it) is truncated to k.  One wave per query.
+template <int R>
+__global__ __launch_bounds__(64) void rerank_kernel(const float* __restrict__ queries, int dim,
+                                                    const float* __restrict__ originals,
+                                                    const uint64_t* __restrict__ ids,
+                                                    const uint32_t* __restrict__ cand_pos,
+                                                    const uint32_t* __restrict__ cand_cnt,
+                                                    uint32_t fetch_k, uint32_t k,
+                                                    uint64_t* __restrict__ out_ids,
+                                                    float* __restrict__ out_dists,
+                                                    uint32_t* __restrict__ out_counts) {
+  const uint64_t q = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* __restrict__ qv = queries + q * dim;
+  const uint32_t cnt = cand_cnt[q];
+  WaveTopK<R> tk;
+  tk.init((int)k);
+  for (uint32_t base = 0; base < cnt; base += 64) {
+    const uint32_t c = base + lane;
+    float d = f_inf();
+    uint32_t pos = kNoPos;
+    if (c < cnt) {
+      pos = cand_pos[q * fetch_k + c];
+      d = __builtin_sqrtf(l2sq_ref_rt(qv, originals + (uint64_t)pos * dim, dim));
+    }
+    tk.offer(d, pos);
+  }
+  uint32_t count = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t s = r * 64 + lane;
+    const bool valid = s < k && tk.p[r] != kNoPos;
+    count += (uint32_t)__popcll(__ballot(valid));
+    if (s < k) {
+      out_ids[q * k + s] = valid ? ids[tk.p[r]] : ~0ull;
+      out_dists[q * k + s] = valid ? tk.d[r] : f_inf();
+    }
+  }
+  if (lane == 0) out_counts[q] = count;
+}
+
+int regs_for(uint32_t k) {
+  int r = (int)((k + 63) / 64), p = 1;
+  while (p < r) p <<= 1;
+  return p;
+}
+
+hipError_t launch_rerank(const float* queries, uint64_t nq, int dim, const float* originals,
+                         const uint64_t* ids, const uint32_t* cand_pos, const uint32_t* cand_cnt,
+                         uint32_t fetch_k, uint32_t k, uint64_t* out_ids, float* out_dists,
+                         uint32_t* out_counts, hipStream_t s) {
+#define FDB_RR(R)                                                                             \
+  hipLaunchKernelGGL(rerank_kernel<R>, dim3((unsigned)nq), dim3(64), 0, s, queries, dim,      \
+                     originals, ids, cand_pos, cand_cnt, fetch_k, k, out_ids, out_dists,     \
+                     out_counts);                                                             \
+  break;
+  switch (regs_for(k)) {
+    case 1: FDB_RR(1)
+    case 2: FDB_RR(2)
+    case 4: FDB_RR(4)
+    case 8: FDB_RR(8)
+    case 16: FDB_RR(16)
+    default: return hipErrorInvalidValue;
+  }
+#undef FDB_RR
+  return hipGetLastError();
+}
+
+unsigned blocks_for(uint64_t n, unsigned t) { return (unsigned)((n + t - 1) / t); }
+
+// Members of each cluster in ascending point order (a stable counting sort).
+void group_members(const std::vector<int32_t>& assign, int k, std::vector<uint32_t>& off,
+                   std::vector<uint32_t>& members) {
+  for (int32_t a : assign)
+    if (a < 0 || a >= k) throw Error(FDB_ERR_NAN, "assignment failed (NaN distance)");
+  off.assign(k + 1, 0);
+  for (int32_t a : assign) off[a + 1]++;
+  for (int c = 0; c < k; ++c) off[c + 1] += off[c];
+  std::vector<uint32_t> fill(off.begin(), off.end() - 1);
+  members.resize(assign.size());
+  for (size_t i = 0; i < assign.size(); ++i) members[fill[assign[i]]++] = (uint32_t)i;
+}
+
+// KMeans::fit_raw (kmeans.rs:87-193) with a seeded stream: random-sample
+// initialisation above KMEANSPP_THRESHOLD = 64 (constants.rs:25), k-means++
+// otherwise; Lloyd steps on the GPU (assignment with the first-minimum rule,
+// f32 means summed in point order); stop when the mean squared centroid
+// shift (measure_change, kmeans.rs:320-329) is below 0.001
+// (CONVERGENCE_THRESHOLD, constants.rs:29).
+std::vector<float> kmeans_gpu(const float* h_points, uint64_t n, int dim, int k, int max_iters,
+                              uint64_t seed, hipStream_t s) {
+  if (n < (uint64_t)k || k <= 0)
+    throw Error(FDB_ERR_INVALID_ARGUMENT, "k-means needs at least k training vectors");
+  if (n > 0xFFFFFFFFull) throw Error(FDB_ERR_UNSUPPORTED, "k-means sample above 2^32 rows");
+  Stream rng(seed);
+  std::vector<float> cents((size_t)k * dim);
+  auto row = [&](uint64_t i) { return h_points + i * (uint64_t)dim; };
+  if (k > 64) {
+    std::vector<uint64_t> idx(n);
+    for (uint64_t i = 0; i < n; ++i) idx[i] = i;
+    shuffle(rng, idx);
+    for (int c = 0; c < k; ++c) std::memcpy(&cents[(size_t)c * dim], row(idx[c]), 4 * dim);
+  } else {
+    const uint64_t first = rng.index(n);
+    std::memcpy(&cents[0], row(first), 4 * dim);
+    std::vector<float> dist(n, 3.40282347e38f);
+    for (int c = 1; c < k; ++c) {
+      // running min over the centroids chosen so far equals the reference's
+      // fold(f32::MAX, f32::min) over all of them
+      const float* last = &cents[(size_t)(c - 1) * dim];
+      for (uint64_t i = 0; i < n; ++i) dist[i] = std::fmin(dist[i], host_l2sq_ref(row(i), last, dim));
+      float total = -0.0f;
+      for (uint64_t i = 0; i < n; ++i) total += dist[i];
+      uint64_t sel;
+      if (total == 0.0f) {
+        sel = rng.index(n);
+      } else {
+        float r = rng.unit() * total;
+        sel = n - 1;
+        for (uint64_t i = 0; i < n; ++i) {
+          r -= dist[i];
+          if (r <= 0.0f) {
+            sel = i;
+            break;
+          }
+        }
+      }
+      std::memcpy(&cents[(size_t)c * dim], row(sel), 4 * dim);
+    }
+  }
+  DevBuf<float> d_pts, d_c, d_cT, d_next;
+  DevBuf<int32_t> d_assign;
+  DevBuf<uint32_t> d_mem, d_off;
+  d_pts.upload(h_points, n * dim, s);
+  d_c.reserve((size_t)k * dim);
+  d_cT.reserve((size_t)k * dim);
+  d_next.reserve((size_t)k * dim);
+  d_assign.reserve(n);
+  std::vector<int32_t> assign(n);
+  std::vector<uint32_t> off, members;
+  std::vector<float> next((size_t)k * dim);
+  for (int it = 0; it < max_iters; ++it) {
+    FDB_HIP(hipMemcpyAsync(d_c.p, cents.data(), 4 * cents.size(), hipMemcpyHostToDevice, s));
+    FDB_HIP(launch_transpose_centroids(d_c.p, k, dim, d_cT.p, s));
+    FDB_HIP(launch_assign(d_pts.p, n, dim, d_cT.p, k, d_assign.p, s));
+    FDB_HIP(hipMemcpyAsync(assign.data(), d_assign.p, 4 * n, hipMemcpyDeviceToHost, s));
+    FDB_HIP(hipStreamSynchronize(s));
+    group_members(assign, k, off, members);
+    d_mem.upload(members.data(), members.size(), s);
+    d_off.upload(off.data(), off.size(), s);
+    FDB_HIP(launch_kmeans_update(d_pts.p, dim, d_mem.p, d_off.p, k, d_c.p, d_next.p, s));
+    FDB_HIP(hipMemcpyAsync(next.data(), d_next.p, 4 * next.size(), hipMemcpyDeviceToHost, s));
+    FDB_HIP(hipStreamSynchronize(s));
+    float total = -0.0f;
+    for (int c = 0; c < k; ++c)
+      total += host_l2sq_ref(&cents[(size_t)c * dim], &next[(size_t)c * dim], dim);
+    const float change = total / (float)k;
+    cents.swap(next);
+    if (change < 0.001f) break;
+  }
+  return cents;
+}
+
+}  // namespace
+
+IvfPqIndex::IvfPqIndex(IvfPqArtifacts&& art) : host_(std::move(art)) {
+  nprobe_.store(std::min<uint64_t>(host_.nprobe, host_.nlist), std::memory_order_relaxed);
+  FDB_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  for (auto& e : ev_) FDB_HIP(hipEventCreate(&e));
+  const uint64_t N = host_.ids.size();
+  if (N >= 0xFFFFFFFFull) throw Error(FDB_ERR_UNSUPPORTED, "more than 2^32-2 vectors");
+  centroids_.upload(host_.centroids.data(), host_.centroids.size(), stream_);
+  centT_.reserve(host_.centroids.size());
+  FDB_HIP(launch_transpose_centroids(centroids_.p, host_.nlist, host_.dim, centT_.p, stream_));
+  codebooks_.upload(host_.codebooks.data(), host_.codebooks.size(), stream_);
+  std::vector<uint32_t> off32(host_.offsets.begin(), host_.offsets.end());
+  off_.upload(off32.data(), off32.size(), stream_);
+  codes_.upload(host_.codes.data(), std::max<size_t>(host_.codes.size(), 16), stream_);
+  ids_.upload(host_.ids.data(), std::max<size_t>(host_.ids.size(), 1), stream_);
+  if (host_.has_originals) originals_.upload(host_.originals.data(), host_.originals.size(), stream_);
+  err_.reserve(1);
+  hipLaunchKernelGGL(clear_int_kernel, dim3(1), dim3(1), 0, stream_, err_.p);
+  FDB_HIP(hipGetLastError());
+  FDB_HIP(hipStreamSynchronize(stream_));
+}
+
+IvfPqIndex::~IvfPqIndex() {
+  if (stream_) (void)hipStreamSynchronize(stream_);
+  for (auto& e : ev_)
+    if (e) (void)hipEventDestroy(e);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void IvfPqIndex::enable_reranking(const float* v, uint64_t factor) {
+  std::lock_guard<std::mutex> g(mu_);
+  host_.originals.assign(v, v + host_.ids.size() * (uint64_t)host_.dim);
+  host_.has_originals = true;
+  host_.rerank_factor = std::max<uint64_t>(factor, 1);
+  originals_.upload(host_.originals.data(), host_.originals.size(), stream_);
+  FDB_HIP(hipStreamSynchronize(stream_));
+}
+
+void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, int order,
+                     uint64_t* d_ids, float* d_dists, uint32_t* d_counts, hipStream_t s,
+                     float* coarse_ms, float* scan_ms) {
+  if (nq == 0) return;
+  if (k == 0 || np == 0) {
+    hipLaunchKernelGGL(fill_empty_kernel, dim3(blocks_for(nq * std::max<uint32_t>(k, 1), 256)),
+                       dim3(256), 0, s, nq, k, d_ids, d_dists, d_counts);
+    FDB_HIP(hipGetLastError());
+    if (coarse_ms) *coarse_ms = 0.0f;
+    if (scan_ms) *scan_ms = 0.0f;
+    return;
+  }
+  const bool rerank = host_.has_originals;
+  const uint64_t fetch = rerank ? (uint64_t)k * host_.rerank_factor : k;
+  if (fetch > 1024) throw Error(FDB_ERR_UNSUPPORTED, "k * rerank_factor above 1024");
+  if (np > 1024 && np < host_.nlist) throw Error(FDB_ERR_UNSUPPORTED, "nprobe above 1024");
+  probes_.reserve(nq * np);
+  const bool timed = coarse_ms || scan_ms;
+  if (timed) FDB_HIP(hipEventRecord(ev_[0], s));
+  if (np >= host_.nlist) {
+    np = host_.nlist;
+    hipLaunchKernelGGL(iota_probes_kernel, dim3(blocks_for(nq * np, 256)), dim3(256), 0, s, nq, np,
+                       probes_.p);
+    FDB_HIP(hipGetLastError());
+    hipLaunchKernelGGL(nan_check_kernel, dim3(blocks_for(nq * host_.dim, 256)), dim3(256), 0, s,
+                       d_qs, nq * host_.dim, err_.p);
+    FDB_HIP(hipGetLastError());
+  } else {
+    FDB_HIP(launch_coarse_select(d_qs, nq, host_.dim, centT_.p, host_.nlist, (int)np, probes_.p,
+                                 nullptr, err_.p, s));
+  }
+  if (timed) FDB_HIP(hipEventRecord(ev_[1], s));
+  IvfPqScanArgs a{};
+  a.queries = d_qs;
+  a.nq = nq;
+  a.dim = (int)host_.dim;
+  a.M = (int)host_.M;
+  a.dsub = (int)host_.dsub;
+  a.probes = probes_.p;
+  a.np = (int)np;
+  a.nlist = (int)host_.nlist;
+  a.centroids = centroids_.p;
+  a.codebooks = codebooks_.p;
+  a.list_off = off_.p;
+  a.codes = codes_.p;
+  a.ids = ids_.p;
+  a.k = (int)fetch;
+  a.order = order;
+  if (rerank) {
+    cand_ids_.reserve(nq * fetch);
+    cand_d_.reserve(nq * fetch);
+    cand_pos_.reserve(nq * fetch);
+    cand_cnt_.reserve(nq);
+    a.out_ids = cand_ids_.p;
+    a.out_dists = cand_d_.p;
+    a.out_pos = cand_pos_.p;
+    a.out_counts = cand_cnt_.p;
+  } else {
+    a.out_ids = d_ids;
+    a.out_dists = d_dists;
+    a.out_pos = nullptr;
+    a.out_counts = d_counts;
+  }
+  FDB_HIP(launch_ivfpq_scan(a, s));
+  if (rerank)
+    FDB_HIP(launch_rerank(d_qs, nq, (int)host_.dim, originals_.p, ids_.p, cand_pos_.p, cand_cnt_.p,
+                          (uint32_t)fetch, k, d_ids, d_dists, d_counts, s));
+  if (timed) {
+    FDB_HIP(hipEventRecord(ev_[2], s));
+    FDB_HIP(hipEventSynchronize(ev_[2]));
+    if (coarse_ms) FDB_HIP(hipEventElapsedTime(coarse_ms, ev_[0], ev_[1]));
+    if (scan_ms) FDB_HIP(hipEventElapsedTime(scan_ms, ev_[1], ev_[2]));
+  }
+}
+
+uint32_t IvfPqIndex::search(const float* q, uint32_t k, uint64_t* ids, float* dists) {
+  std::lock_guard<std::mutex> g(mu_);
+  const uint32_t np = (uint32_t)std::min<uint64_t>(nprobe(), host_.nlist);  // 0 probes 0 lists
+  q_.upload(q, host_.dim, stream_);
+  const uint32_t kk = std::max<uint32_t>(k, 1);
+  out_ids_.reserve(kk);
+  out_d_.reserve(kk);
+  out_cnt_.reserve(1);
+  run(q_.p, 1, k, np, kAdcGroups4, out_ids_.p, out_d_.p, out_cnt_.p, stream_, nullptr, nullptr);
+  uint32_t cnt = 0;
+  if (k) {
+    FDB_HIP(hipMemcpyAsync(ids, out_ids_.p, 8 * (size_t)k, hipMemcpyDeviceToHost, stream_));
+    FDB_HIP(hipMemcpyAsync(dists, out_d_.p, 4 * (size_t)k, hipMemcpyDeviceToHost, stream_));
+  }
+  FDB_HIP(hipMemcpyAsync(&cnt, out_cnt_.p, 4, hipMemcpyDeviceToHost, stream_));
+  FDB_HIP(hipStreamSynchronize(stream_));
+  int flag = 0;
+  FDB_HIP(hipMemcpy(&flag, err_.p, 4, hipMemcpyDeviceToHost));
+  if (flag) {
+    hipLaunchKernelGGL(clear_int_kernel, dim3(1), dim3(1), 0, stream_, err_.p);
+    FDB_HIP(hipStreamSynchronize(stream_));
+    throw Error(FDB_ERR_NAN, "NaN centroid distance (query contains NaN)");
+  }
+  return cnt;
+}
+
+void IvfPqIndex::batch_search(const float* qs, uint64_t nq, uint32_t k, uint64_t* ids,
+                              float* dists, uint32_t* counts) {
+  if (nq == 0) return;
+  std::lock_guard<std::mutex> g(mu_);
+  // batch_search probes [..=nth]: at least one list (ivf_pq.rs:877-881)
+  const uint32_t np = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(nprobe(), host_.nlist));
+  q_.upload(qs, nq * host_.dim, stream_);
+  const uint32_t kk = std::max<uint32_t>(k, 1);
+  out_ids_.reserve(nq * kk);
+  out_d_.reserve(nq * kk);
+  out_cnt_.reserve(nq);
+  run(q_.p, nq, k, np, kAdcLanes8, out_ids_.p, out_d_.p, out_cnt_.p, stream_, nullptr, nullptr);
+  if (k) {
+    FDB_HIP(hipMemcpyAsync(ids, out_ids_.p, 8 * nq * k, hipMemcpyDeviceToHost, stream_));
+    FDB_HIP(hipMemcpyAsync(dists, out_d_.p, 4 * nq * k, hipMemcpyDeviceToHost, stream_));
+  }
+  FDB_HIP(hipMemcpyAsync(counts, out_cnt_.p, 4 * nq, hipMemcpyDeviceToHost, stream_));
+  FDB_HIP(hipStreamSynchronize(stream_));
+  int flag = 0;
+  FDB_HIP(hipMemcpy(&flag, err_.p, 4, hipMemcpyDeviceToHost));
+  if (flag) {
+    hipLaunchKernelGGL(clear_int_kernel, dim3(1), dim3(1), 0, stream_, err_.p);
+    FDB_HIP(hipStreamSynchronize(stream_));
+    throw Error(FDB_ERR_NAN, "NaN centroid distance (a query contains NaN)");
+  }
+}
+
+void IvfPqIndex::batch_search_device(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids,
+                                     float* d_dists, uint32_t* d_counts, hipStream_t s,
+                                     float* coarse_ms, float* scan_ms) {
+  std::lock_guard<std::mutex> g(mu_);
+  const uint32_t np = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(nprobe(), host_.nlist));
+  run(d_qs, nq, k, np, kAdcLanes8, d_ids, d_dists, d_counts, s ? s : stream_, coarse_ms, scan_ms);
+}
+
+bool IvfPqIndex::sync(hipStream_t s) {
+  std::lock_guard<std::mutex> g(mu_);
+  FDB_HIP(hipStreamSynchronize(s ? s : stream_));
+  int flag = 0;
+  FDB_HIP(hipMemcpy(&flag, err_.p, 4, hipMemcpyDeviceToHost));
+  if (flag) {
+    hipLaunchKernelGGL(clear_int_kernel, dim3(1), dim3(1), 0, stream_, err_.p);
+    FDB_HIP(hipStreamSynchronize(stream_));
+  }
+  return flag != 0;
+}
+
+void IvfPqIndex::probe(const float* qs, uint64_t nq, uint32_t nprobe, int32_t* lists,
+                       float* dists) {
+  if (nq == 0 || nprobe == 0) return;
+  std::lock_guard<std::mutex> g(mu_);
+  if (nprobe > host_.nlist) throw Error(FDB_ERR_INVALID_ARGUMENT, "nprobe above nlist");
+  if (nprobe > 1024) throw Error(FDB_ERR_UNSUPPORTED, "nprobe above 1024");
+  q_.upload(qs, nq * host_.dim, stream_);
+  probes_.reserve(nq * nprobe);
+  probe_d_.reserve(nq * nprobe);
+  FDB_HIP(launch_coarse_select(q_.p, nq, host_.dim, centT_.p, host_.nlist, (int)nprobe, probes_.p,
+                               probe_d_.p, err_.p, stream_));
+  FDB_HIP(hipMemcpyAsync(lists, probes_.p, 4 * nq * nprobe, hipMemcpyDeviceToHost, stream_));
+  if (dists)
+    FDB_HIP(hipMemcpyAsync(dists, probe_d_.p, 4 * nq * nprobe, hipMemcpyDeviceToHost, stream_));
+  FDB_HIP(hipStreamSynchronize(stream_));
+}
+
+void IvfPqIndex::encode(const float* residuals, uint64_t nq, uint8_t* codes) {
+  if (nq == 0) return;
+  std::lock_guard<std::mutex> g(mu_);
+  // encode residuals directly: vectors = residuals, centroid rows = a zero row
+  DevBuf<float> zero;
+  std::vector<float> z(host_.dim, 0.0f);
+  zero.upload(z.data(), z.size(), stream_);
+  std::vector<uint64_t> rows(nq);
+  for (uint64_t i = 0; i < nq; ++i) rows[i] = i;
+  std::vector<int32_t> lists(nq, 0);
+  DevBuf<uint64_t> d_rows;
+  DevBuf<int32_t> d_lists;
+  d_rows.upload(rows.data(), nq, stream_);
+  d_lists.upload(lists.data(), nq, stream_);
+  q_.upload(residuals, nq * host_.dim, stream_);
+  codes_out_.reserve(nq * host_.M);
+  FDB_HIP(launch_pq_encode(q_.p, d_rows.p, d_lists.p, nq, host_.dim, zero.p, codebooks_.p, host_.M,
+                           host_.dsub, codes_out_.p, stream_));
+  FDB_HIP(hipMemcpyAsync(codes, codes_out_.p, nq * host_.M, hipMemcpyDeviceToHost, stream_));
+  FDB_HIP(hipStreamSynchronize(stream_));
+}
+
+// IVFPQIndex::build, ivf_pq.rs:374-506.  Sampling streams:
+//   splitmix64_at(seed, 0)      training-sample shuffle (:383-396)
+//   splitmix64_at(seed, 1)      coarse k-means initialisation (:398-400)
+//   splitmix64_at(seed, 2)      PQ residual-sample shuffle (:422-446)
+//   splitmix64_at(seed, 16 + m) PQ k-means initialisation of subspace m
+IvfPqArtifacts IvfPqIndex::build(const float* vectors, const uint64_t* ids, uint64_t n,
+                                 uint32_t dim, uint32_t nlist, uint32_t M, uint32_t metric,
+                                 uint64_t seed) {
+  if (n == 0 || dim == 0 || nlist == 0 || M == 0 || dim % M != 0)
+    throw Error(FDB_ERR_INVALID_ARGUMENT, "build needs n, dim, nlist > 0 and M dividing dim");
+  if (metric > 4) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown metric");
+  if (n >= 0xFFFFFFFFull) throw Error(FDB_ERR_UNSUPPORTED, "more than 2^32-2 vectors");
+  if (dim > 4096) throw Error(FDB_ERR_UNSUPPORTED, "dim above 4096");
+  for (uint64_t i = 0; i < n * dim; ++i)
+    if (std::isnan(vectors[i])) throw Error(FDB_ERR_NAN, "NaN in the vectors to index");
+  const uint32_t dsub = dim / M;
+  hipStream_t s;
+  FDB_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  struct StreamGuard {
+    hipStream_t s;
+    ~StreamGuard() {
+      (void)hipStreamSynchronize(s);
+      (void)hipStreamDestroy(s);
+    }
+  } guard{s};
+  auto row = [&](uint64_t i) { return vectors + i * (uint64_t)dim; };
+
+  // 1. coarse centroids from a sample of at most 30k vectors
+  const uint64_t ts = std::min<uint64_t>(n, 30000);
+  std::vector<float> sample;
+  if (n <= ts) {
+    sample.assign(vectors, vectors + n * dim);
+  } else {
+    Stream rng(splitmix64_at(seed, 0));
+    std::vector<uint64_t> idx(n);
+    for (uint64_t i = 0; i < n; ++i) idx[i] = i;
+    shuffle(rng, idx);
+    sample.resize(ts * dim);
+    for (uint64_t i = 0; i < ts; ++i) std::memcpy(&sample[i * dim], row(idx[i]), 4 * dim);
+  }
+  std::vector<float> cents = kmeans_gpu(sample.data(), ts, dim, nlist, 25, splitmix64_at(seed, 1), s);
+
+  // 2. assign every vector to its nearest centroid
+  DevBuf<float> d_vec, d_cent, d_centT;
+  DevBuf<int32_t> d_assign;
+  d_vec.upload(vectors, n * dim, s);
+  d_cent.upload(cents.data(), cents.size(), s);
+  d_centT.reserve(cents.size());
+  d_assign.reserve(n);
+  FDB_HIP(launch_transpose_centroids(d_cent.p, nlist, dim, d_centT.p, s));
+  FDB_HIP(launch_assign(d_vec.p, n, dim, d_centT.p, nlist, d_assign.p, s));
+  std::vector<int32_t> assign(n);
+  FDB_HIP(hipMemcpyAsync(assign.data(), d_assign.p, 4 * n, hipMemcpyDeviceToHost, s));
+  FDB_HIP(hipStreamSynchronize(s));
+  for (int32_t a : assign)
+    if (a < 0 || a >= (int32_t)nlist) throw Error(FDB_ERR_NAN, "list assignment failed (NaN distance)");
+
+  // 3. PQ codebooks from the residuals of a shuffled sample of <= 100k
+  const uint64_t ps = std::min<uint64_t>(n, 100000);
+  if (ps < 256) throw Error(FDB_ERR_INVALID_ARGUMENT, "PQ training needs at least 256 vectors");
+  std::vector<float> resid(ps * dim);
+  {
+    Stream rng(splitmix64_at(seed, 2));
+    std::vector<uint64_t> idx(n);
+    for (uint64_t i = 0; i < n; ++i) idx[i] = i;
+    shuffle(rng, idx);
+    for (uint64_t t = 0; t < ps; ++t) {
+      const float* v = row(idx[t]);
+      const float* c = &cents[(size_t)assign[idx[t]] * dim];
+      for (uint32_t j = 0; j < dim; ++j) resid[t * dim + j] = v[j] - c[j];
+    }
+  }
+  std::vector<float> cb((size_t)M * 256 * dsub);
+  std::vector<float> sub(ps * dsub);
+  for (uint32_t m = 0; m < M; ++m) {
+    for (uint64_t t = 0; t < ps; ++t) std::memcpy(&sub[t * dsub], &resid[t * dim + (size_t)m * dsub], 4 * dsub);
+    std::vector<float> c = kmeans_gpu(sub.data(), ps, dsub, 256, 25, splitmix64_at(seed, 16 + m), s);
+    std::memcpy(&cb[(size_t)m * 256 * dsub], c.data(), 4 * c.size());
+  }
+
+  // 4. lists in vector order, codes of the residuals
+  IvfPqArtifacts a;
+  a.nlist = nlist;
+  a.dim = dim;
+  a.M = M;
+  a.dsub = dsub;
+  a.metric = metric;
+  a.nprobe = 1;
+  a.centroids = std::move(cents);
+  a.codebooks = std::move(cb);
+  a.offsets.assign(nlist + 1, 0);
+  for (uint64_t i = 0; i < n; ++i) a.offsets[assign[i] + 1]++;
+  for (uint32_t l = 0; l < nlist; ++l) a.offsets[l + 1] += a.offsets[l];
+  std::vector<uint64_t> fill(a.offsets.begin(), a.offsets.end() - 1);
+  std::vector<uint64_t> rows(n);
+  std::vector<int32_t> row_list(n);
+  for (uint64_t i = 0; i < n; ++i) {
+    const uint64_t p = fill[assign[i]]++;
+    rows[p] = i;
+    row_list[p] = assign[i];
+  }
+  a.ids.resize(n);
+  for (uint64_t p = 0; p < n; ++p) a.ids[p] = ids ? ids[rows[p]] : rows[p];
+  DevBuf<uint64_t> d_rows;
+  DevBuf<int32_t> d_rl;
+  DevBuf<float> d_cb;
+  DevBuf<uint8_t> d_codes;
+  d_rows.upload(rows.data(), n, s);
+  d_rl.upload(row_list.data(), n, s);
+  d_cb.upload(a.codebooks.data(), a.codebooks.size(), s);
+  d_codes.reserve(n * M);
+  FDB_HIP(launch_pq_encode(d_vec.p, d_rows.p, d_rl.p, n, dim, d_cent.p, d_cb.p, M, dsub, d_codes.p, s));
+  a.codes.resize(n * M);
+  FDB_HIP(hipMemcpyAsync(a.codes.data(), d_codes.p, n * M, hipMemcpyDeviceToHost, s));
+  FDB_HIP(hipStreamSynchronize(s));
+  return a;
+}
+
+}  // namespace fdb

@@ -1,0 +1,506 @@
+// forge-db query-path kernels for gfx950 (wave64).
+//
+// coarse_select_kernel  exact squared-L2 query-to-centroid distances in the
+//                       reference's AVX2 order + nprobe selection in registers
+//                       (src/index/ivf_pq.rs:538-553, src/index/ivf.rs:164-177)
+// ivfpq_scan_kernel     per query: residual LUTs in LDS (src/pq.rs:149-189),
+//                       ADC over the probed lists' codes (src/pq.rs:218-485),
+//                       wave64 top-k and merge (src/index/ivf_pq.rs:590-677,
+//                       :850-1047)
+// kmeans_update_kernel, pq_encode_kernel, transpose kernels: build side
+//                       (src/kmeans.rs:87-193, src/pq.rs:114-139)
+#include "fdb_kernels.hpp"
+
+#include <algorithm>
+
+#include "fdb_device.hpp"
+
+namespace fdb {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kCoarseQB = 8;     // queries per workgroup in the coarse kernel
+constexpr int kCoarseChunk = 1024;  // centroids per LDS distance chunk
+
+// ---------------------------------------------------------------------------
+// Coarse selection.  One workgroup: kCoarseQB queries against all centroids.
+// Thread c computes centroid c's distance to each query: for lane l of the
+// reference's 8 FMA lanes it streams rows l*d8 .. l*d8+d8-1 of centT (one
+// coalesced float per lane per row), so each query's 8 lane chains are formed
+// one after another and added to the running total left to right.  Queries
+// sit in LDS in the same permuted order and are read as wave-uniform
+// broadcasts.  Distances for a chunk of centroids go to LDS; each wave then
+// selects for two of the queries with a WaveTopK.
+// ---------------------------------------------------------------------------
+template <int R>
+__global__ __launch_bounds__(kThreads) void coarse_select_kernel(
+    const float* __restrict__ queries, uint64_t nq, int dim, const float* __restrict__ centT,
+    int nlist, int nsel, int32_t* __restrict__ out_lists, float* __restrict__ out_dists,
+    int* __restrict__ err_flag) {
+  extern __shared__ float smem[];
+  float* qs = smem;                         // [QB][dim], permuted
+  float* dist = smem + kCoarseQB * dim;     // [QB][chunk]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const uint64_t q0 = (uint64_t)blockIdx.x * kCoarseQB;
+  const int d8 = dim / 8;
+
+  for (int e = tid; e < kCoarseQB * dim; e += kThreads) {
+    const int qq = e / dim;
+    const int d = e - qq * dim;
+    const int row = (d >= 8 * d8) ? d : (d % 8) * d8 + d / 8;
+    qs[qq * dim + row] = (q0 + qq < nq) ? queries[(q0 + qq) * (uint64_t)dim + d] : 0.0f;
+  }
+
+  constexpr int QW = kCoarseQB / 4;  // queries selected per wave
+  WaveTopK<R> tk[QW];
+#pragma unroll
+  for (int j = 0; j < QW; ++j) tk[j].init(nsel);
+  bool saw_nan = false;
+  __syncthreads();
+
+  for (int c0 = 0; c0 < nlist; c0 += kCoarseChunk) {
+    for (int cc = tid; cc < kCoarseChunk; cc += kThreads) {
+      const int c = c0 + cc;
+      float tot[kCoarseQB];
+#pragma unroll
+      for (int qq = 0; qq < kCoarseQB; ++qq) tot[qq] = 0.0f;
+      if (c < nlist) {
+        for (int l = 0; l < 8 && d8 > 0; ++l) {
+          float chain[kCoarseQB];
+#pragma unroll
+          for (int qq = 0; qq < kCoarseQB; ++qq) chain[qq] = 0.0f;
+          for (int i = 0; i < d8; ++i) {
+            const int row = l * d8 + i;
+            const float cv = centT[(uint64_t)row * nlist + c];
+#pragma unroll
+            for (int qq = 0; qq < kCoarseQB; ++qq) {
+              const float df = qs[qq * dim + row] - cv;
+              chain[qq] = __builtin_fmaf(df, df, chain[qq]);
+            }
+          }
+#pragma unroll
+          for (int qq = 0; qq < kCoarseQB; ++qq) tot[qq] = (l == 0) ? chain[qq] : tot[qq] + chain[qq];
+        }
+        for (int row = 8 * d8; row < dim; ++row) {
+          const float cv = centT[(uint64_t)row * nlist + c];
+#pragma unroll
+          for (int qq = 0; qq < kCoarseQB; ++qq) {
+            const float df = qs[qq * dim + row] - cv;
+            tot[qq] = tot[qq] + df * df;
+          }
+        }
+      }
+#pragma unroll
+      for (int qq = 0; qq < kCoarseQB; ++qq) dist[qq * kCoarseChunk + cc] = tot[qq];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < QW; ++j) {
+      const int qq = wave + 4 * j;
+      for (int cc = 0; cc < kCoarseChunk && c0 + cc < nlist; cc += 64) {
+        const int c = c0 + cc + lane;
+        float dv = f_inf();
+        if (c < nlist) {
+          dv = dist[qq * kCoarseChunk + cc + lane];
+          if (dv != dv) saw_nan = true;
+        }
+        tk[j].offer(dv, (uint32_t)c);
+      }
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < QW; ++j) {
+    const uint64_t q = q0 + wave + 4 * j;
+    if (q >= nq) continue;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int s = r * 64 + lane;
+      if (s < nsel) {
+        out_lists[q * nsel + s] = (int32_t)tk[j].p[r];
+        if (out_dists) out_dists[q * nsel + s] = tk[j].d[r];
+      }
+    }
+  }
+  if (saw_nan && err_flag) atomicOr(err_flag, 1);
+}
+
+template <int R>
+hipError_t launch_coarse_t(const float* queries, uint64_t nq, int dim, const float* centT, int nlist,
+                           int nsel, int32_t* out_lists, float* out_dists, int* err_flag,
+                           hipStream_t stream) {
+  const size_t lds = sizeof(float) * ((size_t)kCoarseQB * dim + (size_t)kCoarseQB * kCoarseChunk);
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)coarse_select_kernel<R>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const uint64_t blocks = (nq + kCoarseQB - 1) / kCoarseQB;
+  hipLaunchKernelGGL(coarse_select_kernel<R>, dim3((unsigned)blocks), dim3(kThreads), lds, stream,
+                     queries, nq, dim, centT, nlist, nsel, out_lists, out_dists, err_flag);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Fused IVF-PQ scan.  One workgroup per query.  The probed lists are taken G
+// at a time: the G residuals q - c_p go to LDS, then thread t (one per
+// codeword) builds entry t of every subspace table for all G lists, holding
+// the codeword in registers and reading the residual as a wave-uniform LDS
+// broadcast, so each codebook row is fetched once per G lists.  The scan
+// streams each list's codes (one code vector per lane, coalesced), sums the
+// LDS table entries in the requested reference order and feeds a per-wave
+// top-k; the four wave lists are merged at the end.
+// ---------------------------------------------------------------------------
+template <int MT>
+__device__ __forceinline__ void load_code(const uint8_t* __restrict__ codes, uint32_t i,
+                                          uint32_t (&w)[(MT + 3) / 4]) {
+  if constexpr (MT % 16 == 0) {
+    const uint4* p = reinterpret_cast<const uint4*>(codes + (uint64_t)i * MT);
+#pragma unroll
+    for (int t = 0; t < MT / 16; ++t) {
+      const uint4 v = p[t];
+      w[4 * t] = v.x;
+      w[4 * t + 1] = v.y;
+      w[4 * t + 2] = v.z;
+      w[4 * t + 3] = v.w;
+    }
+  } else if constexpr (MT % 8 == 0) {
+    const uint2* p = reinterpret_cast<const uint2*>(codes + (uint64_t)i * MT);
+#pragma unroll
+    for (int t = 0; t < MT / 8; ++t) {
+      const uint2 v = p[t];
+      w[2 * t] = v.x;
+      w[2 * t + 1] = v.y;
+    }
+  } else {
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(codes + (uint64_t)i * MT);
+#pragma unroll
+    for (int t = 0; t < MT / 4; ++t) w[t] = p[t];
+  }
+}
+
+template <int MT, int DT, int R, int ORDER>
+__global__ __launch_bounds__(kThreads) void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
+  extern __shared__ float smem[];
+  const int M = MT ? MT : a.M;
+  const int dsub = DT ? DT : a.dsub;
+  const int D = M * dsub;
+  float* lut = smem;                          // [G][M][256]
+  float* resid = smem + (size_t)G * M * 256;  // [G][D]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const uint64_t q = blockIdx.x;
+  const float* __restrict__ qv = a.queries + q * D;
+  const int32_t* __restrict__ pr = a.probes + q * (uint64_t)a.np;
+
+  WaveTopK<R> tk;
+  tk.init(a.k);
+
+  for (int g0 = 0; g0 < a.np; g0 += G) {
+    const int ng = min(G, a.np - g0);
+    for (int e = tid; e < ng * D; e += kThreads) {
+      const int j = e / D;
+      const int d = e - j * D;
+      const int p = pr[g0 + j];
+      // a probe slot left empty (NaN distances) has p = -1: no list to scan
+      resid[j * D + d] = (p >= 0 && p < a.nlist) ? qv[d] - a.centroids[(uint64_t)p * D + d] : 0.0f;
+    }
+    __syncthreads();
+    for (int m = 0; m < M; ++m) {
+      const float* __restrict__ cbp = a.codebooks + ((uint64_t)m * 256 + tid) * dsub;
+      if constexpr (DT > 0) {
+        float cbv[DT];
+#pragma unroll
+        for (int t = 0; t < DT; ++t) cbv[t] = cbp[t];
+        for (int j = 0; j < ng; ++j)
+          lut[(j * M + m) * 256 + tid] = l2sq_ref<DT>(resid + j * D + m * DT, cbv);
+      } else {
+        for (int j = 0; j < ng; ++j)
+          lut[(j * M + m) * 256 + tid] = l2sq_ref_rt(resid + j * D + m * dsub, cbp, dsub);
+      }
+    }
+    __syncthreads();
+    for (int j = 0; j < ng; ++j) {
+      const int p = pr[g0 + j];
+      if (p < 0 || p >= a.nlist) continue;  // uniform across the workgroup
+      const uint32_t s = a.list_off[p];
+      const uint32_t e = a.list_off[p + 1];
+      const float* __restrict__ L = lut + (size_t)j * M * 256;
+      for (uint32_t base = s; base < e; base += kThreads) {
+        const uint32_t i = base + tid;
+        float dist = f_inf();
+        if (i < e) {
+          if constexpr (MT > 0) {
+            uint32_t w[(MT + 3) / 4];
+            load_code<MT>(a.codes, i, w);
+            dist = adc_sum<MT, ORDER>(L, w);
+          } else {
+            dist = adc_sum_rt<ORDER>(L, a.codes + (uint64_t)i * M, M);
+          }
+        }
+        tk.offer(dist, i);
+      }
+    }
+    __syncthreads();
+  }
+
+  // merge the four wave lists in wave 0
+  float* md = smem;
+  uint32_t* mp = reinterpret_cast<uint32_t*>(smem + 4 * 64 * R);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    md[wave * 64 * R + r * 64 + lane] = tk.d[r];
+    mp[wave * 64 * R + r * 64 + lane] = tk.p[r];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w = 1; w < 4; ++w)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int s = w * 64 * R + r * 64 + lane;
+      tk.offer(md[s], mp[s]);
+    }
+  const int k = a.k;
+  uint32_t count = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int s = r * 64 + lane;
+    const bool valid = (s < k) && (tk.p[r] != kNoPos);
+    count += (uint32_t)__popcll(__ballot(valid));
+    if (s < k) {
+      a.out_ids[q * k + s] = valid ? a.ids[tk.p[r]] : ~0ull;
+      a.out_dists[q * k + s] = valid ? tk.d[r] : f_inf();
+      if (a.out_pos) a.out_pos[q * k + s] = valid ? tk.p[r] : kNoPos;
+    }
+  }
+  if (lane == 0) a.out_counts[q] = count;
+}
+
+using ScanFn = void (*)(IvfPqScanArgs, int);
+
+template <int MT, int DT, int ORDER>
+ScanFn pick_scan_r(int R) {
+  switch (R) {
+    case 1: return ivfpq_scan_kernel<MT, DT, 1, ORDER>;
+    case 2: return ivfpq_scan_kernel<MT, DT, 2, ORDER>;
+    case 4: return ivfpq_scan_kernel<MT, DT, 4, ORDER>;
+    case 8: return ivfpq_scan_kernel<MT, DT, 8, ORDER>;
+    case 16: return ivfpq_scan_kernel<MT, DT, 16, ORDER>;
+  }
+  return nullptr;
+}
+
+template <int MT, int DT>
+ScanFn pick_scan(int R, int order) {
+  return order == kAdcLanes8 ? pick_scan_r<MT, DT, kAdcLanes8>(R) : pick_scan_r<MT, DT, kAdcGroups4>(R);
+}
+
+int topk_regs(int k) {
+  int r = (k + 63) / 64;
+  int p = 1;
+  while (p < r) p <<= 1;
+  return p;
+}
+
+// ---------------------------------------------------------------------------
+// Build side.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void transpose_centroids_kernel(const float* __restrict__ cents,
+                                                                       int k, int dim,
+                                                                       float* __restrict__ centT) {
+  const uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (e >= (uint64_t)k * dim) return;
+  const int c = (int)(e / dim);
+  const int d = (int)(e - (uint64_t)c * dim);
+  const int d8 = dim / 8;
+  const int row = (d >= 8 * d8) ? d : (d % 8) * d8 + d / 8;
+  centT[(uint64_t)row * k + c] = cents[e];
+}
+
+// One workgroup per cluster; thread t owns dimensions t, t+256, ...; the
+// members are added in ascending point order, as the reference's sequential
+// loop over points does.
+__global__ __launch_bounds__(kThreads) void kmeans_update_kernel(
+    const float* __restrict__ points, int dim, const uint32_t* __restrict__ members,
+    const uint32_t* __restrict__ member_off, const float* __restrict__ old_cents,
+    float* __restrict__ new_cents) {
+  const int c = blockIdx.x;
+  const uint32_t s = member_off[c], e = member_off[c + 1];
+  for (int d = threadIdx.x; d < dim; d += kThreads) {
+    float out;
+    if (s == e) {
+      out = old_cents[(uint64_t)c * dim + d];
+    } else {
+      float sum = 0.0f;
+      for (uint32_t i = s; i < e; ++i) sum = sum + points[(uint64_t)members[i] * dim + d];
+      out = sum / (float)(e - s);
+    }
+    new_cents[(uint64_t)c * dim + d] = out;
+  }
+}
+
+// Thread per (row, subspace): argmin over the 256 codewords with the first
+// minimum kept (min_by), distances in the reference order on the residual
+// r = x - c computed in f32.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void pq_encode_kernel(
+    const float* __restrict__ vectors, const uint64_t* __restrict__ rows,
+    const int32_t* __restrict__ row_list, uint64_t n, int dim, const float* __restrict__ centroids,
+    const float* __restrict__ codebooks, int M, int dsub_rt, uint8_t* __restrict__ codes) {
+  const int dsub = DT ? DT : dsub_rt;
+  const uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (e >= n * (uint64_t)M) return;
+  const uint64_t p = e / M;
+  const int m = (int)(e - p * M);
+  const float* __restrict__ x = vectors + rows[p] * (uint64_t)dim + (uint64_t)m * dsub;
+  const float* __restrict__ c = centroids + (uint64_t)row_list[p] * dim + (uint64_t)m * dsub;
+  const float* __restrict__ cb = codebooks + (uint64_t)m * 256 * dsub;
+  float best;
+  int bi = 0;
+  if constexpr (DT > 0) {
+    float r[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) r[t] = x[t] - c[t];
+    best = l2sq_ref<DT>(r, cb);
+    for (int j = 1; j < 256; ++j) {
+      const float d = l2sq_ref<DT>(r, cb + j * DT);
+      if (best > d) {
+        best = d;
+        bi = j;
+      }
+    }
+  } else {
+    // residual recomputed per codeword; x[t] - c[t] rounds identically each time
+    auto dist_to = [&](int j) {
+      const float* b = cb + (uint64_t)j * dsub;
+      const int nb = dsub / 8;
+      float total = 0.0f;
+      if (nb > 0) {
+        float lane[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) lane[l] = 0.0f;
+        for (int i = 0; i < nb; ++i)
+#pragma unroll
+          for (int l = 0; l < 8; ++l) {
+            const float df = (x[8 * i + l] - c[8 * i + l]) - b[8 * i + l];
+            lane[l] = __builtin_fmaf(df, df, lane[l]);
+          }
+        total = lane[0];
+#pragma unroll
+        for (int l = 1; l < 8; ++l) total = total + lane[l];
+      }
+      for (int i = 8 * nb; i < dsub; ++i) {
+        const float df = (x[i] - c[i]) - b[i];
+        total = total + df * df;
+      }
+      return total;
+    };
+    best = dist_to(0);
+    for (int j = 1; j < 256; ++j) {
+      const float d = dist_to(j);
+      if (best > d) {
+        best = d;
+        bi = j;
+      }
+    }
+  }
+  codes[p * M + m] = (uint8_t)bi;
+}
+
+}  // namespace
+
+hipError_t launch_coarse_select(const float* queries, uint64_t nq, int dim, const float* centT,
+                                int nlist, int nsel, int32_t* out_lists, float* out_dists,
+                                int* err_flag, hipStream_t stream) {
+  if (nq == 0) return hipSuccess;
+  if (nsel <= 0 || nsel > 1024 || nlist <= 0 || dim <= 0) return hipErrorInvalidValue;
+  switch (topk_regs(nsel)) {
+    case 1: return launch_coarse_t<1>(queries, nq, dim, centT, nlist, nsel, out_lists, out_dists, err_flag, stream);
+    case 2: return launch_coarse_t<2>(queries, nq, dim, centT, nlist, nsel, out_lists, out_dists, err_flag, stream);
+    case 4: return launch_coarse_t<4>(queries, nq, dim, centT, nlist, nsel, out_lists, out_dists, err_flag, stream);
+    case 8: return launch_coarse_t<8>(queries, nq, dim, centT, nlist, nsel, out_lists, out_dists, err_flag, stream);
+    case 16: return launch_coarse_t<16>(queries, nq, dim, centT, nlist, nsel, out_lists, out_dists, err_flag, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_ivfpq_scan(const IvfPqScanArgs& a, hipStream_t stream) {
+  if (a.nq == 0) return hipSuccess;
+  if (a.k <= 0 || a.k > 1024 || a.M <= 0 || a.dsub <= 0) return hipErrorInvalidValue;
+  const int R = topk_regs(a.k);
+  ScanFn fn;
+  int G;
+  if (a.M == 16 && a.dsub == 8) {
+    fn = pick_scan<16, 8>(R, a.order);
+    G = 4;
+  } else if (a.M == 32 && a.dsub == 3) {
+    fn = pick_scan<32, 3>(R, a.order);
+    G = 2;
+  } else {
+    fn = pick_scan<0, 0>(R, a.order);
+    G = std::max(1, std::min(8, 64 / a.M));
+  }
+  if (!fn) return hipErrorInvalidValue;
+  const size_t lut_bytes = sizeof(float) * ((size_t)G * a.M * 256 + (size_t)G * a.dim);
+  const size_t merge_bytes = (size_t)4 * 64 * R * 8;
+  const size_t lds = std::max(lut_bytes, merge_bytes);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     160 * 1024);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(fn, dim3((unsigned)a.nq), dim3(kThreads), lds, stream, a, G);
+  return hipGetLastError();
+}
+
+hipError_t launch_kmeans_update(const float* points, int dim, const uint32_t* members,
+                                const uint32_t* member_off, int k, const float* old_cents,
+                                float* new_cents, hipStream_t stream) {
+  if (k <= 0) return hipSuccess;
+  hipLaunchKernelGGL(kmeans_update_kernel, dim3(k), dim3(kThreads), 0, stream, points, dim, members,
+                     member_off, old_cents, new_cents);
+  return hipGetLastError();
+}
+
+hipError_t launch_pq_encode(const float* vectors, const uint64_t* rows, const int32_t* row_list,
+                            uint64_t n, int dim, const float* centroids, const float* codebooks,
+                            int M, int dsub, uint8_t* codes, hipStream_t stream) {
+  const uint64_t total = n * (uint64_t)M;
+  if (total == 0) return hipSuccess;
+  const unsigned blocks = (unsigned)((total + kThreads - 1) / kThreads);
+  switch (dsub) {
+    case 8:
+      hipLaunchKernelGGL(pq_encode_kernel<8>, dim3(blocks), dim3(kThreads), 0, stream, vectors, rows,
+                         row_list, n, dim, centroids, codebooks, M, dsub, codes);
+      break;
+    case 3:
+      hipLaunchKernelGGL(pq_encode_kernel<3>, dim3(blocks), dim3(kThreads), 0, stream, vectors, rows,
+                         row_list, n, dim, centroids, codebooks, M, dsub, codes);
+      break;
+    case 4:
+      hipLaunchKernelGGL(pq_encode_kernel<4>, dim3(blocks), dim3(kThreads), 0, stream, vectors, rows,
+                         row_list, n, dim, centroids, codebooks, M, dsub, codes);
+      break;
+    default:
+      hipLaunchKernelGGL(pq_encode_kernel<0>, dim3(blocks), dim3(kThreads), 0, stream, vectors, rows,
+                         row_list, n, dim, centroids, codebooks, M, dsub, codes);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_transpose_centroids(const float* cents, int k, int dim, float* centT,
+                                      hipStream_t stream) {
+  const uint64_t total = (uint64_t)k * dim;
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(transpose_centroids_kernel, dim3((unsigned)((total + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, stream, cents, k, dim, centT);
+  return hipGetLastError();
+}
+
+}  // namespace fdb

@@ -1,0 +1,325 @@
+"""forgedb — Python mirror of forge-db's query-path API on MI355X.
+
+Thin ctypes layer over ``lib/libforgedb_hip.so`` (the C ABI declared in
+``include/forgedb_hip.h``).  Names, argument meaning and error behaviour follow
+the reference's Rust API:
+
+* ``IVFPQIndex``  — src/index/ivf_pq.rs: ``build``, ``set_nprobe``/``nprobe``,
+  ``search``, ``batch_search``, ``batch_search_parallel``, ``save``/``load``,
+  ``enable_reranking``.
+* ``DistanceMetric`` — src/distance/mod.rs:17-32.
+
+There is no CPU fallback: when the HIP library is absent, importing works but
+every constructor raises ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+import os
+from typing import List, Optional, Sequence, Tuple
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libforgedb_hip.so")
+
+__all__ = [
+    "DistanceMetric", "ForgeDbError", "IVFPQIndex", "load_library", "LIB_PATH",
+    "EXPORTED_SYMBOLS",
+]
+
+# every symbol declared in include/forgedb_hip.h
+EXPORTED_SYMBOLS = (
+    "fdb_last_error", "fdb_version",
+    "fdb_ivfpq_create", "fdb_ivfpq_build", "fdb_ivfpq_load", "fdb_ivfpq_save",
+    "fdb_ivfpq_destroy", "fdb_ivfpq_set_nprobe", "fdb_ivfpq_nprobe",
+    "fdb_ivfpq_describe", "fdb_ivfpq_export", "fdb_ivfpq_enable_reranking",
+    "fdb_ivfpq_search", "fdb_ivfpq_batch_search", "fdb_ivfpq_batch_search_device",
+    "fdb_ivfpq_sync", "fdb_ivfpq_probe", "fdb_ivfpq_encode",
+    "fdb_ivfpq_batch_search_device_timed",
+)
+
+
+class DistanceMetric(enum.IntEnum):
+    """src/distance/mod.rs:17-32 (ordinals as the brute-force metric byte)."""
+    Euclidean = 0
+    EuclideanSquared = 1
+    Cosine = 2
+    DotProduct = 3
+    Manhattan = 4
+
+
+STATUS_NAMES = {
+    0: "Ok", -1: "InvalidArgument", -2: "DimensionMismatch", -3: "NaN",
+    -4: "OutOfMemory", -5: "Hip", -6: "Io", -7: "InvalidFormat",
+    -8: "ChecksumMismatch", -9: "Unsupported", -10: "NoDevice",
+}
+
+
+class ForgeDbError(RuntimeError):
+    """A nonzero fdb_status; ``.status`` holds the code, ``.kind`` its name."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        self.kind = STATUS_NAMES.get(status, str(status))
+        super().__init__(f"{self.kind}: {message}")
+
+
+class _Desc(C.Structure):
+    _fields_ = [("nlist", C.c_uint32), ("dim", C.c_uint32), ("n_subvectors", C.c_uint32),
+                ("subvector_dim", C.c_uint32), ("n_vectors", C.c_uint64),
+                ("metric", C.c_uint32), ("reranking", C.c_uint32),
+                ("rerank_factor", C.c_uint64)]
+
+
+_lib_handle = None
+_P = C.c_void_p
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    """Load the HIP library (once).  Raises RuntimeError when it is not built."""
+    global _lib_handle
+    if _lib_handle is not None:
+        return _lib_handle
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"forgedb HIP library not found at {path}; build it with "
+            "`python -c 'import __graft_entry__ as g; g.build()'` (make -C forge-db_amd)")
+    lib = C.CDLL(path)
+    lib.fdb_last_error.restype = C.c_char_p
+    lib.fdb_version.restype = C.c_char_p
+    st = C.c_int32
+    sig = {
+        "fdb_ivfpq_create": [_P, C.c_uint32, C.c_uint32, _P, C.c_uint32, _P, _P, _P, C.c_uint32, _P],
+        "fdb_ivfpq_build": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                            C.c_uint64, _P],
+        "fdb_ivfpq_load": [C.c_char_p, _P],
+        "fdb_ivfpq_save": [_P, C.c_char_p],
+        "fdb_ivfpq_describe": [_P, _P],
+        "fdb_ivfpq_export": [_P, _P, _P, _P, _P, _P],
+        "fdb_ivfpq_enable_reranking": [_P, _P, C.c_uint64],
+        "fdb_ivfpq_search": [_P, _P, C.c_uint32, C.c_uint32, _P, _P, _P],
+        "fdb_ivfpq_batch_search": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, _P, _P, _P],
+        "fdb_ivfpq_batch_search_device": [_P, _P, C.c_uint64, C.c_uint32, _P, _P, _P, _P],
+        "fdb_ivfpq_batch_search_device_timed": [_P, _P, C.c_uint64, C.c_uint32, _P, _P, _P, _P,
+                                                _P, _P],
+        "fdb_ivfpq_sync": [_P, _P],
+        "fdb_ivfpq_probe": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, _P, _P],
+        "fdb_ivfpq_encode": [_P, _P, C.c_uint64, C.c_uint32, _P],
+    }
+    for name, args in sig.items():
+        f = getattr(lib, name)
+        f.argtypes = args
+        f.restype = st
+    lib.fdb_ivfpq_destroy.argtypes = [_P]
+    lib.fdb_ivfpq_destroy.restype = None
+    lib.fdb_ivfpq_set_nprobe.argtypes = [_P, C.c_uint64]
+    lib.fdb_ivfpq_set_nprobe.restype = None
+    lib.fdb_ivfpq_nprobe.argtypes = [_P]
+    lib.fdb_ivfpq_nprobe.restype = C.c_uint64
+    _lib_handle = lib
+    return lib
+
+
+def _check(lib, status: int) -> None:
+    if status != 0:
+        raise ForgeDbError(status, lib.fdb_last_error().decode(errors="replace"))
+
+
+def _ptr(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _rows(results_ids: np.ndarray, results_d: np.ndarray, counts: np.ndarray):
+    return [[(int(results_ids[q, j]), float(results_d[q, j])) for j in range(int(counts[q]))]
+            for q in range(results_ids.shape[0])]
+
+
+class IVFPQIndex:
+    """IVF-PQ index resident in HBM — src/index/ivf_pq.rs:343-359.
+
+    Lists are stored in list order as CSR: ``list_offsets[nlist+1]`` into
+    ``ids[N]`` (u64) and ``codes[N, M]`` (u8); ``centroids[nlist, dim]`` and
+    ``codebooks[M, 256, dim // M]`` are f32.
+    """
+
+    def __init__(self, handle: int):
+        self._lib = load_library()
+        self._h = C.c_void_p(handle)
+        d = _Desc()
+        _check(self._lib, self._lib.fdb_ivfpq_describe(self._h, C.byref(d)))
+        self.nlist, self._dim = int(d.nlist), int(d.dim)
+        self.n_subvectors, self.subvector_dim = int(d.n_subvectors), int(d.subvector_dim)
+        self.metric = DistanceMetric(int(d.metric))
+
+    # -- construction -------------------------------------------------------
+    @classmethod
+    def from_artifacts(cls, centroids, codebooks, list_offsets, ids, codes,
+                       metric: DistanceMetric = DistanceMetric.Euclidean) -> "IVFPQIndex":
+        lib = load_library()
+        cen = _f32(centroids)
+        cb = _f32(codebooks)
+        off = np.ascontiguousarray(list_offsets, dtype=np.uint64)
+        idv = np.ascontiguousarray(ids, dtype=np.uint64)
+        cod = np.ascontiguousarray(codes, dtype=np.uint8)
+        nlist, dim = cen.shape
+        M = cb.shape[0]
+        out = C.c_void_p()
+        _check(lib, lib.fdb_ivfpq_create(_ptr(cen), nlist, dim, _ptr(cb), M, _ptr(off),
+                                         _ptr(idv), _ptr(cod), int(metric), C.byref(out)))
+        return cls(out.value)
+
+    @classmethod
+    def build(cls, vectors, n_clusters: int, n_subvectors: int,
+              metric: DistanceMetric = DistanceMetric.Euclidean, seed: int = 0,
+              ids=None) -> "IVFPQIndex":
+        """IVFPQIndex::build (ivf_pq.rs:374-506), on the GPU, seeded."""
+        lib = load_library()
+        v = _f32(vectors)
+        idv = None if ids is None else np.ascontiguousarray(ids, dtype=np.uint64)
+        out = C.c_void_p()
+        _check(lib, lib.fdb_ivfpq_build(_ptr(v), _ptr(idv), v.shape[0], v.shape[1], n_clusters,
+                                        n_subvectors, int(metric), seed, C.byref(out)))
+        return cls(out.value)
+
+    @classmethod
+    def load(cls, path: str) -> "IVFPQIndex":
+        """Persistable::load (ivf_pq.rs:1977-1982)."""
+        lib = load_library()
+        out = C.c_void_p()
+        _check(lib, lib.fdb_ivfpq_load(os.fsencode(path), C.byref(out)))
+        return cls(out.value)
+
+    load_mmap = load  # ivf_pq.rs:1984-1993 deserialises into owned memory too
+
+    def save(self, path: str) -> None:
+        _check(self._lib, self._lib.fdb_ivfpq_save(self._h, os.fsencode(path)))
+
+    def close(self) -> None:
+        if self._h is not None and self._h.value:
+            self._lib.fdb_ivfpq_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- configuration --------------------------------------------------------
+    def set_nprobe(self, nprobe: int) -> None:
+        self._lib.fdb_ivfpq_set_nprobe(self._h, int(nprobe))
+
+    def nprobe(self) -> int:
+        return int(self._lib.fdb_ivfpq_nprobe(self._h))
+
+    def dim(self) -> int:
+        return self._dim
+
+    def n_partitions(self) -> int:
+        return self.nlist
+
+    def describe(self) -> dict:
+        d = _Desc()
+        _check(self._lib, self._lib.fdb_ivfpq_describe(self._h, C.byref(d)))
+        return {f: getattr(d, f) for f, _ in _Desc._fields_}
+
+    def __len__(self) -> int:
+        return int(self.describe()["n_vectors"])
+
+    def enable_reranking(self, vectors_list_order, rerank_factor: int) -> None:
+        """enable_reranking (ivf_pq.rs:513-517); vectors given in list order."""
+        v = _f32(vectors_list_order)
+        _check(self._lib, self._lib.fdb_ivfpq_enable_reranking(self._h, _ptr(v), rerank_factor))
+
+    def export(self) -> dict:
+        d = self.describe()
+        n, M, dim = d["n_vectors"], d["n_subvectors"], d["dim"]
+        out = dict(centroids=np.empty((self.nlist, dim), np.float32),
+                   codebooks=np.empty((M, 256, d["subvector_dim"]), np.float32),
+                   list_offsets=np.empty(self.nlist + 1, np.uint64),
+                   ids=np.empty(n, np.uint64), codes=np.empty((n, M), np.uint8))
+        _check(self._lib, self._lib.fdb_ivfpq_export(
+            self._h, _ptr(out["centroids"]), _ptr(out["codebooks"]), _ptr(out["list_offsets"]),
+            _ptr(out["ids"]), _ptr(out["codes"])))
+        return out
+
+    def list_offsets(self) -> np.ndarray:
+        off = np.empty(self.nlist + 1, np.uint64)
+        _check(self._lib, self._lib.fdb_ivfpq_export(self._h, None, None, _ptr(off), None, None))
+        return off
+
+    # -- search -------------------------------------------------------------
+    def search(self, query, k: int) -> List[Tuple[int, float]]:
+        """search (ivf_pq.rs:590-677) -> [(id, squared ADC distance)] ascending."""
+        q = _f32(query).reshape(-1)
+        ids = np.empty(max(k, 1), np.uint64)
+        d = np.empty(max(k, 1), np.float32)
+        cnt = C.c_uint32()
+        _check(self._lib, self._lib.fdb_ivfpq_search(self._h, _ptr(q), q.shape[0], k, _ptr(ids),
+                                                     _ptr(d), C.byref(cnt)))
+        return [(int(ids[j]), float(d[j])) for j in range(cnt.value)]
+
+    def batch_search_arrays(self, queries, k: int):
+        """batch_search as arrays: (ids [nq,k] u64, dists [nq,k] f32, counts [nq])."""
+        q = _f32(queries)
+        if q.ndim != 2:
+            raise ForgeDbError(-1, "queries must be [nq, dim]")
+        nq = q.shape[0]
+        ids = np.empty((nq, max(k, 1)), np.uint64)
+        d = np.empty((nq, max(k, 1)), np.float32)
+        counts = np.empty(nq, np.uint32)
+        _check(self._lib, self._lib.fdb_ivfpq_batch_search(self._h, _ptr(q), nq, q.shape[1], k,
+                                                           _ptr(ids), _ptr(d), _ptr(counts)))
+        return ids[:, :k], d[:, :k], counts
+
+    def batch_search(self, queries: Sequence, k: int) -> List[List[Tuple[int, float]]]:
+        """batch_search (ivf_pq.rs:850-1047) -> per query [(id, dist)] ascending."""
+        if len(queries) == 0:
+            return []
+        ids, d, counts = self.batch_search_arrays(np.asarray(queries, np.float32), k)
+        return _rows(ids, d, counts)
+
+    # on the GPU the chunked Rayon variant (ivf_pq.rs:1060-1084) is the same launch
+    batch_search_parallel = batch_search
+
+    def batch_search_device(self, d_queries: int, nq: int, k: int, d_ids: int, d_dists: int,
+                            d_counts: int, stream: int = 0, timed: bool = False):
+        """Device pointers in and out; enqueues on `stream`.  With timed=True
+        waits and returns (coarse_ms, scan_ms) from HIP events on that stream."""
+        if timed:
+            cm, sm = C.c_float(), C.c_float()
+            _check(self._lib, self._lib.fdb_ivfpq_batch_search_device_timed(
+                self._h, C.c_void_p(d_queries), nq, k, C.c_void_p(d_ids), C.c_void_p(d_dists),
+                C.c_void_p(d_counts), C.c_void_p(stream), C.byref(cm), C.byref(sm)))
+            return cm.value, sm.value
+        _check(self._lib, self._lib.fdb_ivfpq_batch_search_device(
+            self._h, C.c_void_p(d_queries), nq, k, C.c_void_p(d_ids), C.c_void_p(d_dists),
+            C.c_void_p(d_counts), C.c_void_p(stream)))
+        return None
+
+    def sync(self, stream: int = 0) -> None:
+        _check(self._lib, self._lib.fdb_ivfpq_sync(self._h, C.c_void_p(stream)))
+
+    def probe(self, queries, nprobe: int):
+        """Coarse quantizer: (lists [nq,nprobe] i32, dists [nq,nprobe] f32)."""
+        q = _f32(queries)
+        nq = q.shape[0]
+        lists = np.empty((nq, nprobe), np.int32)
+        d = np.empty((nq, nprobe), np.float32)
+        _check(self._lib, self._lib.fdb_ivfpq_probe(self._h, _ptr(q), nq, q.shape[1], nprobe,
+                                                    _ptr(lists), _ptr(d)))
+        return lists, d
+
+    def encode(self, residuals) -> np.ndarray:
+        """ProductQuantizer::encode (pq.rs:114-139) of residual rows."""
+        r = _f32(residuals)
+        nq = r.shape[0]
+        codes = np.empty((nq, self.n_subvectors), np.uint8)
+        _check(self._lib, self._lib.fdb_ivfpq_encode(self._h, _ptr(r), nq, r.shape[1], _ptr(codes)))
+        return codes

@@ -1,0 +1,174 @@
+/*
+ * forgedb_hip.h — C ABI of the MI355X (gfx950) query path for forge-db.
+ *
+ * Each entry point replaces one method of the reference's Rust API; the
+ * reference file:line it stands in for is given beside it.  A Rust shim crate
+ * binds these with `extern "C"` and keeps the reference's signatures
+ * (infallible search methods panic with fdb_last_error() on a nonzero status).
+ *
+ * Conventions
+ *   - Plain pointers and sizes only.  "host" buffers are ordinary CPU memory;
+ *     "_device" entry points take device pointers and a hipStream_t (as void*,
+ *     NULL = the handle's own stream) and only enqueue work.
+ *   - Vectors and queries are row-major f32 [n][dim].
+ *   - Result rows are [nq][k]: ids ascending by distance, then padding
+ *     (id = UINT64_MAX, distance = +inf) after out_counts[q] valid entries.
+ *   - Status: 0 = FDB_OK, negative = error; fdb_last_error() describes the
+ *     last error on the calling thread.
+ *   - Threading: a handle may be searched from several threads at once (calls
+ *     on one handle serialise on its stream); set_nprobe may race with
+ *     searches (relaxed atomic, as the reference's AtomicUsize).  Creating,
+ *     loading and destroying need exclusive access.
+ */
+#ifndef FORGEDB_HIP_H
+#define FORGEDB_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FDB_API __attribute__((visibility("default")))
+
+typedef int32_t fdb_status;
+enum {
+  FDB_OK = 0,
+  FDB_ERR_INVALID_ARGUMENT = -1,   /* ForgeDbError::InvalidParameter */
+  FDB_ERR_DIMENSION_MISMATCH = -2, /* ForgeDbError::DimensionMismatch; the
+                                      reference panics (pq.rs:150, simd.rs:339) */
+  FDB_ERR_NAN = -3,                /* a NaN centroid distance; the reference
+                                      panics in select_nth_unstable_by
+                                      (ivf_pq.rs:547) */
+  FDB_ERR_OUT_OF_MEMORY = -4,
+  FDB_ERR_HIP = -5,                /* any other HIP runtime failure */
+  FDB_ERR_IO = -6,                 /* ForgeDbError::Io */
+  FDB_ERR_INVALID_FORMAT = -7,     /* ForgeDbError::InvalidFormat */
+  FDB_ERR_CHECKSUM_MISMATCH = -8,  /* ForgeDbError::ChecksumMismatch */
+  FDB_ERR_UNSUPPORTED = -9,        /* a size this build does not handle */
+  FDB_ERR_NO_DEVICE = -10
+};
+
+/* DistanceMetric, src/distance/mod.rs:17-32 (same ordinals as the
+ * brute-force payload metric byte, src/index/brute_force.rs:282-288). */
+enum {
+  FDB_METRIC_EUCLIDEAN = 0,
+  FDB_METRIC_EUCLIDEAN_SQUARED = 1,
+  FDB_METRIC_COSINE = 2,
+  FDB_METRIC_DOT_PRODUCT = 3,
+  FDB_METRIC_MANHATTAN = 4
+};
+
+FDB_API const char* fdb_last_error(void);
+FDB_API const char* fdb_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* IVF-PQ: src/index/ivf_pq.rs                                              */
+/* ------------------------------------------------------------------------ */
+typedef struct fdb_ivfpq fdb_ivfpq;
+
+typedef struct {
+  uint32_t nlist;        /* n_partitions(), ivf_pq.rs:1110 */
+  uint32_t dim;          /* dim(), ivf_pq.rs:1121 */
+  uint32_t n_subvectors; /* ProductQuantizer::n_subvectors, pq.rs:37 */
+  uint32_t subvector_dim;
+  uint64_t n_vectors;    /* len_with_tombstones(), ivf_pq.rs:1096 */
+  uint32_t metric;
+  uint32_t reranking;    /* 1 when original vectors are resident */
+  uint64_t rerank_factor;
+} fdb_ivfpq_desc;
+
+/* Build from trained artifacts (the state IVFPQIndex::build leaves behind,
+ * ivf_pq.rs:494-505).  centroids [nlist][dim]; codebooks [M][256][dim/M];
+ * list_offsets [nlist+1] into ids [N] and codes [N][M], both in list order.
+ * nprobe starts at 1 (ivf_pq.rs:501). */
+FDB_API fdb_status fdb_ivfpq_create(const float* centroids, uint32_t nlist, uint32_t dim,
+                                    const float* codebooks, uint32_t n_subvectors,
+                                    const uint64_t* list_offsets, const uint64_t* ids,
+                                    const uint8_t* codes, uint32_t metric, fdb_ivfpq** out);
+
+/* IVFPQIndex::build, ivf_pq.rs:374-506, run on the GPU: k-means coarse
+ * training on a 30k sample, list assignment, PQ training on a 100k residual
+ * sample, residual encoding.  The reference draws its samples from an
+ * unseeded thread_rng; here they come from the SplitMix64 streams
+ * splitmix64(seed, 0|1|2|16+m).  ids may be NULL (ids 0..n-1). */
+FDB_API fdb_status fdb_ivfpq_build(const float* vectors, const uint64_t* ids, uint64_t n,
+                                   uint32_t dim, uint32_t n_clusters, uint32_t n_subvectors,
+                                   uint32_t metric, uint64_t seed, fdb_ivfpq** out);
+
+/* Persistable::load / load_mmap / save for IVF-PQ, ivf_pq.rs:1970-1994:
+ * 24-byte header + CRC-32 (persistence/mod.rs:77-94,169-188) around the
+ * bincode payload of SerializableIVFPQ (ivf_pq.rs:307-316). */
+FDB_API fdb_status fdb_ivfpq_load(const char* path, fdb_ivfpq** out);
+FDB_API fdb_status fdb_ivfpq_save(const fdb_ivfpq* index, const char* path);
+
+FDB_API void fdb_ivfpq_destroy(fdb_ivfpq* index);
+
+/* set_nprobe (ivf_pq.rs:524-527): stores min(nprobe, nlist), relaxed. */
+FDB_API void fdb_ivfpq_set_nprobe(fdb_ivfpq* index, uint64_t nprobe);
+/* nprobe() (ivf_pq.rs:1116-1118) */
+FDB_API uint64_t fdb_ivfpq_nprobe(const fdb_ivfpq* index);
+
+FDB_API fdb_status fdb_ivfpq_describe(const fdb_ivfpq* index, fdb_ivfpq_desc* out);
+
+/* Copies the resident artifacts back (any pointer may be NULL). */
+FDB_API fdb_status fdb_ivfpq_export(const fdb_ivfpq* index, float* centroids, float* codebooks,
+                                    uint64_t* list_offsets, uint64_t* ids, uint8_t* codes);
+
+/* enable_reranking (ivf_pq.rs:513-517): original vectors [N][dim] in list
+ * order (the same positions as ids/codes); searches then fetch
+ * k * rerank_factor ADC candidates and return exact sqrt(L2) re-ranked
+ * results (rerank_results, ivf_pq.rs:556-582). */
+FDB_API fdb_status fdb_ivfpq_enable_reranking(fdb_ivfpq* index, const float* vectors_list_order,
+                                              uint64_t rerank_factor);
+
+/* search (ivf_pq.rs:590-677): one query, its nprobe lists (0 lists when
+ * nprobe is 0), ADC summed as asymmetric_distance_fast (pq.rs:218-245).
+ * out_ids/out_dists hold k entries. */
+FDB_API fdb_status fdb_ivfpq_search(fdb_ivfpq* index, const float* query, uint32_t dim,
+                                    uint32_t k, uint64_t* out_ids, float* out_dists,
+                                    uint32_t* out_count);
+
+/* batch_search (ivf_pq.rs:850-1047) and batch_search_parallel (:1060-1084):
+ * nq queries, max(nprobe,1) lists each, ADC summed in the 8-lane AVX2 order
+ * (pq.rs:318-485).  Results [nq][k] in input order. */
+FDB_API fdb_status fdb_ivfpq_batch_search(fdb_ivfpq* index, const float* queries, uint64_t nq,
+                                          uint32_t dim, uint32_t k, uint64_t* out_ids,
+                                          float* out_dists, uint32_t* out_counts);
+
+/* The same with inputs and outputs already in device memory; enqueues only.
+ * A NaN query is reported by the next fdb_ivfpq_sync. */
+FDB_API fdb_status fdb_ivfpq_batch_search_device(fdb_ivfpq* index, const float* d_queries,
+                                                 uint64_t nq, uint32_t k, uint64_t* d_out_ids,
+                                                 float* d_out_dists, uint32_t* d_out_counts,
+                                                 void* hip_stream);
+/* Waits for the handle's work on `hip_stream` (NULL = own stream) and
+ * returns FDB_ERR_NAN if a device search since the last sync saw a NaN. */
+FDB_API fdb_status fdb_ivfpq_sync(fdb_ivfpq* index, void* hip_stream);
+
+/* Coarse quantizer alone (find_nearest_partitions, ivf_pq.rs:538-553): the
+ * nprobe nearest lists per query, ascending by (distance, list id), with the
+ * exact reference-order squared distances. */
+FDB_API fdb_status fdb_ivfpq_probe(fdb_ivfpq* index, const float* queries, uint64_t nq,
+                                   uint32_t dim, uint32_t nprobe, int32_t* out_lists,
+                                   float* out_dists);
+
+/* ProductQuantizer::encode (pq.rs:114-139) of nq residual vectors [nq][dim]
+ * against the index's codebooks: codes [nq][M]. */
+FDB_API fdb_status fdb_ivfpq_encode(fdb_ivfpq* index, const float* residuals, uint64_t nq,
+                                    uint32_t dim, uint8_t* out_codes);
+
+/* Kernel timing for measurement: runs one batch_search_device and returns the
+ * durations in ms of the coarse and scan kernels (HIP events on the stream
+ * they run on). */
+FDB_API fdb_status fdb_ivfpq_batch_search_device_timed(fdb_ivfpq* index, const float* d_queries,
+                                                       uint64_t nq, uint32_t k,
+                                                       uint64_t* d_out_ids, float* d_out_dists,
+                                                       uint32_t* d_out_counts, void* hip_stream,
+                                                       float* coarse_ms, float* scan_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,209 @@
+"""IVF-PQ parity: the HIP path (through the C ABI) against the oracle on the
+same artifacts and queries.
+
+Bar: probed lists and PQ codes bit-exact; distances bit-exact (the kernels
+reproduce the reference's summation orders, which is stricter than the
+1e-4 relative tolerance allowed); ids identical except among exactly equal
+distances (rel = 0 in tie_aware_match).
+"""
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+import refcpu
+from conftest import tie_aware_match
+from forgedb import DistanceMetric, ForgeDbError, IVFPQIndex, datagen
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_index(art, metric=DistanceMetric.Euclidean):
+    return IVFPQIndex.from_artifacts(art["centroids"], art["codebooks"], art["list_offsets"],
+                                     art["ids"], art["codes"], metric)
+
+
+def check_batch(gx, ox, queries, k, label):
+    gi, gd, gc = gx.batch_search_arrays(queries, k)
+    oi, od, oc = ox.batch_search(queries, k)
+    assert np.array_equal(gc, oc.astype(np.uint32)), f"{label}: counts differ"
+    for q in range(len(queries)):
+        c = int(oc[q])
+        assert np.array_equal(gd[q, :c], od[q, :c]), f"{label} q{q}: distances {gd[q,:c]} vs {od[q,:c]}"
+        ok, msg = tie_aware_match(gi[q, :c], gd[q, :c], oi[q, :c], od[q, :c], rel=0)
+        assert ok, f"{label} q{q}: {msg}"
+        assert np.all(gi[q, c:] == np.iinfo(np.uint64).max)
+        assert np.all(np.isinf(gd[q, c:]))
+
+
+def test_probe_parity_bit_exact(small_ivfpq):
+    print("probe parity: 64 queries, nlist 64, nprobe 1/16/64", flush=True)
+    gx = gpu_index(small_ivfpq["art"])
+    ox = small_ivfpq["oracle"]
+    for nprobe in (1, 16, 64):
+        lists, d = gx.probe(small_ivfpq["queries"], nprobe)
+        for q, qv in enumerate(small_ivfpq["queries"]):
+            ol, odist = ox.probes(qv, nprobe)
+            assert np.array_equal(d[q], odist), (nprobe, q)
+            assert np.array_equal(lists[q], ol), (nprobe, q)
+
+
+@pytest.mark.parametrize("nprobe,k", [(1, 10), (8, 10), (16, 1), (16, 64), (16, 65), (16, 100),
+                                      (64, 10), (5, 256), (3, 1000)])
+def test_batch_search_parity(small_ivfpq, nprobe, k):
+    print(f"batch parity nprobe={nprobe} k={k}", flush=True)
+    gx = gpu_index(small_ivfpq["art"])
+    ox = small_ivfpq["oracle"]
+    gx.set_nprobe(nprobe)
+    ox.set_nprobe(nprobe)
+    assert gx.nprobe() == ox.nprobe()
+    check_batch(gx, ox, small_ivfpq["queries"], k, f"np{nprobe} k{k}")
+
+
+def test_single_search_parity(small_ivfpq):
+    print("single search parity (groups-of-4 ADC order)", flush=True)
+    gx = gpu_index(small_ivfpq["art"])
+    ox = small_ivfpq["oracle"]
+    for nprobe in (0, 1, 16):
+        gx.set_nprobe(nprobe)
+        ox.set_nprobe(nprobe)
+        for qv in small_ivfpq["queries"][:16]:
+            g = gx.search(qv, 10)
+            oi, od = ox.search(qv, 10)
+            assert len(g) == len(oi)
+            gi = np.array([x[0] for x in g], np.uint64)
+            gd = np.array([x[1] for x in g], np.float32)
+            assert np.array_equal(gd, od)
+            ok, msg = tie_aware_match(gi, gd, oi, od, rel=0)
+            assert ok, msg
+
+
+@pytest.mark.parametrize("dim,M,nlist", [(96, 32, 32), (128, 8, 16), (16, 4, 8), (48, 12, 12),
+                                         (20, 5, 6), (64, 64, 8)])
+def test_shapes_parity(dim, M, nlist):
+    print(f"shape parity dim={dim} M={M} nlist={nlist}", flush=True)
+    base = datagen.gaussian_mixture(dim + M, 99, 4000, dim, ncomp=32, centre_std=2.0)
+    ox = refcpu.IvfPq.build(base, nlist=nlist, M=M, seed=1)
+    gx = gpu_index(ox.export())
+    q = datagen.gaussian_mixture(dim + M + 1, 99, 24, dim, ncomp=32, centre_std=2.0)
+    for nprobe, k in ((1, 5), (3, 10), (nlist, 50)):
+        gx.set_nprobe(nprobe)
+        ox.set_nprobe(nprobe)
+        check_batch(gx, ox, q, k, f"d{dim} M{M} np{nprobe}")
+
+
+def test_edges(small_ivfpq):
+    print("edge cases: nprobe 0, k 0, k > candidates, empty lists", flush=True)
+    art = dict(small_ivfpq["art"])
+    gx = gpu_index(art)
+    q = small_ivfpq["queries"][:4]
+    gx.set_nprobe(0)
+    assert gx.nprobe() == 0
+    assert gx.search(q[0], 10) == []           # search probes no list
+    ids, d, c = gx.batch_search_arrays(q, 10)  # batch_search probes one
+    assert np.all(c == 10)
+    gx.set_nprobe(10_000)
+    assert gx.nprobe() == 64                   # clamped to nlist
+    ids, d, c = gx.batch_search_arrays(q, 0)
+    assert ids.shape == (4, 0) and np.all(c == 0)
+    assert gx.batch_search([], 5) == []
+    # an index where most lists are empty and k exceeds the candidates
+    off = np.zeros(65, np.uint64)
+    off[5:] = 7
+    off[40:] = 12
+    small = dict(centroids=art["centroids"], codebooks=art["codebooks"], list_offsets=off,
+                 ids=art["ids"][:12], codes=art["codes"][:12])
+    gx2 = gpu_index(small)
+    ox2 = refcpu.IvfPq.create(small["centroids"], small["codebooks"], off, small["ids"], small["codes"])
+    for nprobe in (1, 30, 64):
+        gx2.set_nprobe(nprobe)
+        ox2.set_nprobe(nprobe)
+        check_batch(gx2, ox2, small_ivfpq["queries"], 20, f"sparse np{nprobe}")
+
+
+def test_errors(small_ivfpq):
+    print("error statuses", flush=True)
+    gx = gpu_index(small_ivfpq["art"])
+    q = small_ivfpq["queries"][:3].copy()
+    with pytest.raises(ForgeDbError) as e:
+        gx.batch_search_arrays(q[:, :100], 5)
+    assert e.value.kind == "DimensionMismatch"
+    q[1, 7] = np.nan
+    gx.set_nprobe(4)
+    with pytest.raises(ForgeDbError) as e:
+        gx.batch_search_arrays(q, 5)
+    assert e.value.kind == "NaN"
+    # the handle stays usable
+    gx.batch_search_arrays(small_ivfpq["queries"][:3], 5)
+    with pytest.raises(ForgeDbError) as e:
+        IVFPQIndex.from_artifacts(np.zeros((4, 10), np.float32), np.zeros((3, 256, 3), np.float32),
+                                  np.zeros(5, np.uint64), np.zeros(0, np.uint64),
+                                  np.zeros((0, 3), np.uint8))
+    assert e.value.kind == "InvalidArgument"
+
+
+def test_encode_parity(small_ivfpq):
+    print("encode parity", flush=True)
+    gx = gpu_index(small_ivfpq["art"])
+    art = small_ivfpq["art"]
+    rng = np.random.default_rng(0)
+    resid = (small_ivfpq["base"][:512] - art["centroids"][rng.integers(0, 64, 512)]).astype(np.float32)
+    codes = gx.encode(resid)
+    for i in range(0, 512, 7):
+        assert np.array_equal(codes[i], refcpu.pq_encode(art["codebooks"], resid[i]))
+
+
+@pytest.mark.parametrize("n,dim,nlist,M", [(3000, 16, 8, 4), (5000, 32, 100, 8), (2000, 96, 70, 32)])
+def test_build_parity(n, dim, nlist, M):
+    """GPU build (k-means, assignment, PQ training, encode) equals the oracle's
+    seeded restatement of IVFPQIndex::build bit for bit."""
+    print(f"build parity n={n} dim={dim} nlist={nlist} M={M}", flush=True)
+    x = datagen.gaussian_mixture(n + dim, 5, n, dim, ncomp=40, centre_std=2.0)
+    ox = refcpu.IvfPq.build(x, nlist=nlist, M=M, seed=11)
+    gx = IVFPQIndex.build(x, nlist, M, seed=11)
+    o, g = ox.export(), gx.export()
+    for key in ("centroids", "codebooks", "list_offsets", "ids", "codes"):
+        assert np.array_equal(o[key], g[key]), key
+
+
+def test_rerank_parity(small_ivfpq):
+    print("rerank parity", flush=True)
+    art = small_ivfpq["art"]
+    base = small_ivfpq["base"]
+    orig = base[art["ids"].astype(np.int64)]
+    gx = gpu_index(art)
+    ox = refcpu.IvfPq.create(art["centroids"], art["codebooks"], art["list_offsets"], art["ids"],
+                             art["codes"])
+    gx.enable_reranking(orig, 4)
+    ox.enable_reranking(orig, 4)
+    assert gx.describe()["reranking"] == 1
+    for nprobe in (4, 16):
+        gx.set_nprobe(nprobe)
+        ox.set_nprobe(nprobe)
+        check_batch(gx, ox, small_ivfpq["queries"], 10, f"rerank np{nprobe}")
+
+
+def test_save_load_roundtrip(small_ivfpq):
+    print("save/load roundtrip", flush=True)
+    gx = gpu_index(small_ivfpq["art"])
+    gx.set_nprobe(9)
+    with tempfile.TemporaryDirectory() as d:
+        p = os.path.join(d, "ix.fdb")
+        gx.save(p)
+        lx = IVFPQIndex.load(p)
+        assert lx.nprobe() == 9
+        a, b = gx.export(), lx.export()
+        for key in a:
+            assert np.array_equal(a[key], b[key]), key
+        q = small_ivfpq["queries"]
+        ga = gx.batch_search_arrays(q, 10)
+        gb = lx.batch_search_arrays(q, 10)
+        for x, y in zip(ga, gb):
+            assert np.array_equal(x, y)
+        raw = bytearray(open(p, "rb").read())
+        raw[100] ^= 0xFF
+        open(p, "wb").write(bytes(raw))
+        with pytest.raises(ForgeDbError) as e:
+            IVFPQIndex.load(p)
+        assert e.value.kind == "ChecksumMismatch"
