@@ -176,16 +176,25 @@ __device__ __forceinline__ float adc_sum_rt(const float* __restrict__ lut, const
 }
 
 // ---------------------------------------------------------------------------
-// Wave64 top-k.  One sorted list of 64*R (distance, position) pairs spread
-// over the wave: slot s = r*64 + lane lives in register r of that lane.  The
-// list keeps the k smallest values offered so far; a new value goes after
-// existing equal ones, so among exact ties the earliest offered wins.
+// Wave64 top-k.  One sorted list of 64*R (distance, key) pairs spread over
+// the wave: slot s = r*64 + lane lives in register r of that lane.  Pairs are
+// ordered by distance, then by key (a list position, centroid index or
+// candidate rank), so the k smallest are the same set whatever order they are
+// offered in; exact distance ties resolve to the smaller key.  The reference
+// leaves that order to BinaryHeap / select_nth_unstable, so this is one of
+// the orders it can produce.  An empty slot is (+inf, kNoPos), which no
+// offered pair with key kNoPos can displace.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ bool pair_lt(float d1, uint32_t p1, float d2, uint32_t p2) {
+  return d1 < d2 || (d1 == d2 && p1 < p2);
+}
+
 template <int R>
 struct WaveTopK {
   float d[R];
   uint32_t p[R];
-  float tau;  // value in slot k-1 (wave-uniform); +inf until k values arrived
+  float tau;      // pair in slot k-1 (wave-uniform); (+inf, kNoPos) until k arrived
+  uint32_t tau_p;
   int k;
 
   __device__ __forceinline__ void init(int kk) {
@@ -196,23 +205,30 @@ struct WaveTopK {
     }
     k = kk;
     tau = f_inf();
+    tau_p = kNoPos;
   }
 
-  __device__ __forceinline__ float slot_value(int s) const {
+  __device__ __forceinline__ void read_tau() {
+    const int s = k - 1;
     const int rs = s >> 6;
     float v = d[0];
+    uint32_t w = p[0];
 #pragma unroll
     for (int r = 1; r < R; ++r)
-      if (r == rs) v = d[r];
-    return readlane_f(v, s & 63);
+      if (r == rs) {
+        v = d[r];
+        w = p[r];
+      }
+    tau = readlane_f(v, s & 63);
+    tau_p = readlane_u(w, s & 63);
   }
 
-  // Insert one wave-uniform pair.  Caller guarantees dn < tau.
+  // Insert one wave-uniform pair.  Caller guarantees (dn, pn) < (tau, tau_p).
   __device__ __forceinline__ void insert(float dn, uint32_t pn) {
     const int lane = lane_id();
     int pos = 0;
 #pragma unroll
-    for (int r = 0; r < R; ++r) pos += __popcll(__ballot(d[r] <= dn));
+    for (int r = 0; r < R; ++r) pos += __popcll(__ballot(pair_lt(d[r], p[r], dn, pn)));
 #pragma unroll
     for (int r = R - 1; r >= 0; --r) {
       float up_d = __shfl_up(d[r], 1);
@@ -234,19 +250,19 @@ struct WaveTopK {
         p[r] = pn;
       }
     }
-    tau = slot_value(k - 1);
+    read_tau();
   }
 
-  // Every lane offers one pair (use +inf to offer nothing).  Lanes are taken
-  // in ascending order.
-  __device__ __forceinline__ void offer(float dist, uint32_t pos) {
-    uint64_t mask = __ballot(dist < tau);
+  // Every lane offers one pair; a lane with nothing to offer passes
+  // (+inf, kNoPos).
+  __device__ __forceinline__ void offer(float dist, uint32_t key) {
+    uint64_t mask = __ballot(pair_lt(dist, key, tau, tau_p));
     while (mask) {
       const int l = __ffsll((unsigned long long)mask) - 1;
       mask &= mask - 1;
       const float dn = readlane_f(dist, l);
-      const uint32_t pn = readlane_u(pos, l);
-      if (dn < tau) insert(dn, pn);
+      const uint32_t pn = readlane_u(key, l);
+      if (pair_lt(dn, pn, tau, tau_p)) insert(dn, pn);
     }
   }
 };

@@ -37,8 +37,9 @@ __global__ void nan_check_kernel(const float* __restrict__ q, uint64_t n, int* e
 
 // rerank_results, ivf_pq.rs:556-582: candidates arrive sorted by ADC
 // distance; each gets sqrt of the exact reference-order squared L2 to its
-// original vector, and a stable ascending order of those (offered in ADC
-// order, ties keep it) is truncated to k.  One wave per query.
+// original vector, and a stable ascending sort of those (ties keep the ADC
+// order: the tie key is the candidate's rank) is truncated to k.  One wave
+// per query.
 template <int R>
 __global__ __launch_bounds__(64) void rerank_kernel(const float* __restrict__ queries, int dim,
                                                     const float* __restrict__ originals,
@@ -58,12 +59,13 @@ __global__ __launch_bounds__(64) void rerank_kernel(const float* __restrict__ qu
   for (uint32_t base = 0; base < cnt; base += 64) {
     const uint32_t c = base + lane;
     float d = f_inf();
-    uint32_t pos = kNoPos;
+    uint32_t rank = kNoPos;
     if (c < cnt) {
-      pos = cand_pos[q * fetch_k + c];
+      const uint32_t pos = cand_pos[q * fetch_k + c];
       d = __builtin_sqrtf(l2sq_ref_rt(qv, originals + (uint64_t)pos * dim, dim));
+      rank = c;
     }
-    tk.offer(d, pos);
+    tk.offer(d, rank);
   }
   uint32_t count = 0;
 #pragma unroll
@@ -72,7 +74,7 @@ __global__ __launch_bounds__(64) void rerank_kernel(const float* __restrict__ qu
     const bool valid = s < k && tk.p[r] != kNoPos;
     count += (uint32_t)__popcll(__ballot(valid));
     if (s < k) {
-      out_ids[q * k + s] = valid ? ids[tk.p[r]] : ~0ull;
+      out_ids[q * k + s] = valid ? ids[cand_pos[q * fetch_k + tk.p[r]]] : ~0ull;
       out_dists[q * k + s] = valid ? tk.d[r] : f_inf();
     }
   }

@@ -103,11 +103,13 @@ __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
       for (int cc = 0; cc < kCoarseChunk && c0 + cc < nlist; cc += 64) {
         const int c = c0 + cc + lane;
         float dv = f_inf();
+        uint32_t key = kNoPos;
         if (c < nlist) {
           dv = dist[qq * kCoarseChunk + cc + lane];
+          key = (uint32_t)c;
           if (dv != dv) saw_nan = true;
         }
-        tk[j].offer(dv, (uint32_t)c);
+        tk[j].offer(dv, key);
       }
     }
     __syncthreads();
@@ -236,7 +238,9 @@ __global__ __launch_bounds__(kThreads) void ivfpq_scan_kernel(IvfPqScanArgs a, i
       for (uint32_t base = s; base < e; base += kThreads) {
         const uint32_t i = base + tid;
         float dist = f_inf();
+        uint32_t key = kNoPos;
         if (i < e) {
+          key = i;
           if constexpr (MT > 0) {
             uint32_t w[(MT + 3) / 4];
             load_code<MT>(a.codes, i, w);
@@ -245,7 +249,7 @@ __global__ __launch_bounds__(kThreads) void ivfpq_scan_kernel(IvfPqScanArgs a, i
             dist = adc_sum_rt<ORDER>(L, a.codes + (uint64_t)i * M, M);
           }
         }
-        tk.offer(dist, i);
+        tk.offer(dist, key);
       }
     }
     __syncthreads();

@@ -415,13 +415,21 @@ int kmeans_fit(const float* data, uint64_t n, int dim, int k, int max_iters, uin
   return 0;
 }
 
-// Max-heap on distance with the reference's insertion rules.
+// Max-heap with the reference's insertion rules.  BinaryHeap leaves the order
+// among equal distances unspecified; here items compare by (distance, key)
+// where key is the row position, so exact ties resolve to the earlier row —
+// one of the outcomes the reference can produce, and the one the HIP kernels
+// produce.
 struct HeapItem {
   uint64_t id;
   float d;
+  uint64_t key;
 };
+inline bool item_lt(float d1, uint64_t k1, float d2, uint64_t k2) {
+  return d1 < d2 || (d1 == d2 && k1 < k2);
+}
 struct HeapLess {
-  bool operator()(const HeapItem& a, const HeapItem& b) const { return a.d < b.d; }
+  bool operator()(const HeapItem& a, const HeapItem& b) const { return item_lt(a.d, a.key, b.d, b.key); }
 };
 using MaxHeap = std::priority_queue<HeapItem, std::vector<HeapItem>, HeapLess>;
 
@@ -699,10 +707,22 @@ struct PosItem {
   uint64_t pos;
   float d;
 };
+// ordered by (distance, list position); see HeapItem
 struct PosLess {
-  bool operator()(const PosItem& a, const PosItem& b) const { return a.d < b.d; }
+  bool operator()(const PosItem& a, const PosItem& b) const { return item_lt(a.d, a.pos, b.d, b.pos); }
 };
 using PosHeap = std::priority_queue<PosItem, std::vector<PosItem>, PosLess>;
+
+// the reference's "dist < threshold || len < fetch_k" with the pair order;
+// threshold is (f32::MAX, max) while the heap is not full
+struct Threshold {
+  float d;
+  uint64_t pos;
+};
+inline Threshold threshold_of(const PosHeap& heap, uint64_t fetch_k) {
+  if (heap.size() >= fetch_k && !heap.empty()) return {heap.top().d, heap.top().pos};
+  return {3.40282347e38f, ~0ull};
+}
 
 // heap contents, stable-sorted ascending, then rerank or truncate
 int finish(const fdbo_ivfpq* h, const float* q, PosHeap& heap, int k, uint64_t* out_ids,
@@ -752,11 +772,10 @@ int fdbo_ivfpq_search(const fdbo_ivfpq* h, const float* q, int k, uint64_t* out_
     for (int j = 0; j < h->dim; ++j) resid[j] = q[j] - c[j];
     pq_lut(h->codebooks.data(), h->M, h->dsub, resid.data(), lut.data());
     // threshold read once per list (:638-642)
-    float threshold = (heap.size() >= fetch_k) ? (heap.empty() ? 3.40282347e38f : heap.top().d)
-                                               : 3.40282347e38f;
+    const Threshold th = threshold_of(heap, fetch_k);
     for (uint64_t j = h->offsets[p]; j < h->offsets[p + 1]; ++j) {
       float dist = adc_groups4(lut.data(), &h->codes[j * h->M], h->M);
-      if (dist < threshold || heap.size() < fetch_k) {
+      if (item_lt(dist, j, th.d, th.pos) || heap.size() < fetch_k) {
         heap.push({j, dist});
         if (heap.size() > fetch_k) heap.pop();
       }
@@ -806,10 +825,9 @@ void fdbo_ivfpq_batch_search(const fdbo_ivfpq* h, const float* queries, uint64_t
       }
       for (size_t t = 0; t < qidx.size(); ++t) {
         PosHeap& heap = heaps[qidx[t]];
-        float threshold = (heap.size() >= fetch_k) ? (heap.empty() ? 3.40282347e38f : heap.top().d)
-                                                   : 3.40282347e38f;
+        const Threshold th = threshold_of(heap, fetch_k);
         float dist = dists[t];
-        if (dist < threshold || heap.size() < fetch_k) {
+        if (item_lt(dist, j, th.d, th.pos) || heap.size() < fetch_k) {
           heap.push({j, dist});
           if (heap.size() > fetch_k) heap.pop();
         }
@@ -843,16 +861,17 @@ void fdbo_ivfpq_batch_search_parallel(const fdbo_ivfpq* h, const float* queries,
 // ---------------------------------------------------------------------------
 namespace {
 // scan_range, :105-148: push while len < k, else replace the max only when
-// strictly smaller.
+// smaller (in (distance, row) order: a later row never displaces an equal
+// earlier one, as with the reference's strict `<` in a sequential scan).
 void bf_scan(const float* data, const uint64_t* ids, int dim, int metric, const float* q,
              uint64_t start, uint64_t end, MaxHeap& heap, int k) {
   for (uint64_t i = start; i < end; ++i) {
     float d = fdbo_metric(metric, q, data + i * (uint64_t)dim, (size_t)dim);
     if ((int)heap.size() < k) {
-      heap.push({ids[i], d});
-    } else if (!heap.empty() && d < heap.top().d) {
+      heap.push({ids[i], d, i});
+    } else if (!heap.empty() && item_lt(d, i, heap.top().d, heap.top().key)) {
       heap.pop();
-      heap.push({ids[i], d});
+      heap.push({ids[i], d, i});
     }
   }
 }
@@ -880,7 +899,7 @@ int fdbo_bf_search_parallel(const float* data, const uint64_t* ids, uint64_t n, 
       local.pop();
       if ((int)acc.size() < k) {
         acc.push(it);
-      } else if (!acc.empty() && it.d < acc.top().d) {
+      } else if (!acc.empty() && item_lt(it.d, it.key, acc.top().d, acc.top().key)) {
         acc.pop();
         acc.push(it);
       }

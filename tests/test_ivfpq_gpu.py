@@ -3,8 +3,9 @@ same artifacts and queries.
 
 Bar: probed lists and PQ codes bit-exact; distances bit-exact (the kernels
 reproduce the reference's summation orders, which is stricter than the
-1e-4 relative tolerance allowed); ids identical except among exactly equal
-distances (rel = 0 in tie_aware_match).
+1e-4 relative tolerance allowed); ids identical, with exact distance ties
+ordered by list position on both sides (the reference leaves that order to
+its BinaryHeap, so this is one of the orders it can return).
 """
 import os
 import tempfile
@@ -13,7 +14,7 @@ import numpy as np
 import pytest
 
 import refcpu
-from conftest import tie_aware_match
+
 from forgedb import DistanceMetric, ForgeDbError, IVFPQIndex, datagen
 
 pytestmark = pytest.mark.gpu
@@ -31,8 +32,8 @@ def check_batch(gx, ox, queries, k, label):
     for q in range(len(queries)):
         c = int(oc[q])
         assert np.array_equal(gd[q, :c], od[q, :c]), f"{label} q{q}: distances {gd[q,:c]} vs {od[q,:c]}"
-        ok, msg = tie_aware_match(gi[q, :c], gd[q, :c], oi[q, :c], od[q, :c], rel=0)
-        assert ok, f"{label} q{q}: {msg}"
+        # both sides order exact distance ties by list position
+        assert np.array_equal(gi[q, :c], oi[q, :c]), f"{label} q{q}: ids {gi[q,:c]} vs {oi[q,:c]}"
         assert np.all(gi[q, c:] == np.iinfo(np.uint64).max)
         assert np.all(np.isinf(gd[q, c:]))
 
@@ -75,8 +76,7 @@ def test_single_search_parity(small_ivfpq):
             gi = np.array([x[0] for x in g], np.uint64)
             gd = np.array([x[1] for x in g], np.float32)
             assert np.array_equal(gd, od)
-            ok, msg = tie_aware_match(gi, gd, oi, od, rel=0)
-            assert ok, msg
+            assert np.array_equal(gi, oi)
 
 
 @pytest.mark.parametrize("dim,M,nlist", [(96, 32, 32), (128, 8, 16), (16, 4, 8), (48, 12, 12),
