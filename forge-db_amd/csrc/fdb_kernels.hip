@@ -187,9 +187,66 @@ __device__ __forceinline__ void load_code(const uint8_t* __restrict__ codes, uin
   }
 }
 
-template <int MT, int DT, int R, int ORDER>
-__global__ __launch_bounds__(kThreads) void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
-  extern __shared__ float smem[];
+// Lists of one LUT group: code range [start, start+len) of each slot.
+template <int GMAX>
+struct GroupLists {
+  uint32_t start[GMAX];
+  uint32_t len[GMAX];
+  int ng;
+};
+
+// Scan of one probed list with a compile-time LUT slot J.  Each wave takes
+// batches of 64 consecutive codes (batch b = lanes b*64 .. b*64+63), waves
+// striding by NW; U batches per wave are loaded before any is summed so U
+// code loads are in flight.  The loads are branch-free: a batch or lane past
+// the end re-reads the list's last code (len > 0) and carries key kNoPos.
+template <int MT, int ORDER, int R, int NW, int U, int J>
+__device__ __forceinline__ void scan_list(const float* __restrict__ lut, uint32_t start, uint32_t len,
+                                          uint32_t w0, int lane, const uint8_t* __restrict__ codes,
+                                          WaveTopK<R>& tk) {
+  const uint32_t nb = (len + 63) / 64;
+  const uint32_t last = start + len - 1;
+  for (uint32_t b0 = w0; b0 < nb; b0 += (uint32_t)(NW * U)) {
+    uint32_t w[U][(MT + 3) / 4];
+    uint32_t key[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t i = start + (b0 + (uint32_t)(u * NW)) * 64 + (uint32_t)lane;
+      const bool valid = i <= last;  // also false for a batch past nb
+      key[u] = valid ? i : kNoPos;
+      load_code<MT>(codes, valid ? i : last, w[u]);
+    }
+    float dist[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float d = adc_sum<MT, ORDER>(lut + J * (MT * 256), w[u]);
+      dist[u] = (key[u] != kNoPos) ? d : f_inf();
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) tk.offer(dist[u], key[u]);
+  }
+}
+
+template <int MT, int ORDER, int R, int NW, int U, int GMAX, int J>
+__device__ __forceinline__ void scan_group(const float* __restrict__ lut, const GroupLists<GMAX>& gl,
+                                           uint32_t w0, int lane, const uint8_t* __restrict__ codes,
+                                           WaveTopK<R>& tk) {
+  if (J < gl.ng && gl.len[J] > 0)
+    scan_list<MT, ORDER, R, NW, U, J>(lut, gl.start[J], gl.len[J], w0, lane, codes, tk);
+  if constexpr (J + 1 < GMAX) scan_group<MT, ORDER, R, NW, U, GMAX, J + 1>(lut, gl, w0, lane, codes, tk);
+}
+
+// One workgroup per query.  MT/DT: compile-time M and dsub (0 = runtime, then
+// the LUTs live in dynamic LDS and each lane locates its list slot);
+// NT threads; U code batches in flight per wave; at most GMAX lists per LUT
+// group (G <= GMAX at run time).
+template <int MT, int DT, int R, int ORDER, int NT, int U, int GMAX>
+__global__ __launch_bounds__(NT) void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
+  constexpr int NW = NT / 64;
+  constexpr int SLDS = (MT > 0) ? GMAX * MT * 256 + GMAX * MT * DT : 1;
+  __shared__ float s_static[SLDS];
+  extern __shared__ float s_dyn[];
+  float* smem = (MT > 0) ? s_static : s_dyn;
   const int M = MT ? MT : a.M;
   const int dsub = DT ? DT : a.dsub;
   const int D = M * dsub;
@@ -198,6 +255,7 @@ __global__ __launch_bounds__(kThreads) void ivfpq_scan_kernel(IvfPqScanArgs a, i
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const uint32_t w0 = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
   const uint64_t q = blockIdx.x;
   const float* __restrict__ qv = a.queries + q * D;
   const int32_t* __restrict__ pr = a.probes + q * (uint64_t)a.np;
@@ -207,57 +265,72 @@ __global__ __launch_bounds__(kThreads) void ivfpq_scan_kernel(IvfPqScanArgs a, i
 
   for (int g0 = 0; g0 < a.np; g0 += G) {
     const int ng = min(G, a.np - g0);
-    for (int e = tid; e < ng * D; e += kThreads) {
+    GroupLists<GMAX> gl;
+    gl.ng = ng;
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j) {
+      gl.start[j] = 0;
+      gl.len[j] = 0;
+      if (j < ng) {
+        const int p = pr[g0 + j];
+        // a probe slot left empty (NaN distances) has p = -1: nothing to scan
+        if (p >= 0 && p < a.nlist) {
+          gl.start[j] = a.list_off[p];
+          gl.len[j] = a.list_off[p + 1] - gl.start[j];
+        }
+      }
+    }
+
+    for (int e = tid; e < ng * D; e += NT) {
       const int j = e / D;
       const int d = e - j * D;
       const int p = pr[g0 + j];
-      // a probe slot left empty (NaN distances) has p = -1: no list to scan
       resid[j * D + d] = (p >= 0 && p < a.nlist) ? qv[d] - a.centroids[(uint64_t)p * D + d] : 0.0f;
     }
     __syncthreads();
-    for (int m = 0; m < M; ++m) {
-      const float* __restrict__ cbp = a.codebooks + ((uint64_t)m * 256 + tid) * dsub;
+    // LUT: thread -> codeword tid & 255 of subspaces tid>>8, +NT/256, ...
+    const int cw = tid & 255;
+    for (int m = tid >> 8; m < M; m += NT / 256) {
+      const float* __restrict__ cbp = a.codebooks + ((uint64_t)m * 256 + cw) * dsub;
       if constexpr (DT > 0) {
         float cbv[DT];
 #pragma unroll
         for (int t = 0; t < DT; ++t) cbv[t] = cbp[t];
-        for (int j = 0; j < ng; ++j)
-          lut[(j * M + m) * 256 + tid] = l2sq_ref<DT>(resid + j * D + m * DT, cbv);
+#pragma unroll
+        for (int j = 0; j < GMAX; ++j)
+          if (j < ng) lut[(j * M + m) * 256 + cw] = l2sq_ref<DT>(resid + j * D + m * DT, cbv);
       } else {
         for (int j = 0; j < ng; ++j)
-          lut[(j * M + m) * 256 + tid] = l2sq_ref_rt(resid + j * D + m * dsub, cbp, dsub);
+          lut[(j * M + m) * 256 + cw] = l2sq_ref_rt(resid + j * D + m * dsub, cbp, dsub);
       }
     }
     __syncthreads();
-    for (int j = 0; j < ng; ++j) {
-      const int p = pr[g0 + j];
-      if (p < 0 || p >= a.nlist) continue;  // uniform across the workgroup
-      const uint32_t s = a.list_off[p];
-      const uint32_t e = a.list_off[p + 1];
-      const float* __restrict__ L = lut + (size_t)j * M * 256;
-      for (uint32_t base = s; base < e; base += kThreads) {
-        const uint32_t i = base + tid;
-        float dist = f_inf();
-        uint32_t key = kNoPos;
-        if (i < e) {
-          key = i;
-          if constexpr (MT > 0) {
-            uint32_t w[(MT + 3) / 4];
-            load_code<MT>(a.codes, i, w);
-            dist = adc_sum<MT, ORDER>(L, w);
-          } else {
+
+    if constexpr (MT > 0) {
+      scan_group<MT, ORDER, R, NW, U, GMAX, 0>(lut, gl, w0, lane, a.codes, tk);
+    } else {
+      // generic shape: lists one after another, one code per lane
+      for (int j = 0; j < ng; ++j) {
+        const uint32_t s = gl.start[j], e = s + gl.len[j];
+        const float* __restrict__ L = lut + (size_t)j * M * 256;
+        for (uint32_t base = s; base < e; base += NT) {
+          const uint32_t i = base + tid;
+          float dist = f_inf();
+          uint32_t key = kNoPos;
+          if (i < e) {
+            key = i;
             dist = adc_sum_rt<ORDER>(L, a.codes + (uint64_t)i * M, M);
           }
+          tk.offer(dist, key);
         }
-        tk.offer(dist, key);
       }
     }
     __syncthreads();
   }
 
-  // merge the four wave lists in wave 0
+  // merge the wave lists in wave 0
   float* md = smem;
-  uint32_t* mp = reinterpret_cast<uint32_t*>(smem + 4 * 64 * R);
+  uint32_t* mp = reinterpret_cast<uint32_t*>(smem + NW * 64 * R);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     md[wave * 64 * R + r * 64 + lane] = tk.d[r];
@@ -265,7 +338,7 @@ __global__ __launch_bounds__(kThreads) void ivfpq_scan_kernel(IvfPqScanArgs a, i
   }
   __syncthreads();
   if (wave != 0) return;
-  for (int w = 1; w < 4; ++w)
+  for (int w = 1; w < NW; ++w)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int s = w * 64 * R + r * 64 + lane;
@@ -289,14 +362,32 @@ __global__ __launch_bounds__(kThreads) void ivfpq_scan_kernel(IvfPqScanArgs a, i
 
 using ScanFn = void (*)(IvfPqScanArgs, int);
 
+// Launch shape per specialisation: threads, code vectors in flight per lane,
+// and lists per LUT group (G LUTs of M KiB each stay within 64 KiB of LDS so
+// two 512-thread workgroups fit a CU's 160 KiB).
+template <int MT, int DT>
+struct ScanShape {
+  static constexpr int NT = 256, U = 1, GMAX = 8;
+};
+template <>
+struct ScanShape<16, 8> {
+  static constexpr int NT = 512, U = 4, GMAX = 4;
+};
+template <>
+struct ScanShape<32, 3> {
+  static constexpr int NT = 512, U = 2, GMAX = 2;
+};
+
 template <int MT, int DT, int ORDER>
 ScanFn pick_scan_r(int R) {
+  using S = ScanShape<MT, DT>;
+  // k above 256 needs 8-16 top-k registers per list: one batch in flight
   switch (R) {
-    case 1: return ivfpq_scan_kernel<MT, DT, 1, ORDER>;
-    case 2: return ivfpq_scan_kernel<MT, DT, 2, ORDER>;
-    case 4: return ivfpq_scan_kernel<MT, DT, 4, ORDER>;
-    case 8: return ivfpq_scan_kernel<MT, DT, 8, ORDER>;
-    case 16: return ivfpq_scan_kernel<MT, DT, 16, ORDER>;
+    case 1: return ivfpq_scan_kernel<MT, DT, 1, ORDER, S::NT, S::U, S::GMAX>;
+    case 2: return ivfpq_scan_kernel<MT, DT, 2, ORDER, S::NT, S::U, S::GMAX>;
+    case 4: return ivfpq_scan_kernel<MT, DT, 4, ORDER, S::NT, S::U, S::GMAX>;
+    case 8: return ivfpq_scan_kernel<MT, DT, 8, ORDER, S::NT, 1, S::GMAX>;
+    case 16: return ivfpq_scan_kernel<MT, DT, 16, ORDER, S::NT, 1, S::GMAX>;
   }
   return nullptr;
 }
@@ -440,26 +531,33 @@ hipError_t launch_ivfpq_scan(const IvfPqScanArgs& a, hipStream_t stream) {
   if (a.k <= 0 || a.k > 1024 || a.M <= 0 || a.dsub <= 0) return hipErrorInvalidValue;
   const int R = topk_regs(a.k);
   ScanFn fn;
-  int G;
+  int G, nt;
+  bool static_lds = true;  // specialised shapes size their LDS at compile time
   if (a.M == 16 && a.dsub == 8) {
     fn = pick_scan<16, 8>(R, a.order);
-    G = 4;
+    G = ScanShape<16, 8>::GMAX;
+    nt = ScanShape<16, 8>::NT;
   } else if (a.M == 32 && a.dsub == 3) {
     fn = pick_scan<32, 3>(R, a.order);
-    G = 2;
+    G = ScanShape<32, 3>::GMAX;
+    nt = ScanShape<32, 3>::NT;
   } else {
     fn = pick_scan<0, 0>(R, a.order);
-    G = std::max(1, std::min(8, 64 / a.M));
+    G = std::max(1, std::min(ScanShape<0, 0>::GMAX, 64 / a.M));
+    nt = ScanShape<0, 0>::NT;
+    static_lds = false;
   }
   if (!fn) return hipErrorInvalidValue;
   const size_t lut_bytes = sizeof(float) * ((size_t)G * a.M * 256 + (size_t)G * a.dim);
-  const size_t merge_bytes = (size_t)4 * 64 * R * 8;
-  const size_t lds = std::max(lut_bytes, merge_bytes);
-  if (lds > 160 * 1024) return hipErrorInvalidValue;
-  hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     160 * 1024);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(fn, dim3((unsigned)a.nq), dim3(kThreads), lds, stream, a, G);
+  const size_t merge_bytes = (size_t)(nt / 64) * 64 * R * 8;
+  if (std::max(lut_bytes, merge_bytes) > 160 * 1024) return hipErrorInvalidValue;
+  const size_t lds = static_lds ? 0 : std::max(lut_bytes, merge_bytes);
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(fn, dim3((unsigned)a.nq), dim3(nt), lds, stream, a, G);
   return hipGetLastError();
 }
 
