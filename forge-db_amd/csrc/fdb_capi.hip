@@ -56,7 +56,7 @@ void validate(const IvfPqArtifacts& a) {
     throw Error(FDB_ERR_INVALID_ARGUMENT, "list_offsets must have nlist+1 entries starting at 0");
   for (uint32_t l = 0; l < a.nlist; ++l)
     if (a.offsets[l + 1] < a.offsets[l]) throw Error(FDB_ERR_INVALID_ARGUMENT, "list_offsets decrease");
-  if (a.dim > 4096) throw Error(FDB_ERR_UNSUPPORTED, "dim above 4096");
+  if (a.dim > 2048) throw Error(FDB_ERR_UNSUPPORTED, "dim above 2048");
   if (a.M > 128) throw Error(FDB_ERR_UNSUPPORTED, "more than 128 subvectors");
 }
 

@@ -175,7 +175,7 @@ std::vector<float> kmeans_gpu(const float* h_points, uint64_t n, int dim, int k,
   DevBuf<uint32_t> d_mem, d_off;
   d_pts.upload(h_points, n * dim, s);
   d_c.reserve((size_t)k * dim);
-  d_cT.reserve((size_t)k * dim);
+  d_cT.reserve((size_t)centT_ld(k) * dim);
   d_next.reserve((size_t)k * dim);
   d_assign.reserve(n);
   std::vector<int32_t> assign(n);
@@ -212,7 +212,7 @@ IvfPqIndex::IvfPqIndex(IvfPqArtifacts&& art) : host_(std::move(art)) {
   const uint64_t N = host_.ids.size();
   if (N >= 0xFFFFFFFFull) throw Error(FDB_ERR_UNSUPPORTED, "more than 2^32-2 vectors");
   centroids_.upload(host_.centroids.data(), host_.centroids.size(), stream_);
-  centT_.reserve(host_.centroids.size());
+  centT_.reserve((size_t)centT_ld(host_.nlist) * host_.dim);
   FDB_HIP(launch_transpose_centroids(centroids_.p, host_.nlist, host_.dim, centT_.p, stream_));
   codebooks_.upload(host_.codebooks.data(), host_.codebooks.size(), stream_);
   std::vector<uint32_t> off32(host_.offsets.begin(), host_.offsets.end());
@@ -441,7 +441,7 @@ IvfPqArtifacts IvfPqIndex::build(const float* vectors, const uint64_t* ids, uint
     throw Error(FDB_ERR_INVALID_ARGUMENT, "build needs n, dim, nlist > 0 and M dividing dim");
   if (metric > 4) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown metric");
   if (n >= 0xFFFFFFFFull) throw Error(FDB_ERR_UNSUPPORTED, "more than 2^32-2 vectors");
-  if (dim > 4096) throw Error(FDB_ERR_UNSUPPORTED, "dim above 4096");
+  if (dim > 2048) throw Error(FDB_ERR_UNSUPPORTED, "dim above 2048");
   for (uint64_t i = 0; i < n * dim; ++i)
     if (std::isnan(vectors[i])) throw Error(FDB_ERR_NAN, "NaN in the vectors to index");
   const uint32_t dsub = dim / M;
@@ -476,7 +476,7 @@ IvfPqArtifacts IvfPqIndex::build(const float* vectors, const uint64_t* ids, uint
   DevBuf<int32_t> d_assign;
   d_vec.upload(vectors, n * dim, s);
   d_cent.upload(cents.data(), cents.size(), s);
-  d_centT.reserve(cents.size());
+  d_centT.reserve((size_t)centT_ld(nlist) * dim);
   d_assign.reserve(n);
   FDB_HIP(launch_transpose_centroids(d_cent.p, nlist, dim, d_centT.p, s));
   FDB_HIP(launch_assign(d_vec.p, n, dim, d_centT.p, nlist, d_assign.p, s));

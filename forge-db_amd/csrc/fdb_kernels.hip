@@ -20,27 +20,27 @@ namespace fdb {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kCoarseQB = 8;     // queries per workgroup in the coarse kernel
-constexpr int kCoarseChunk = 1024;  // centroids per LDS distance chunk
+constexpr int kCoarseTQ = 4;                 // queries per wave
+constexpr int kCoarseQB = 4 * kCoarseTQ;     // queries per workgroup (4 waves)
 
 // ---------------------------------------------------------------------------
-// Coarse selection.  One workgroup: kCoarseQB queries against all centroids.
-// Thread c computes centroid c's distance to each query: for lane l of the
-// reference's 8 FMA lanes it streams rows l*d8 .. l*d8+d8-1 of centT (one
-// coalesced float per lane per row), so each query's 8 lane chains are formed
-// one after another and added to the running total left to right.  Queries
-// sit in LDS in the same permuted order and are read as wave-uniform
-// broadcasts.  Distances for a chunk of centroids go to LDS; each wave then
-// selects for two of the queries with a WaveTopK.
+// Coarse selection.  A workgroup takes kCoarseQB queries, each wave 4 of
+// them, and sweeps all centroids 256 at a time: lane L holds centroids
+// c..c+3 (c = base + 4L).  For lane l of the reference's 8 FMA lanes it
+// walks rows l*d8 .. l*d8+d8-1 of centT: one coalesced float4 of centroid
+// values and one wave-uniform (broadcast) float4 of the wave's 4 query values
+// per row feed 16 independent FMA chains; each finished lane chain is added
+// to the running total left to right, then the tail rows are added as
+// separate multiply and add.  The 16 distances go straight from registers
+// into the wave's 4 WaveTopK lists.  centT rows have ldc >= nlist (a
+// multiple of 256) entries; columns >= nlist are never selected.
 // ---------------------------------------------------------------------------
 template <int R>
 __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
     const float* __restrict__ queries, uint64_t nq, int dim, const float* __restrict__ centT,
-    int nlist, int nsel, int32_t* __restrict__ out_lists, float* __restrict__ out_dists,
+    int ldc, int nlist, int nsel, int32_t* __restrict__ out_lists, float* __restrict__ out_dists,
     int* __restrict__ err_flag) {
-  extern __shared__ float smem[];
-  float* qs = smem;                         // [QB][dim], permuted
-  float* dist = smem + kCoarseQB * dim;     // [QB][chunk]
+  extern __shared__ float qsT[];  // [dim][QB], rows permuted
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -51,80 +51,84 @@ __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
     const int qq = e / dim;
     const int d = e - qq * dim;
     const int row = (d >= 8 * d8) ? d : (d % 8) * d8 + d / 8;
-    qs[qq * dim + row] = (q0 + qq < nq) ? queries[(q0 + qq) * (uint64_t)dim + d] : 0.0f;
+    qsT[row * kCoarseQB + qq] = (q0 + qq < nq) ? queries[(q0 + qq) * (uint64_t)dim + d] : 0.0f;
   }
-
-  constexpr int QW = kCoarseQB / 4;  // queries selected per wave
-  WaveTopK<R> tk[QW];
+  WaveTopK<R> tk[kCoarseTQ];
 #pragma unroll
-  for (int j = 0; j < QW; ++j) tk[j].init(nsel);
+  for (int t = 0; t < kCoarseTQ; ++t) tk[t].init(nsel);
   bool saw_nan = false;
   __syncthreads();
 
-  for (int c0 = 0; c0 < nlist; c0 += kCoarseChunk) {
-    for (int cc = tid; cc < kCoarseChunk; cc += kThreads) {
-      const int c = c0 + cc;
-      float tot[kCoarseQB];
+  const float* __restrict__ qw = qsT + wave * kCoarseTQ;
+  for (int base = 0; base < nlist; base += 256) {
+    const int c = base + 4 * lane;
+    float tot[kCoarseTQ][4];
 #pragma unroll
-      for (int qq = 0; qq < kCoarseQB; ++qq) tot[qq] = 0.0f;
-      if (c < nlist) {
-        for (int l = 0; l < 8 && d8 > 0; ++l) {
-          float chain[kCoarseQB];
+    for (int t = 0; t < kCoarseTQ; ++t)
 #pragma unroll
-          for (int qq = 0; qq < kCoarseQB; ++qq) chain[qq] = 0.0f;
-          for (int i = 0; i < d8; ++i) {
-            const int row = l * d8 + i;
-            const float cv = centT[(uint64_t)row * nlist + c];
+      for (int u = 0; u < 4; ++u) tot[t][u] = 0.0f;
+#pragma unroll 1
+    for (int l = 0; l < 8 && d8 > 0; ++l) {
+      float ch[kCoarseTQ][4];
 #pragma unroll
-            for (int qq = 0; qq < kCoarseQB; ++qq) {
-              const float df = qs[qq * dim + row] - cv;
-              chain[qq] = __builtin_fmaf(df, df, chain[qq]);
-            }
+      for (int t = 0; t < kCoarseTQ; ++t)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ch[t][u] = 0.0f;
+#pragma unroll 2
+      for (int i = 0; i < d8; ++i) {
+        const int row = l * d8 + i;
+        const float4 cv = *reinterpret_cast<const float4*>(centT + (uint64_t)row * ldc + c);
+        const float4 qv = *reinterpret_cast<const float4*>(qw + row * kCoarseQB);
+        const float cva[4] = {cv.x, cv.y, cv.z, cv.w};
+        const float qva[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int t = 0; t < kCoarseTQ; ++t)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float df = qva[t] - cva[u];
+            ch[t][u] = __builtin_fmaf(df, df, ch[t][u]);
           }
-#pragma unroll
-          for (int qq = 0; qq < kCoarseQB; ++qq) tot[qq] = (l == 0) ? chain[qq] : tot[qq] + chain[qq];
-        }
-        for (int row = 8 * d8; row < dim; ++row) {
-          const float cv = centT[(uint64_t)row * nlist + c];
-#pragma unroll
-          for (int qq = 0; qq < kCoarseQB; ++qq) {
-            const float df = qs[qq * dim + row] - cv;
-            tot[qq] = tot[qq] + df * df;
-          }
-        }
       }
 #pragma unroll
-      for (int qq = 0; qq < kCoarseQB; ++qq) dist[qq * kCoarseChunk + cc] = tot[qq];
-    }
-    __syncthreads();
+      for (int t = 0; t < kCoarseTQ; ++t)
 #pragma unroll
-    for (int j = 0; j < QW; ++j) {
-      const int qq = wave + 4 * j;
-      for (int cc = 0; cc < kCoarseChunk && c0 + cc < nlist; cc += 64) {
-        const int c = c0 + cc + lane;
-        float dv = f_inf();
-        uint32_t key = kNoPos;
-        if (c < nlist) {
-          dv = dist[qq * kCoarseChunk + cc + lane];
-          key = (uint32_t)c;
-          if (dv != dv) saw_nan = true;
+        for (int u = 0; u < 4; ++u) tot[t][u] = (l == 0) ? ch[t][u] : tot[t][u] + ch[t][u];
+    }
+    for (int row = 8 * d8; row < dim; ++row) {
+      const float4 cv = *reinterpret_cast<const float4*>(centT + (uint64_t)row * ldc + c);
+      const float4 qv = *reinterpret_cast<const float4*>(qw + row * kCoarseQB);
+      const float cva[4] = {cv.x, cv.y, cv.z, cv.w};
+      const float qva[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+      for (int t = 0; t < kCoarseTQ; ++t)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float df = qva[t] - cva[u];
+          tot[t][u] = tot[t][u] + df * df;
         }
-        tk[j].offer(dv, key);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool in = c + u < nlist;
+#pragma unroll
+      for (int t = 0; t < kCoarseTQ; ++t) {
+        const float dv = in ? tot[t][u] : f_inf();
+        if (in && dv != dv) saw_nan = true;
+        tk[t].offer(dv, in ? (uint32_t)(c + u) : kNoPos);
       }
     }
-    __syncthreads();
   }
 
 #pragma unroll
-  for (int j = 0; j < QW; ++j) {
-    const uint64_t q = q0 + wave + 4 * j;
+  for (int t = 0; t < kCoarseTQ; ++t) {
+    const uint64_t q = q0 + wave * kCoarseTQ + t;
     if (q >= nq) continue;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int s = r * 64 + lane;
       if (s < nsel) {
-        out_lists[q * nsel + s] = (int32_t)tk[j].p[r];
-        if (out_dists) out_dists[q * nsel + s] = tk[j].d[r];
+        out_lists[q * nsel + s] = (int32_t)tk[t].p[r];
+        if (out_dists) out_dists[q * nsel + s] = tk[t].d[r];
       }
     }
   }
@@ -132,20 +136,18 @@ __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
 }
 
 template <int R>
-hipError_t launch_coarse_t(const float* queries, uint64_t nq, int dim, const float* centT, int nlist,
-                           int nsel, int32_t* out_lists, float* out_dists, int* err_flag,
+hipError_t launch_coarse_t(const float* queries, uint64_t nq, int dim, const float* centT, int ldc,
+                           int nlist, int nsel, int32_t* out_lists, float* out_dists, int* err_flag,
                            hipStream_t stream) {
-  const size_t lds = sizeof(float) * ((size_t)kCoarseQB * dim + (size_t)kCoarseQB * kCoarseChunk);
-  static bool attr_set = false;
-  if (!attr_set) {
+  const size_t lds = sizeof(float) * (size_t)kCoarseQB * dim;
+  if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void*)coarse_select_kernel<R>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    attr_set = true;
   }
   const uint64_t blocks = (nq + kCoarseQB - 1) / kCoarseQB;
   hipLaunchKernelGGL(coarse_select_kernel<R>, dim3((unsigned)blocks), dim3(kThreads), lds, stream,
-                     queries, nq, dim, centT, nlist, nsel, out_lists, out_dists, err_flag);
+                     queries, nq, dim, centT, ldc, nlist, nsel, out_lists, out_dists, err_flag);
   return hipGetLastError();
 }
 
@@ -410,13 +412,14 @@ int topk_regs(int k) {
 __global__ __launch_bounds__(kThreads) void transpose_centroids_kernel(const float* __restrict__ cents,
                                                                        int k, int dim,
                                                                        float* __restrict__ centT) {
+  const int ldc = centT_ld(k);
   const uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (e >= (uint64_t)k * dim) return;
+  if (e >= (uint64_t)ldc * dim) return;
   const int c = (int)(e / dim);
   const int d = (int)(e - (uint64_t)c * dim);
   const int d8 = dim / 8;
   const int row = (d >= 8 * d8) ? d : (d % 8) * d8 + d / 8;
-  centT[(uint64_t)row * k + c] = cents[e];
+  centT[(uint64_t)row * ldc + c] = (c < k) ? cents[e] : 0.0f;
 }
 
 // One workgroup per cluster; thread t owns dimensions t, t+256, ...; the
@@ -515,13 +518,13 @@ hipError_t launch_coarse_select(const float* queries, uint64_t nq, int dim, cons
                                 int nlist, int nsel, int32_t* out_lists, float* out_dists,
                                 int* err_flag, hipStream_t stream) {
   if (nq == 0) return hipSuccess;
-  if (nsel <= 0 || nsel > 1024 || nlist <= 0 || dim <= 0) return hipErrorInvalidValue;
+  if (nsel <= 0 || nsel > 1024 || nlist <= 0 || dim <= 0 || dim > 2048) return hipErrorInvalidValue;
   switch (topk_regs(nsel)) {
-    case 1: return launch_coarse_t<1>(queries, nq, dim, centT, nlist, nsel, out_lists, out_dists, err_flag, stream);
-    case 2: return launch_coarse_t<2>(queries, nq, dim, centT, nlist, nsel, out_lists, out_dists, err_flag, stream);
-    case 4: return launch_coarse_t<4>(queries, nq, dim, centT, nlist, nsel, out_lists, out_dists, err_flag, stream);
-    case 8: return launch_coarse_t<8>(queries, nq, dim, centT, nlist, nsel, out_lists, out_dists, err_flag, stream);
-    case 16: return launch_coarse_t<16>(queries, nq, dim, centT, nlist, nsel, out_lists, out_dists, err_flag, stream);
+    case 1: return launch_coarse_t<1>(queries, nq, dim, centT, centT_ld(nlist), nlist, nsel, out_lists, out_dists, err_flag, stream);
+    case 2: return launch_coarse_t<2>(queries, nq, dim, centT, centT_ld(nlist), nlist, nsel, out_lists, out_dists, err_flag, stream);
+    case 4: return launch_coarse_t<4>(queries, nq, dim, centT, centT_ld(nlist), nlist, nsel, out_lists, out_dists, err_flag, stream);
+    case 8: return launch_coarse_t<8>(queries, nq, dim, centT, centT_ld(nlist), nlist, nsel, out_lists, out_dists, err_flag, stream);
+    case 16: return launch_coarse_t<16>(queries, nq, dim, centT, centT_ld(nlist), nlist, nsel, out_lists, out_dists, err_flag, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -598,7 +601,7 @@ hipError_t launch_pq_encode(const float* vectors, const uint64_t* rows, const in
 
 hipError_t launch_transpose_centroids(const float* cents, int k, int dim, float* centT,
                                       hipStream_t stream) {
-  const uint64_t total = (uint64_t)k * dim;
+  const uint64_t total = (uint64_t)centT_ld(k) * dim;
   if (total == 0) return hipSuccess;
   hipLaunchKernelGGL(transpose_centroids_kernel, dim3((unsigned)((total + kThreads - 1) / kThreads)),
                      dim3(kThreads), 0, stream, cents, k, dim, centT);

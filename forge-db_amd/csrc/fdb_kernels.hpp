@@ -17,6 +17,10 @@ hipError_t launch_coarse_select(const float* queries, uint64_t nq, int dim, cons
                                 int nlist, int nsel, int32_t* out_lists, float* out_dists,
                                 int* err_flag, hipStream_t stream);
 
+// Leading dimension of centT: rows are padded to a multiple of 256 columns
+// (the coarse kernel reads 256 centroids per sweep); padding is zero.
+__host__ __device__ inline int centT_ld(int k) { return (k + 255) / 256 * 256; }
+
 // Row of the permuted dimension order used by centT: for the 8*floor(dim/8)
 // leading dimensions, dim 8*i + l sits at row l*floor(dim/8) + i; the tail
 // dimensions keep their place.
@@ -75,7 +79,7 @@ hipError_t launch_pq_encode(const float* vectors, const uint64_t* rows, const in
                             uint64_t n, int dim, const float* centroids, const float* codebooks,
                             int M, int dsub, uint8_t* codes, hipStream_t stream);
 
-// Transpose + permute centroids [k][dim] into centT [dim][k].
+// Transpose + permute centroids [k][dim] into centT [dim][centT_ld(k)].
 hipError_t launch_transpose_centroids(const float* cents, int k, int dim, float* centT,
                                       hipStream_t stream);
 
