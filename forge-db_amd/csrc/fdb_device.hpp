@@ -211,14 +211,16 @@ struct WaveTopK {
   __device__ __forceinline__ void read_tau() {
     const int s = k - 1;
     const int rs = s >> 6;
+    // running comparison, not `r == rs`: an equality select chain over an
+    // array is turned into an indexed (scratch) access by the compiler
     float v = d[0];
     uint32_t w = p[0];
 #pragma unroll
-    for (int r = 1; r < R; ++r)
-      if (r == rs) {
-        v = d[r];
-        w = p[r];
-      }
+    for (int r = 1; r < R; ++r) {
+      const bool in = r <= rs;
+      v = in ? d[r] : v;
+      w = in ? p[r] : w;
+    }
     tau = readlane_f(v, s & 63);
     tau_p = readlane_u(w, s & 63);
   }

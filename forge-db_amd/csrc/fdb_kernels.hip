@@ -35,7 +35,9 @@ constexpr int kCoarseQB = 4 * kCoarseTQ;     // queries per workgroup (4 waves)
 // into the wave's 4 WaveTopK lists.  centT rows have ldc >= nlist (a
 // multiple of 256) entries; columns >= nlist are never selected.
 // ---------------------------------------------------------------------------
-template <int R>
+// D8T: compile-time floor(dim / 8) (0 = runtime), so one lane's rows can be
+// loaded before any is used.
+template <int R, int D8T>
 __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
     const float* __restrict__ queries, uint64_t nq, int dim, const float* __restrict__ centT,
     int ldc, int nlist, int nsel, int32_t* __restrict__ out_lists, float* __restrict__ out_dists,
@@ -45,7 +47,7 @@ __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const uint64_t q0 = (uint64_t)blockIdx.x * kCoarseQB;
-  const int d8 = dim / 8;
+  const int d8 = D8T ? D8T : dim / 8;
 
   for (int e = tid; e < kCoarseQB * dim; e += kThreads) {
     const int qq = e / dim;
@@ -74,20 +76,40 @@ __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
       for (int t = 0; t < kCoarseTQ; ++t)
 #pragma unroll
         for (int u = 0; u < 4; ++u) ch[t][u] = 0.0f;
+      if constexpr (D8T > 0) {
+        float4 cvs[D8T];
+#pragma unroll
+        for (int i = 0; i < D8T; ++i)
+          cvs[i] = *reinterpret_cast<const float4*>(centT + (uint64_t)(l * D8T + i) * ldc + c);
+#pragma unroll
+        for (int i = 0; i < D8T; ++i) {
+          const float4 qv = *reinterpret_cast<const float4*>(qw + (l * D8T + i) * kCoarseQB);
+          const float cva[4] = {cvs[i].x, cvs[i].y, cvs[i].z, cvs[i].w};
+          const float qva[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+          for (int t = 0; t < kCoarseTQ; ++t)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const float df = qva[t] - cva[u];
+              ch[t][u] = __builtin_fmaf(df, df, ch[t][u]);
+            }
+        }
+      } else {
 #pragma unroll 2
-      for (int i = 0; i < d8; ++i) {
-        const int row = l * d8 + i;
-        const float4 cv = *reinterpret_cast<const float4*>(centT + (uint64_t)row * ldc + c);
-        const float4 qv = *reinterpret_cast<const float4*>(qw + row * kCoarseQB);
-        const float cva[4] = {cv.x, cv.y, cv.z, cv.w};
-        const float qva[4] = {qv.x, qv.y, qv.z, qv.w};
+        for (int i = 0; i < d8; ++i) {
+          const int row = l * d8 + i;
+          const float4 cv = *reinterpret_cast<const float4*>(centT + (uint64_t)row * ldc + c);
+          const float4 qv = *reinterpret_cast<const float4*>(qw + row * kCoarseQB);
+          const float cva[4] = {cv.x, cv.y, cv.z, cv.w};
+          const float qva[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
-        for (int t = 0; t < kCoarseTQ; ++t)
+          for (int t = 0; t < kCoarseTQ; ++t)
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float df = qva[t] - cva[u];
-            ch[t][u] = __builtin_fmaf(df, df, ch[t][u]);
-          }
+            for (int u = 0; u < 4; ++u) {
+              const float df = qva[t] - cva[u];
+              ch[t][u] = __builtin_fmaf(df, df, ch[t][u]);
+            }
+        }
       }
 #pragma unroll
       for (int t = 0; t < kCoarseTQ; ++t)
@@ -140,14 +162,17 @@ hipError_t launch_coarse_t(const float* queries, uint64_t nq, int dim, const flo
                            int nlist, int nsel, int32_t* out_lists, float* out_dists, int* err_flag,
                            hipStream_t stream) {
   const size_t lds = sizeof(float) * (size_t)kCoarseQB * dim;
+  void (*fn)(const float*, uint64_t, int, const float*, int, int, int, int32_t*, float*, int*) =
+      dim / 8 == 16 ? coarse_select_kernel<R, 16>
+                    : (dim / 8 == 12 ? coarse_select_kernel<R, 12> : coarse_select_kernel<R, 0>);
   if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)coarse_select_kernel<R>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
     if (e != hipSuccess) return e;
   }
   const uint64_t blocks = (nq + kCoarseQB - 1) / kCoarseQB;
-  hipLaunchKernelGGL(coarse_select_kernel<R>, dim3((unsigned)blocks), dim3(kThreads), lds, stream,
-                     queries, nq, dim, centT, ldc, nlist, nsel, out_lists, out_dists, err_flag);
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kThreads), lds, stream, queries, nq, dim,
+                     centT, ldc, nlist, nsel, out_lists, out_dists, err_flag);
   return hipGetLastError();
 }
 
@@ -313,7 +338,9 @@ __global__ __launch_bounds__(NT) void ivfpq_scan_kernel(IvfPqScanArgs a, int G) 
     } else {
       // generic shape: lists one after another, one code per lane
       for (int j = 0; j < ng; ++j) {
-        const uint32_t s = gl.start[j], e = s + gl.len[j];
+        const int p = pr[g0 + j];
+        if (p < 0 || p >= a.nlist) continue;  // uniform
+        const uint32_t s = a.list_off[p], e = a.list_off[p + 1];
         const float* __restrict__ L = lut + (size_t)j * M * 256;
         for (uint32_t base = s; base < e; base += NT) {
           const uint32_t i = base + tid;
