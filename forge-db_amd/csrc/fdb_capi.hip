@@ -164,6 +164,18 @@ void fdb_ivfpq_set_nprobe(fdb_ivfpq* h, uint64_t nprobe) {
 
 uint64_t fdb_ivfpq_nprobe(const fdb_ivfpq* h) { return (h && h->impl) ? h->impl->nprobe() : 0; }
 
+fdb_status fdb_ivfpq_set_lut_mode(fdb_ivfpq* h, uint32_t mode) {
+  return guarded([&] {
+    if (mode > 1) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown LUT mode");
+    if (!H(h)->set_lut_mode((int)mode))
+      throw Error(FDB_ERR_UNSUPPORTED, "fast LUTs need 16 x 8 or 32 x 3 subvectors");
+  });
+}
+
+uint32_t fdb_ivfpq_lut_mode(const fdb_ivfpq* h) {
+  return (h && h->impl) ? (uint32_t)h->impl->lut_mode() : 0;
+}
+
 fdb_status fdb_ivfpq_describe(const fdb_ivfpq* h, fdb_ivfpq_desc* out) {
   return guarded([&] {
     if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");

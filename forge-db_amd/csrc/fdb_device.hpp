@@ -259,6 +259,18 @@ struct WaveTopK {
   // (+inf, kNoPos).
   __device__ __forceinline__ void offer(float dist, uint32_t key) {
     uint64_t mask = __ballot(pair_lt(dist, key, tau, tau_p));
+    drain(mask, dist, key);
+  }
+
+  // Hot-loop form: `valid` lanes offer (dist, key).  The per-lane test is a
+  // single compare (dist <= tau); the exact pair order is checked only for
+  // the few lanes that pass it.
+  __device__ __forceinline__ void offer_valid(float dist, uint32_t key, bool valid) {
+    uint64_t mask = __ballot(valid && dist <= tau);
+    drain(mask, dist, key);
+  }
+
+  __device__ __forceinline__ void drain(uint64_t mask, float dist, uint32_t key) {
     while (mask) {
       const int l = __ffsll((unsigned long long)mask) - 1;
       mask &= mask - 1;

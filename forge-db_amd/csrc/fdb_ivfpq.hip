@@ -215,6 +215,8 @@ IvfPqIndex::IvfPqIndex(IvfPqArtifacts&& art) : host_(std::move(art)) {
   centT_.reserve((size_t)centT_ld(host_.nlist) * host_.dim);
   FDB_HIP(launch_transpose_centroids(centroids_.p, host_.nlist, host_.dim, centT_.p, stream_));
   codebooks_.upload(host_.codebooks.data(), host_.codebooks.size(), stream_);
+  cbnorm_.reserve((size_t)host_.M * 256);
+  FDB_HIP(launch_codebook_norms(codebooks_.p, host_.M, host_.dsub, cbnorm_.p, stream_));
   std::vector<uint32_t> off32(host_.offsets.begin(), host_.offsets.end());
   off_.upload(off32.data(), off32.size(), stream_);
   codes_.upload(host_.codes.data(), std::max<size_t>(host_.codes.size(), 16), stream_);
@@ -231,6 +233,14 @@ IvfPqIndex::~IvfPqIndex() {
   for (auto& e : ev_)
     if (e) (void)hipEventDestroy(e);
   if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+bool IvfPqIndex::set_lut_mode(int mode) {
+  if (mode != 0 && mode != 1) return false;
+  const bool shaped = (host_.M == 16 && host_.dsub == 8) || (host_.M == 32 && host_.dsub == 3);
+  if (mode == 1 && !shaped) return false;
+  lut_mode_.store(mode, std::memory_order_relaxed);
+  return true;
 }
 
 void IvfPqIndex::enable_reranking(const float* v, uint64_t factor) {
@@ -290,6 +300,8 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
   a.ids = ids_.p;
   a.k = (int)fetch;
   a.order = order;
+  a.lut_mode = lut_mode();
+  a.cbnorm = cbnorm_.p;
   if (rerank) {
     cand_ids_.reserve(nq * fetch);
     cand_d_.reserve(nq * fetch);

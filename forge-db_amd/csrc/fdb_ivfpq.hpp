@@ -28,6 +28,11 @@ class IvfPqIndex {
   void set_nprobe(uint64_t np) { nprobe_.store(np < host_.nlist ? np : host_.nlist, std::memory_order_relaxed); }
   uint64_t nprobe() const { return nprobe_.load(std::memory_order_relaxed); }
 
+  // 0 = exact LUTs (the reference's rounding), 1 = fast LUTs; returns false
+  // when the index shape has no fast kernel
+  bool set_lut_mode(int mode);
+  int lut_mode() const { return lut_mode_.load(std::memory_order_relaxed); }
+
   void enable_reranking(const float* vectors_list_order, uint64_t factor);
 
   // single query with search() semantics; returns count
@@ -53,10 +58,11 @@ class IvfPqIndex {
 
   IvfPqArtifacts host_;
   std::atomic<uint64_t> nprobe_{1};
+  std::atomic<int> lut_mode_{0};
   hipStream_t stream_ = nullptr;
   std::mutex mu_;
 
-  DevBuf<float> centroids_, centT_, codebooks_, originals_;
+  DevBuf<float> centroids_, centT_, codebooks_, cbnorm_, originals_;
   DevBuf<uint32_t> off_;
   DevBuf<uint8_t> codes_;
   DevBuf<uint64_t> ids_;

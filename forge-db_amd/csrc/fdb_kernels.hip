@@ -227,10 +227,12 @@ struct GroupLists {
 // striding by NW; U batches per wave are loaded before any is summed so U
 // code loads are in flight.  The loads are branch-free: a batch or lane past
 // the end re-reads the list's last code (len > 0) and carries key kNoPos.
-template <int MT, int ORDER, int R, int NW, int U, int J>
+// FAST: the LUT holds |cb|^2 - 2<r, cb> and base = |r|^2 is added to every
+// sum; otherwise base is unused (exact mode adds nothing).
+template <int MT, int ORDER, int R, int NW, int U, int J, int FAST>
 __device__ __forceinline__ void scan_list(const float* __restrict__ lut, uint32_t start, uint32_t len,
-                                          uint32_t w0, int lane, const uint8_t* __restrict__ codes,
-                                          WaveTopK<R>& tk) {
+                                          float base, uint32_t w0, int lane,
+                                          const uint8_t* __restrict__ codes, WaveTopK<R>& tk) {
   const uint32_t nb = (len + 63) / 64;
   const uint32_t last = start + len - 1;
   for (uint32_t b0 = w0; b0 < nb; b0 += (uint32_t)(NW * U)) {
@@ -246,32 +248,39 @@ __device__ __forceinline__ void scan_list(const float* __restrict__ lut, uint32_
     float dist[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const float d = adc_sum<MT, ORDER>(lut + J * (MT * 256), w[u]);
-      dist[u] = (key[u] != kNoPos) ? d : f_inf();
+      dist[u] = adc_sum<MT, ORDER>(lut + J * (MT * 256), w[u]);
+      if constexpr (FAST) dist[u] = base + dist[u];
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) tk.offer(dist[u], key[u]);
+    for (int u = 0; u < U; ++u) tk.offer_valid(dist[u], key[u], key[u] != kNoPos);
   }
 }
 
-template <int MT, int ORDER, int R, int NW, int U, int GMAX, int J>
-__device__ __forceinline__ void scan_group(const float* __restrict__ lut, const GroupLists<GMAX>& gl,
-                                           uint32_t w0, int lane, const uint8_t* __restrict__ codes,
-                                           WaveTopK<R>& tk) {
+template <int MT, int ORDER, int R, int NW, int U, int GMAX, int J, int FAST>
+__device__ __forceinline__ void scan_group(const float* __restrict__ lut, const float* __restrict__ rr,
+                                           const GroupLists<GMAX>& gl, uint32_t w0, int lane,
+                                           const uint8_t* __restrict__ codes, WaveTopK<R>& tk) {
   if (J < gl.ng && gl.len[J] > 0)
-    scan_list<MT, ORDER, R, NW, U, J>(lut, gl.start[J], gl.len[J], w0, lane, codes, tk);
-  if constexpr (J + 1 < GMAX) scan_group<MT, ORDER, R, NW, U, GMAX, J + 1>(lut, gl, w0, lane, codes, tk);
+    scan_list<MT, ORDER, R, NW, U, J, FAST>(lut, gl.start[J], gl.len[J], FAST ? rr[J] : 0.0f, w0,
+                                            lane, codes, tk);
+  if constexpr (J + 1 < GMAX)
+    scan_group<MT, ORDER, R, NW, U, GMAX, J + 1, FAST>(lut, rr, gl, w0, lane, codes, tk);
 }
 
 // One workgroup per query.  MT/DT: compile-time M and dsub (0 = runtime, then
 // the LUTs live in dynamic LDS and each lane locates its list slot);
 // NT threads; U code batches in flight per wave; at most GMAX lists per LUT
 // group (G <= GMAX at run time).
-template <int MT, int DT, int R, int ORDER, int NT, int U, int GMAX>
+template <int MT, int DT, int R, int ORDER, int NT, int U, int GMAX, int FAST>
 __global__ __launch_bounds__(NT) void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
+  static_assert(!FAST || MT > 0, "fast LUT mode needs a specialised shape");
   constexpr int NW = NT / 64;
-  constexpr int SLDS = (MT > 0) ? GMAX * MT * 256 + GMAX * MT * DT : 1;
+  // static LDS holds the LUTs + residuals, and later the wave-list merge
+  // (NW lists of 64*R (distance, key) pairs)
+  constexpr int SLUT = GMAX * MT * 256 + GMAX * MT * DT;
+  constexpr int SLDS = (MT > 0) ? (SLUT > NW * 64 * R * 2 ? SLUT : NW * 64 * R * 2) : 1;
   __shared__ float s_static[SLDS];
+  __shared__ float s_rr[GMAX];  // fast mode: |q - c_p|^2 of each list of the group
   extern __shared__ float s_dyn[];
   float* smem = (MT > 0) ? s_static : s_dyn;
   const int M = MT ? MT : a.M;
@@ -312,9 +321,23 @@ __global__ __launch_bounds__(NT) void ivfpq_scan_kernel(IvfPqScanArgs a, int G) 
       const int j = e / D;
       const int d = e - j * D;
       const int p = pr[g0 + j];
-      resid[j * D + d] = (p >= 0 && p < a.nlist) ? qv[d] - a.centroids[(uint64_t)p * D + d] : 0.0f;
+      const float r = (p >= 0 && p < a.nlist) ? qv[d] - a.centroids[(uint64_t)p * D + d] : 0.0f;
+      resid[j * D + d] = FAST ? -2.0f * r : r;  // fast mode keeps -2r (exact scaling)
     }
     __syncthreads();
+    if constexpr (FAST) {
+      // |r|^2 of list j by wave j: (-2r)^2 / 4, any summation order
+      if (wave < ng) {
+        float acc = 0.0f;
+        for (int d = lane; d < D; d += 64) {
+          const float v = resid[wave * D + d];
+          acc = __builtin_fmaf(v, v, acc);
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+        if (lane == 0) s_rr[wave] = 0.25f * acc;
+      }
+    }
     // LUT: thread -> codeword tid & 255 of subspaces tid>>8, +NT/256, ...
     const int cw = tid & 255;
     for (int m = tid >> 8; m < M; m += NT / 256) {
@@ -323,9 +346,22 @@ __global__ __launch_bounds__(NT) void ivfpq_scan_kernel(IvfPqScanArgs a, int G) 
         float cbv[DT];
 #pragma unroll
         for (int t = 0; t < DT; ++t) cbv[t] = cbp[t];
+        if constexpr (FAST) {
+          const float nrm = a.cbnorm[m * 256 + cw];
 #pragma unroll
-        for (int j = 0; j < GMAX; ++j)
-          if (j < ng) lut[(j * M + m) * 256 + cw] = l2sq_ref<DT>(resid + j * D + m * DT, cbv);
+          for (int j = 0; j < GMAX; ++j)
+            if (j < ng) {
+              const float* __restrict__ r2 = resid + j * D + m * DT;  // -2r
+              float t = nrm;
+#pragma unroll
+              for (int i = 0; i < DT; ++i) t = __builtin_fmaf(r2[i], cbv[i], t);
+              lut[(j * M + m) * 256 + cw] = t;
+            }
+        } else {
+#pragma unroll
+          for (int j = 0; j < GMAX; ++j)
+            if (j < ng) lut[(j * M + m) * 256 + cw] = l2sq_ref<DT>(resid + j * D + m * DT, cbv);
+        }
       } else {
         for (int j = 0; j < ng; ++j)
           lut[(j * M + m) * 256 + cw] = l2sq_ref_rt(resid + j * D + m * dsub, cbp, dsub);
@@ -334,7 +370,7 @@ __global__ __launch_bounds__(NT) void ivfpq_scan_kernel(IvfPqScanArgs a, int G) 
     __syncthreads();
 
     if constexpr (MT > 0) {
-      scan_group<MT, ORDER, R, NW, U, GMAX, 0>(lut, gl, w0, lane, a.codes, tk);
+      scan_group<MT, ORDER, R, NW, U, GMAX, 0, FAST>(lut, s_rr, gl, w0, lane, a.codes, tk);
     } else {
       // generic shape: lists one after another, one code per lane
       for (int j = 0; j < ng; ++j) {
@@ -400,30 +436,38 @@ struct ScanShape {
 };
 template <>
 struct ScanShape<16, 8> {
-  static constexpr int NT = 512, U = 4, GMAX = 4;
+  static constexpr int NT = 512, U = 4, GMAX = 3;
 };
 template <>
 struct ScanShape<32, 3> {
   static constexpr int NT = 512, U = 2, GMAX = 2;
 };
 
-template <int MT, int DT, int ORDER>
+template <int MT, int DT, int ORDER, int FAST>
 ScanFn pick_scan_r(int R) {
   using S = ScanShape<MT, DT>;
   // k above 256 needs 8-16 top-k registers per list: one batch in flight
   switch (R) {
-    case 1: return ivfpq_scan_kernel<MT, DT, 1, ORDER, S::NT, S::U, S::GMAX>;
-    case 2: return ivfpq_scan_kernel<MT, DT, 2, ORDER, S::NT, S::U, S::GMAX>;
-    case 4: return ivfpq_scan_kernel<MT, DT, 4, ORDER, S::NT, S::U, S::GMAX>;
-    case 8: return ivfpq_scan_kernel<MT, DT, 8, ORDER, S::NT, 1, S::GMAX>;
-    case 16: return ivfpq_scan_kernel<MT, DT, 16, ORDER, S::NT, 1, S::GMAX>;
+    case 1: return ivfpq_scan_kernel<MT, DT, 1, ORDER, S::NT, S::U, S::GMAX, FAST>;
+    case 2: return ivfpq_scan_kernel<MT, DT, 2, ORDER, S::NT, S::U, S::GMAX, FAST>;
+    case 4: return ivfpq_scan_kernel<MT, DT, 4, ORDER, S::NT, S::U, S::GMAX, FAST>;
+    case 8: return ivfpq_scan_kernel<MT, DT, 8, ORDER, S::NT, 1, S::GMAX, FAST>;
+    case 16: return ivfpq_scan_kernel<MT, DT, 16, ORDER, S::NT, 1, S::GMAX, FAST>;
   }
   return nullptr;
 }
 
+// The fast LUT does not reproduce the reference's rounding, so its summation
+// order is immaterial: it always uses the 8-lane order.
 template <int MT, int DT>
-ScanFn pick_scan(int R, int order) {
-  return order == kAdcLanes8 ? pick_scan_r<MT, DT, kAdcLanes8>(R) : pick_scan_r<MT, DT, kAdcGroups4>(R);
+ScanFn pick_scan(int R, int order, int fast) {
+  if constexpr (MT > 0) {
+    if (fast) return pick_scan_r<MT, DT, kAdcLanes8, 1>(R);
+  } else {
+    if (fast) return nullptr;
+  }
+  return order == kAdcLanes8 ? pick_scan_r<MT, DT, kAdcLanes8, 0>(R)
+                             : pick_scan_r<MT, DT, kAdcGroups4, 0>(R);
 }
 
 int topk_regs(int k) {
@@ -564,15 +608,15 @@ hipError_t launch_ivfpq_scan(const IvfPqScanArgs& a, hipStream_t stream) {
   int G, nt;
   bool static_lds = true;  // specialised shapes size their LDS at compile time
   if (a.M == 16 && a.dsub == 8) {
-    fn = pick_scan<16, 8>(R, a.order);
+    fn = pick_scan<16, 8>(R, a.order, a.lut_mode);
     G = ScanShape<16, 8>::GMAX;
     nt = ScanShape<16, 8>::NT;
   } else if (a.M == 32 && a.dsub == 3) {
-    fn = pick_scan<32, 3>(R, a.order);
+    fn = pick_scan<32, 3>(R, a.order, a.lut_mode);
     G = ScanShape<32, 3>::GMAX;
     nt = ScanShape<32, 3>::NT;
   } else {
-    fn = pick_scan<0, 0>(R, a.order);
+    fn = pick_scan<0, 0>(R, a.order, a.lut_mode);
     G = std::max(1, std::min(ScanShape<0, 0>::GMAX, 64 / a.M));
     nt = ScanShape<0, 0>::NT;
     static_lds = false;
@@ -588,6 +632,25 @@ hipError_t launch_ivfpq_scan(const IvfPqScanArgs& a, hipStream_t stream) {
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL(fn, dim3((unsigned)a.nq), dim3(nt), lds, stream, a, G);
+  return hipGetLastError();
+}
+
+namespace {
+__global__ __launch_bounds__(kThreads) void codebook_norms_kernel(const float* __restrict__ cb, int n,
+                                                                  int dsub, float* __restrict__ out) {
+  const int e = blockIdx.x * kThreads + threadIdx.x;
+  if (e >= n) return;
+  float s = 0.0f;
+  for (int t = 0; t < dsub; ++t) s = __builtin_fmaf(cb[(uint64_t)e * dsub + t], cb[(uint64_t)e * dsub + t], s);
+  out[e] = s;
+}
+}  // namespace
+
+hipError_t launch_codebook_norms(const float* codebooks, int M, int dsub, float* out,
+                                 hipStream_t stream) {
+  const int n = M * 256;
+  hipLaunchKernelGGL(codebook_norms_kernel, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0,
+                     stream, codebooks, n, dsub, out);
   return hipGetLastError();
 }
 

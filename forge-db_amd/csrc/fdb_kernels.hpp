@@ -49,12 +49,22 @@ struct IvfPqScanArgs {
   const uint64_t* ids;       // [N], list order
   int k;
   int order;
+  // LUT mode: 0 = exact (the reference's rounding, bit-exact distances);
+  // 1 = fast: T[m][j] = |cb_mj|^2 - 2<r_m, cb_mj> by FMA, with |r|^2 added
+  // once per code (same quantity, different rounding).  Fast mode needs
+  // cbnorm [M][256] = |cb_mj|^2 and the (16,8) or (32,3) shape.
+  int lut_mode;
+  const float* cbnorm;
   uint64_t* out_ids;
   float* out_dists;
   uint32_t* out_pos;  // nullable: list positions of the results
   uint32_t* out_counts;
 };
 hipError_t launch_ivfpq_scan(const IvfPqScanArgs& a, hipStream_t stream);
+
+// |cb_mj|^2 for every codeword: [M*256]
+hipError_t launch_codebook_norms(const float* codebooks, int M, int dsub, float* out,
+                                 hipStream_t stream);
 
 // Nearest row (first minimum) for each of n points, reference order; used for
 // k-means assignment and list assignment at build time.  Same layout rules

@@ -37,8 +37,10 @@ EXPORTED_SYMBOLS = (
     "fdb_ivfpq_describe", "fdb_ivfpq_export", "fdb_ivfpq_enable_reranking",
     "fdb_ivfpq_search", "fdb_ivfpq_batch_search", "fdb_ivfpq_batch_search_device",
     "fdb_ivfpq_sync", "fdb_ivfpq_probe", "fdb_ivfpq_encode",
-    "fdb_ivfpq_batch_search_device_timed",
+    "fdb_ivfpq_batch_search_device_timed", "fdb_ivfpq_set_lut_mode", "fdb_ivfpq_lut_mode",
 )
+
+LUT_EXACT, LUT_FAST = 0, 1
 
 
 class DistanceMetric(enum.IntEnum):
@@ -107,6 +109,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fdb_ivfpq_sync": [_P, _P],
         "fdb_ivfpq_probe": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, _P, _P],
         "fdb_ivfpq_encode": [_P, _P, C.c_uint64, C.c_uint32, _P],
+        "fdb_ivfpq_set_lut_mode": [_P, C.c_uint32],
     }
     for name, args in sig.items():
         f = getattr(lib, name)
@@ -118,6 +121,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
     lib.fdb_ivfpq_set_nprobe.restype = None
     lib.fdb_ivfpq_nprobe.argtypes = [_P]
     lib.fdb_ivfpq_nprobe.restype = C.c_uint64
+    lib.fdb_ivfpq_lut_mode.argtypes = [_P]
+    lib.fdb_ivfpq_lut_mode.restype = C.c_uint32
     _lib_handle = lib
     return lib
 
@@ -217,6 +222,13 @@ class IVFPQIndex:
 
     def nprobe(self) -> int:
         return int(self._lib.fdb_ivfpq_nprobe(self._h))
+
+    def set_lut_mode(self, mode: int) -> None:
+        """LUT_EXACT (default, bit-identical distances) or LUT_FAST."""
+        _check(self._lib, self._lib.fdb_ivfpq_set_lut_mode(self._h, int(mode)))
+
+    def lut_mode(self) -> int:
+        return int(self._lib.fdb_ivfpq_lut_mode(self._h))
 
     def dim(self) -> int:
         return self._dim

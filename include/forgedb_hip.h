@@ -112,6 +112,18 @@ FDB_API uint64_t fdb_ivfpq_nprobe(const fdb_ivfpq* index);
 
 FDB_API fdb_status fdb_ivfpq_describe(const fdb_ivfpq* index, fdb_ivfpq_desc* out);
 
+/* Lookup-table mode (no counterpart in the reference, whose CPU path has one
+ * way of building tables):
+ *   FDB_LUT_EXACT (default) builds T[m][j] = |r_m - cb_mj|^2 with the
+ *     reference's operation order, so ADC distances are bit-identical;
+ *   FDB_LUT_FAST builds |cb_mj|^2 - 2<r_m, cb_mj> by FMA and adds |r|^2 once
+ *     per code: the same quantity within ~1e-6 relative, ~3x fewer table
+ *     operations.  Available for 16 x 8 and 32 x 3 subvector shapes
+ *     (FDB_ERR_UNSUPPORTED otherwise).  Relaxed atomic, like set_nprobe. */
+enum { FDB_LUT_EXACT = 0, FDB_LUT_FAST = 1 };
+FDB_API fdb_status fdb_ivfpq_set_lut_mode(fdb_ivfpq* index, uint32_t mode);
+FDB_API uint32_t fdb_ivfpq_lut_mode(const fdb_ivfpq* index);
+
 /* Copies the resident artifacts back (any pointer may be NULL). */
 FDB_API fdb_status fdb_ivfpq_export(const fdb_ivfpq* index, float* centroids, float* codebooks,
                                     uint64_t* list_offsets, uint64_t* ids, uint8_t* codes);

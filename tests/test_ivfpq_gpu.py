@@ -207,3 +207,47 @@ def test_save_load_roundtrip(small_ivfpq):
         with pytest.raises(ForgeDbError) as e:
             IVFPQIndex.load(p)
         assert e.value.kind == "ChecksumMismatch"
+
+
+@pytest.mark.parametrize("shape", ["16x8", "32x3"])
+def test_fast_lut_within_tolerance(small_ivfpq, shape):
+    """Fast LUTs compute |cb|^2 - 2<r, cb> + |r|^2: distances within 1e-4
+    relative of the oracle (the north_star bound), ids equal except where
+    distances tie within that tolerance."""
+    print(f"fast LUT tolerance {shape}", flush=True)
+    from conftest import tie_aware_match
+    from forgedb import LUT_FAST
+    if shape == "16x8":
+        art, ox, q = small_ivfpq["art"], small_ivfpq["oracle"], small_ivfpq["queries"]
+    else:
+        base, q = datagen.workload("ivfpq_large", n=20_000, nq=48)
+        ox = refcpu.IvfPq.build(base, nlist=64, M=32, seed=2)
+        art = ox.export()
+    gx = gpu_index(art)
+    gx.set_lut_mode(LUT_FAST)
+    assert gx.lut_mode() == LUT_FAST
+    worst = 0.0
+    for nprobe, k in ((1, 10), (8, 10), (16, 100)):
+        gx.set_nprobe(nprobe)
+        ox.set_nprobe(nprobe)
+        gi, gd, gc = gx.batch_search_arrays(q, k)
+        oi, od, oc = ox.batch_search(q, k)
+        assert np.array_equal(gc, oc.astype(np.uint32))
+        for t in range(len(q)):
+            c = int(oc[t])
+            rel = np.abs(gd[t, :c].astype(np.float64) - od[t, :c]) / np.maximum(np.abs(od[t, :c]), 1e-30)
+            worst = max(worst, float(rel.max()))
+            ok, msg = tie_aware_match(gi[t, :c], gd[t, :c], oi[t, :c], od[t, :c], rel=1e-4)
+            assert ok, f"np{nprobe} k{k} q{t}: {msg}"
+    print(f"worst relative distance error {worst:.3g}")
+    assert worst < 1e-4
+
+
+def test_fast_lut_unsupported_shape():
+    base = datagen.gaussian_mixture(3, 4, 3000, 16, ncomp=8)
+    ox = refcpu.IvfPq.build(base, nlist=8, M=4, seed=0)
+    gx = gpu_index(ox.export())
+    with pytest.raises(ForgeDbError) as e:
+        gx.set_lut_mode(1)
+    assert e.value.kind == "Unsupported"
+    assert gx.lut_mode() == 0
