@@ -436,7 +436,13 @@ struct ScanShape {
 };
 template <>
 struct ScanShape<16, 8> {
-  static constexpr int NT = 512, U = 4, GMAX = 3;
+#ifndef FDB_SCAN168_SHAPE
+  // measured on the 1M x 128 / nprobe 16 workload against NT 256-1024,
+  // U 1-8, G 1-4: two 16 KiB tables per group keeps 3 workgroups per CU
+  static constexpr int NT = 512, U = 2, GMAX = 2;
+#else
+  static constexpr int NT = FDB_SCAN168_NT, U = FDB_SCAN168_U, GMAX = FDB_SCAN168_G;
+#endif
 };
 template <>
 struct ScanShape<32, 3> {
