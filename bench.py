@@ -69,6 +69,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target wall time of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one plain 1 GiB device-to-device copy (a known-size "
+                         "reference for the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -98,6 +101,15 @@ def main():
     cnt_d = torch.empty(nq, dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
     sptr = stream.cuda_stream
+    if args.calibrate_copy:
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        src.fill_(1.0)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log("[bench] calibration copy: 1 GiB device to device")
 
     def step():
         index.batch_search_device(q_d.data_ptr(), nq, k, ids_d.data_ptr(), dist_d.data_ptr(),

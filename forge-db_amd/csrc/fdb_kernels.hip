@@ -272,7 +272,10 @@ __device__ __forceinline__ void scan_group(const float* __restrict__ lut, const 
 // NT threads; U code batches in flight per wave; at most GMAX lists per LUT
 // group (G <= GMAX at run time).
 template <int MT, int DT, int R, int ORDER, int NT, int U, int GMAX, int FAST>
-__global__ __launch_bounds__(NT) void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
+// At most 64 VGPRs for R <= 2: 8 waves per SIMD, so four 512-thread
+// workgroups (2 x 16 KiB LUTs each) fill a CU.
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(R <= 2 ? 8 : 1, 8)))
+void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
   static_assert(!FAST || MT > 0, "fast LUT mode needs a specialised shape");
   constexpr int NW = NT / 64;
   // static LDS holds the LUTs + residuals, and later the wave-list merge
