@@ -5,6 +5,7 @@
 #include <cstring>
 #include <string>
 
+#include "fdb_flat.hpp"
 #include "fdb_format.hpp"
 #include "fdb_host.hpp"
 #include "fdb_ivfpq.hpp"
@@ -12,6 +13,12 @@
 
 struct fdb_ivfpq {
   fdb::IvfPqIndex* impl;
+};
+struct fdb_bf {
+  fdb::BruteForceIndex* impl;
+};
+struct fdb_ivf {
+  fdb::IvfFlatIndex* impl;
 };
 
 namespace fdb {
@@ -65,6 +72,12 @@ fdb::IvfPqIndex* H(fdb_ivfpq* h) {
   return h->impl;
 }
 const fdb::IvfPqIndex* H(const fdb_ivfpq* h) {
+  if (!h || !h->impl) throw Error(FDB_ERR_INVALID_ARGUMENT, "null index handle");
+  return h->impl;
+}
+
+template <class Handle>
+auto* impl_of(Handle* h) {
   if (!h || !h->impl) throw Error(FDB_ERR_INVALID_ARGUMENT, "null index handle");
   return h->impl;
 }
@@ -278,6 +291,215 @@ fdb_status fdb_ivfpq_encode(fdb_ivfpq* h, const float* residuals, uint64_t nq, u
     if (nq && (!residuals || !out_codes)) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
     if (dim != ix->dim()) throw Error(FDB_ERR_DIMENSION_MISMATCH, "vector dimension does not match the index");
     ix->encode(residuals, nq, out_codes);
+  });
+}
+
+/* ---- brute force ---------------------------------------------------------- */
+
+fdb_status fdb_bf_create(uint32_t metric, fdb_bf** out) {
+  return guarded([&] {
+    if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (metric > 4) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown metric");
+    require_device();
+    auto* impl = new BruteForceIndex(metric);
+    *out = new fdb_bf{impl};
+  });
+}
+
+fdb_status fdb_bf_add(fdb_bf* h, const float* rows, const uint64_t* ids, uint64_t n, uint32_t dim) {
+  return guarded([&] { impl_of(h)->add(rows, ids, n, dim); });
+}
+
+fdb_status fdb_bf_remove(fdb_bf* h, uint64_t id, int* removed) {
+  return guarded([&] {
+    const bool r = impl_of(h)->remove(id);
+    if (removed) *removed = r ? 1 : 0;
+  });
+}
+
+uint64_t fdb_bf_len(const fdb_bf* h) { return (h && h->impl) ? h->impl->size() : 0; }
+uint32_t fdb_bf_dimension(const fdb_bf* h) { return (h && h->impl) ? h->impl->dim() : 0; }
+uint32_t fdb_bf_metric(const fdb_bf* h) { return (h && h->impl) ? h->impl->metric() : 0; }
+
+fdb_status fdb_bf_load(const char* path, fdb_bf** out) {
+  return guarded([&] {
+    if (!out || !path) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    std::vector<uint8_t> file;
+    IoResult r = read_file(path, file);
+    if (r.status) throw Error(r.status, r.message);
+    size_t off = 0;
+    r = verify_header(file, IndexType::BruteForce, off);
+    if (r.status) throw Error(r.status, r.message);
+    BruteForceArtifacts a;
+    r = decode_bf(file.data() + off, file.size() - off, a);
+    if (r.status) throw Error(r.status, r.message);
+    if (a.dim > 0xFFFFFFFFull) throw Error(FDB_ERR_UNSUPPORTED, "dimension above 2^32");
+    require_device();
+    auto* impl = new BruteForceIndex(a.metric);
+    try {
+      if (a.n) impl->add(a.data.data(), a.ids.data(), a.n, (uint32_t)a.dim);
+    } catch (...) {
+      delete impl;
+      throw;
+    }
+    *out = new fdb_bf{impl};
+  });
+}
+
+fdb_status fdb_bf_save(const fdb_bf* h, const char* path) {
+  return guarded([&] {
+    if (!path) throw Error(FDB_ERR_INVALID_ARGUMENT, "null path");
+    const BruteForceIndex* ix = impl_of(h);
+    BruteForceArtifacts a;
+    a.metric = ix->metric();
+    a.n = ix->size();
+    a.dim = ix->dim();
+    a.ids = ix->ids();
+    a.data = ix->rows();
+    IoResult r = write_file(path, IndexType::BruteForce, encode_bf(a));
+    if (r.status) throw Error(r.status, r.message);
+  });
+}
+
+void fdb_bf_destroy(fdb_bf* h) {
+  if (!h) return;
+  delete h->impl;
+  delete h;
+}
+
+fdb_status fdb_bf_export(const fdb_bf* h, float* rows, uint64_t* ids) {
+  return guarded([&] {
+    const BruteForceIndex* ix = impl_of(h);
+    if (rows) std::memcpy(rows, ix->rows().data(), 4 * ix->rows().size());
+    if (ids) std::memcpy(ids, ix->ids().data(), 8 * ix->ids().size());
+  });
+}
+
+fdb_status fdb_bf_search(fdb_bf* h, const float* query, uint32_t dim, uint32_t k, uint64_t* out_ids,
+                         float* out_dists, uint32_t* out_count) {
+  return guarded([&] {
+    BruteForceIndex* ix = impl_of(h);
+    if (!query || !out_count || (k && (!out_ids || !out_dists)))
+      throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (ix->size() && dim != ix->dim())
+      throw Error(FDB_ERR_DIMENSION_MISMATCH, "query dimension does not match the index");
+    if (!ix->size()) {
+      *out_count = 0;
+      return;
+    }
+    *out_count = ix->search(query, k, out_ids, out_dists);
+  });
+}
+
+fdb_status fdb_bf_batch_search(fdb_bf* h, const float* queries, uint64_t nq, uint32_t dim, uint32_t k,
+                               uint64_t* out_ids, float* out_dists, uint32_t* out_counts) {
+  return guarded([&] {
+    BruteForceIndex* ix = impl_of(h);
+    if (nq && (!queries || !out_counts || (k && (!out_ids || !out_dists))))
+      throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (ix->size() && dim != ix->dim())
+      throw Error(FDB_ERR_DIMENSION_MISMATCH, "query dimension does not match the index");
+    if (!ix->size()) {
+      for (uint64_t q = 0; q < nq; ++q) {
+        out_counts[q] = 0;
+        for (uint32_t j = 0; j < k; ++j) {
+          out_ids[q * k + j] = ~0ull;
+          out_dists[q * k + j] = HUGE_VALF;
+        }
+      }
+      return;
+    }
+    ix->batch_search(queries, nq, k, out_ids, out_dists, out_counts);
+  });
+}
+
+fdb_status fdb_bf_batch_search_device(fdb_bf* h, const float* d_queries, uint64_t nq, uint32_t k,
+                                      uint64_t* d_out_ids, float* d_out_dists, uint32_t* d_out_counts,
+                                      void* stream, float* ms) {
+  return guarded([&] {
+    impl_of(h)->batch_search_device(d_queries, nq, k, d_out_ids, d_out_dists, d_out_counts,
+                                    (hipStream_t)stream, ms);
+  });
+}
+
+/* ---- IVF ------------------------------------------------------------------ */
+
+fdb_status fdb_ivf_create(const float* centroids, uint32_t nlist, uint32_t dim,
+                          const uint64_t* list_offsets, const uint64_t* ids, const float* rows,
+                          uint32_t metric, fdb_ivf** out) {
+  return guarded([&] {
+    if (!out || !centroids || !list_offsets) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    require_device();
+    auto* impl = new IvfFlatIndex(centroids, nlist, dim, list_offsets, ids, rows, metric);
+    *out = new fdb_ivf{impl};
+  });
+}
+
+fdb_status fdb_ivf_build(const float* vectors, const uint64_t* ids, uint64_t n, uint32_t dim,
+                         uint32_t n_clusters, uint32_t metric, uint64_t seed, fdb_ivf** out) {
+  return guarded([&] {
+    if (!out || !vectors) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (metric > 4) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown metric");
+    require_device();
+    auto* impl = IvfFlatIndex::build(vectors, ids, n, dim, n_clusters, metric, 100, seed);
+    *out = new fdb_ivf{impl};
+  });
+}
+
+void fdb_ivf_destroy(fdb_ivf* h) {
+  if (!h) return;
+  delete h->impl;
+  delete h;
+}
+
+void fdb_ivf_set_nprobe(fdb_ivf* h, uint64_t nprobe) {
+  if (h && h->impl) h->impl->set_nprobe(nprobe);
+}
+uint64_t fdb_ivf_nprobe(const fdb_ivf* h) { return (h && h->impl) ? h->impl->nprobe() : 0; }
+uint64_t fdb_ivf_len(const fdb_ivf* h) { return (h && h->impl) ? h->impl->size() : 0; }
+uint32_t fdb_ivf_num_partitions(const fdb_ivf* h) { return (h && h->impl) ? h->impl->nlist() : 0; }
+uint32_t fdb_ivf_dimension(const fdb_ivf* h) { return (h && h->impl) ? h->impl->dim() : 0; }
+
+fdb_status fdb_ivf_export(const fdb_ivf* h, float* centroids, uint64_t* list_offsets, uint64_t* ids,
+                          float* rows) {
+  return guarded([&] { impl_of(h)->export_to(centroids, list_offsets, ids, rows); });
+}
+
+fdb_status fdb_ivf_search(fdb_ivf* h, const float* query, uint32_t dim, uint32_t k, uint64_t* out_ids,
+                          float* out_dists, uint32_t* out_count) {
+  return guarded([&] {
+    IvfFlatIndex* ix = impl_of(h);
+    if (!query || !out_count || (k && (!out_ids || !out_dists)))
+      throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (dim != ix->dim()) throw Error(FDB_ERR_DIMENSION_MISMATCH, "query dimension does not match the index");
+    ix->batch_search(query, 1, k, out_ids, out_dists, out_count);
+  });
+}
+
+fdb_status fdb_ivf_batch_search(fdb_ivf* h, const float* queries, uint64_t nq, uint32_t dim, uint32_t k,
+                                uint64_t* out_ids, float* out_dists, uint32_t* out_counts) {
+  return guarded([&] {
+    IvfFlatIndex* ix = impl_of(h);
+    if (nq && (!queries || !out_counts || (k && (!out_ids || !out_dists))))
+      throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (dim != ix->dim()) throw Error(FDB_ERR_DIMENSION_MISMATCH, "query dimension does not match the index");
+    ix->batch_search(queries, nq, k, out_ids, out_dists, out_counts);
+  });
+}
+
+fdb_status fdb_ivf_batch_search_device(fdb_ivf* h, const float* d_queries, uint64_t nq, uint32_t k,
+                                       uint64_t* d_out_ids, float* d_out_dists, uint32_t* d_out_counts,
+                                       void* stream, float* coarse_ms, float* scan_ms) {
+  return guarded([&] {
+    impl_of(h)->batch_search_device(d_queries, nq, k, d_out_ids, d_out_dists, d_out_counts,
+                                    (hipStream_t)stream, coarse_ms, scan_ms);
+  });
+}
+
+fdb_status fdb_ivf_sync(fdb_ivf* h, void* stream) {
+  return guarded([&] {
+    if (impl_of(h)->sync((hipStream_t)stream))
+      throw Error(FDB_ERR_NAN, "NaN centroid distance (a query contains NaN)");
   });
 }
 

@@ -1,0 +1,174 @@
+// Full-precision (uncompressed) search: BruteForceIndex (src/index/brute_force.rs)
+// and IVFIndex (src/index/ivf.rs) on the GPU.
+#pragma once
+
+#include <atomic>
+#include <mutex>
+#include <vector>
+
+#include "fdb_host.hpp"
+
+namespace fdb {
+
+// ---- kernels (fdb_flat.hip) ----------------------------------------------
+
+// Row-major rows [n][dim] -> dim-major, rows permuted like centT:
+// out[prow(d) * ld + r] (ld >= n, multiple of 4; padding is zero).
+hipError_t launch_transpose_rows(const float* rows, uint64_t n, int dim, uint64_t ld, float* out,
+                                 hipStream_t s);
+// Reference-order sum of squares (the norms of cosine_distance_avx2,
+// simd.rs:466-507) of n row-major vectors.
+hipError_t launch_row_norms(const float* rows, uint64_t n, int dim, float* out, hipStream_t s);
+
+// Brute-force partial top-k: queries [nq][dim]; data [dim][ld] permuted;
+// rows [0, n) cut into chunks of chunk_rows; writes per (query, chunk) the k
+// smallest (distance, row) pairs into part [nq][nchunks][k].
+struct FlatTopkArgs {
+  const float* queries;
+  uint64_t nq;
+  int dim;
+  const float* dataT;
+  uint64_t ld, n;
+  const float* row_norm;  // cosine only
+  const float* q_norm;    // cosine only
+  uint64_t chunk_rows;
+  uint32_t nchunks;
+  int metric;
+  int k;
+  float* part_d;
+  uint32_t* part_key;
+};
+hipError_t launch_flat_topk(const FlatTopkArgs& a, hipStream_t s);
+
+// Merge [nq][nparts][k] partial lists into [nq][k] ascending (ties: smaller
+// key), keys mapped to ids through ids (nullable: keys are the ids).
+hipError_t launch_merge_parts(const float* part_d, const uint32_t* part_key, uint64_t nq,
+                              uint32_t nparts, int k, const uint64_t* ids, uint64_t* out_ids,
+                              float* out_d, uint32_t* out_counts, hipStream_t s);
+
+// IVF-flat scan: per query, probes [nq][np] lists of list-blocked data
+// (list p: block [dim][lld_p] at boff[p] floats, rows start at row_off[p]).
+struct IvfFlatScanArgs {
+  const float* queries;
+  uint64_t nq;
+  int dim;
+  const int32_t* probes;
+  int np;
+  int nlist;
+  const float* data;         // list blocks
+  const uint64_t* boff;      // [nlist] float offset of each list block
+  const uint32_t* row_off;   // [nlist+1] row offsets (list order)
+  const float* row_norm;     // cosine: [N] in list order
+  const float* q_norm;       // cosine: [nq]
+  const uint64_t* ids;       // [N] list order
+  int metric;
+  int k;
+  uint64_t* out_ids;
+  float* out_d;
+  uint32_t* out_counts;
+};
+hipError_t launch_ivf_flat_scan(const IvfFlatScanArgs& a, hipStream_t s);
+
+// ---- BruteForceIndex ------------------------------------------------------
+
+class BruteForceIndex {
+ public:
+  // BruteForceIndex::new (brute_force.rs:67): empty, dimension set by the
+  // first add.
+  explicit BruteForceIndex(uint32_t metric);
+  ~BruteForceIndex();
+  uint64_t size() const { return h_ids_.size(); }
+  uint32_t dim() const { return h_ids_.empty() ? 0 : dim_; }
+  uint32_t metric() const { return metric_; }
+  const std::vector<float>& rows() const { return h_rows_; }
+  const std::vector<uint64_t>& ids() const { return h_ids_; }
+
+  // add (brute_force.rs:75 / MutableVectorIndex::add :254-265): appends n
+  // rows [n][dim] with ids (nullable: ids continue from size()).
+  void add(const float* rows, const uint64_t* ids, uint64_t n, uint32_t dim);
+  // MutableVectorIndex::remove (:267-274): the first row with this id is
+  // replaced by the last row (VectorStore::swap_remove, vector.rs:256-270).
+  bool remove(uint64_t id);
+
+  // search / search_parallel (brute_force.rs:162-214): one query
+  uint32_t search(const float* q, uint32_t k, uint64_t* ids, float* dists);
+  // batch_search (brute_force.rs:220-225)
+  void batch_search(const float* qs, uint64_t nq, uint32_t k, uint64_t* ids, float* dists,
+                    uint32_t* counts);
+  void batch_search_device(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids,
+                           float* d_dists, uint32_t* d_counts, hipStream_t s, float* ms = nullptr);
+
+ private:
+  void sync_device();  // re-uploads the rows after add/remove (caller holds mu_)
+  void run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids, float* d_dists,
+           uint32_t* d_counts, hipStream_t s);
+
+  uint32_t dim_ = 0, metric_;
+  std::vector<float> h_rows_;
+  std::vector<uint64_t> h_ids_;
+  bool dirty_ = false;
+  uint64_t n_dev_ = 0;  // rows resident on the device
+  hipStream_t stream_ = nullptr;
+  std::mutex mu_;
+  DevBuf<float> dataT_, row_norm_;
+  DevBuf<uint64_t> ids_;
+  uint64_t ld_ = 0;
+  // scratch
+  DevBuf<float> q_, qn_, part_d_, out_d_;
+  DevBuf<uint32_t> part_k_, out_c_;
+  DevBuf<uint64_t> out_i_;
+  hipEvent_t ev_[2] = {nullptr, nullptr};
+};
+
+// ---- IVFIndex ---------------------------------------------------------------
+
+class IvfFlatIndex {
+ public:
+  // centroids [nlist][dim]; lists in CSR over rows [N][dim] (list order), ids
+  IvfFlatIndex(const float* centroids, uint32_t nlist, uint32_t dim, const uint64_t* offsets,
+               const uint64_t* ids, const float* rows, uint32_t metric);
+  ~IvfFlatIndex();
+  // IVFIndex::build (ivf.rs:91-119) on the GPU with a seeded k-means
+  static IvfFlatIndex* build(const float* vectors, const uint64_t* ids, uint64_t n, uint32_t dim,
+                             uint32_t nlist, uint32_t metric, uint32_t max_iters, uint64_t seed);
+
+  uint32_t nlist() const { return nlist_; }
+  uint32_t metric() const { return metric_; }
+  uint32_t dim() const { return dim_; }
+  uint64_t size() const { return h_ids_.size(); }
+  void set_nprobe(uint64_t np) { nprobe_.store(np < nlist_ ? np : nlist_, std::memory_order_relaxed); }
+  uint64_t nprobe() const { return nprobe_.load(std::memory_order_relaxed); }
+  void export_to(float* centroids, uint64_t* offsets, uint64_t* ids, float* rows) const;
+
+  // search (ivf.rs:162-216) and batch_search (ivf.rs:292-297)
+  void batch_search(const float* qs, uint64_t nq, uint32_t k, uint64_t* ids, float* dists,
+                    uint32_t* counts);
+  void batch_search_device(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids,
+                           float* d_dists, uint32_t* d_counts, hipStream_t s, float* coarse_ms = nullptr,
+                           float* scan_ms = nullptr);
+  // waits for s (null: own stream); true if a device search saw a NaN since
+  // the last sync (the flag is cleared)
+  bool sync(hipStream_t s);
+
+ private:
+  void run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids, float* d_dists,
+           uint32_t* d_counts, hipStream_t s, float* coarse_ms, float* scan_ms);
+
+  uint32_t nlist_, dim_, metric_;
+  std::atomic<uint64_t> nprobe_{1};
+  std::vector<float> h_centroids_, h_rows_;
+  std::vector<uint64_t> h_offsets_, h_ids_;
+  hipStream_t stream_ = nullptr;
+  std::mutex mu_;
+  DevBuf<float> centT_, data_, row_norm_;
+  DevBuf<uint64_t> boff_, ids_;
+  DevBuf<uint32_t> row_off_;
+  DevBuf<float> q_, qn_, out_d_;
+  DevBuf<int32_t> probes_;
+  DevBuf<uint64_t> out_i_;
+  DevBuf<uint32_t> out_c_;
+  DevBuf<int> err_;
+  hipEvent_t ev_[3] = {nullptr, nullptr, nullptr};
+};
+
+}  // namespace fdb

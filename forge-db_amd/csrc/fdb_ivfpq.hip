@@ -110,6 +110,8 @@ hipError_t launch_rerank(const float* queries, uint64_t nq, int dim, const float
 
 unsigned blocks_for(uint64_t n, unsigned t) { return (unsigned)((n + t - 1) / t); }
 
+}  // namespace
+
 // Members of each cluster in ascending point order (a stable counting sort).
 void group_members(const std::vector<int32_t>& assign, int k, std::vector<uint32_t>& off,
                    std::vector<uint32_t>& members) {
@@ -202,8 +204,6 @@ std::vector<float> kmeans_gpu(const float* h_points, uint64_t n, int dim, int k,
   }
   return cents;
 }
-
-}  // namespace
 
 IvfPqIndex::IvfPqIndex(IvfPqArtifacts&& art) : host_(std::move(art)) {
   nprobe_.store(std::min<uint64_t>(host_.nprobe, host_.nlist), std::memory_order_relaxed);

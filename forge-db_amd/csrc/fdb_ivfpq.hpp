@@ -77,4 +77,9 @@ class IvfPqIndex {
   hipEvent_t ev_[3] = {nullptr, nullptr, nullptr};
 };
 
+// Seeded k-means over n host rows [n][dim] (KMeans::fit_raw, kmeans.rs:87-193):
+// k centroids [k][dim] after at most max_iters Lloyd steps on the GPU.
+std::vector<float> kmeans_gpu(const float* h_points, uint64_t n, int dim, int k, int max_iters,
+                              uint64_t seed, hipStream_t s);
+
 }  // namespace fdb

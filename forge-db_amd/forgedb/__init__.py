@@ -7,6 +7,10 @@ the reference's Rust API:
 * ``IVFPQIndex``  — src/index/ivf_pq.rs: ``build``, ``set_nprobe``/``nprobe``,
   ``search``, ``batch_search``, ``batch_search_parallel``, ``save``/``load``,
   ``enable_reranking``.
+* ``BruteForceIndex`` — src/index/brute_force.rs: ``new``/``add``/``remove``,
+  ``search``, ``search_parallel``, ``batch_search``, ``save``/``load``.
+* ``IVFIndex`` — src/index/ivf.rs: ``build``, ``set_nprobe``/``nprobe``,
+  ``search``, ``search_parallel``, ``batch_search``, ``batch_search_optimized``.
 * ``DistanceMetric`` — src/distance/mod.rs:17-32.
 
 There is no CPU fallback: when the HIP library is absent, importing works but
@@ -25,7 +29,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libforgedb_hip.so")
 
 __all__ = [
-    "DistanceMetric", "ForgeDbError", "IVFPQIndex", "load_library", "LIB_PATH",
+    "DistanceMetric", "ForgeDbError", "IVFPQIndex", "BruteForceIndex", "IVFIndex",
+    "load_library", "LIB_PATH",
     "EXPORTED_SYMBOLS",
 ]
 
@@ -38,6 +43,12 @@ EXPORTED_SYMBOLS = (
     "fdb_ivfpq_search", "fdb_ivfpq_batch_search", "fdb_ivfpq_batch_search_device",
     "fdb_ivfpq_sync", "fdb_ivfpq_probe", "fdb_ivfpq_encode",
     "fdb_ivfpq_batch_search_device_timed", "fdb_ivfpq_set_lut_mode", "fdb_ivfpq_lut_mode",
+    "fdb_bf_create", "fdb_bf_add", "fdb_bf_remove", "fdb_bf_len", "fdb_bf_dimension",
+    "fdb_bf_metric", "fdb_bf_load", "fdb_bf_save", "fdb_bf_destroy", "fdb_bf_export",
+    "fdb_bf_search", "fdb_bf_batch_search", "fdb_bf_batch_search_device",
+    "fdb_ivf_create", "fdb_ivf_build", "fdb_ivf_destroy", "fdb_ivf_set_nprobe", "fdb_ivf_nprobe",
+    "fdb_ivf_len", "fdb_ivf_num_partitions", "fdb_ivf_dimension", "fdb_ivf_export",
+    "fdb_ivf_search", "fdb_ivf_batch_search", "fdb_ivf_batch_search_device", "fdb_ivf_sync",
 )
 
 LUT_EXACT, LUT_FAST = 0, 1
@@ -110,6 +121,22 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fdb_ivfpq_probe": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, _P, _P],
         "fdb_ivfpq_encode": [_P, _P, C.c_uint64, C.c_uint32, _P],
         "fdb_ivfpq_set_lut_mode": [_P, C.c_uint32],
+        "fdb_bf_create": [C.c_uint32, _P],
+        "fdb_bf_add": [_P, _P, _P, C.c_uint64, C.c_uint32],
+        "fdb_bf_remove": [_P, C.c_uint64, _P],
+        "fdb_bf_load": [C.c_char_p, _P],
+        "fdb_bf_save": [_P, C.c_char_p],
+        "fdb_bf_export": [_P, _P, _P],
+        "fdb_bf_search": [_P, _P, C.c_uint32, C.c_uint32, _P, _P, _P],
+        "fdb_bf_batch_search": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, _P, _P, _P],
+        "fdb_bf_batch_search_device": [_P, _P, C.c_uint64, C.c_uint32, _P, _P, _P, _P, _P],
+        "fdb_ivf_create": [_P, C.c_uint32, C.c_uint32, _P, _P, _P, C.c_uint32, _P],
+        "fdb_ivf_build": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, _P],
+        "fdb_ivf_export": [_P, _P, _P, _P, _P],
+        "fdb_ivf_search": [_P, _P, C.c_uint32, C.c_uint32, _P, _P, _P],
+        "fdb_ivf_batch_search": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, _P, _P, _P],
+        "fdb_ivf_batch_search_device": [_P, _P, C.c_uint64, C.c_uint32, _P, _P, _P, _P, _P, _P],
+        "fdb_ivf_sync": [_P, _P],
     }
     for name, args in sig.items():
         f = getattr(lib, name)
@@ -123,6 +150,16 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
     lib.fdb_ivfpq_nprobe.restype = C.c_uint64
     lib.fdb_ivfpq_lut_mode.argtypes = [_P]
     lib.fdb_ivfpq_lut_mode.restype = C.c_uint32
+    for name, res in (("fdb_bf_destroy", None), ("fdb_bf_len", C.c_uint64),
+                      ("fdb_bf_dimension", C.c_uint32), ("fdb_bf_metric", C.c_uint32),
+                      ("fdb_ivf_destroy", None), ("fdb_ivf_nprobe", C.c_uint64),
+                      ("fdb_ivf_len", C.c_uint64), ("fdb_ivf_num_partitions", C.c_uint32),
+                      ("fdb_ivf_dimension", C.c_uint32)):
+        f = getattr(lib, name)
+        f.argtypes = [_P]
+        f.restype = res
+    lib.fdb_ivf_set_nprobe.argtypes = [_P, C.c_uint64]
+    lib.fdb_ivf_set_nprobe.restype = None
     _lib_handle = lib
     return lib
 
@@ -335,3 +372,247 @@ class IVFPQIndex:
         codes = np.empty((nq, self.n_subvectors), np.uint8)
         _check(self._lib, self._lib.fdb_ivfpq_encode(self._h, _ptr(r), nq, r.shape[1], _ptr(codes)))
         return codes
+
+
+def _search_one(fn, h, query, k: int):
+    q = _f32(query).reshape(-1)
+    ids = np.empty(max(k, 1), np.uint64)
+    d = np.empty(max(k, 1), np.float32)
+    cnt = C.c_uint32()
+    _check(load_library(), fn(h, _ptr(q), q.shape[0], k, _ptr(ids), _ptr(d), C.byref(cnt)))
+    return [(int(ids[j]), float(d[j])) for j in range(cnt.value)]
+
+
+def _search_batch(fn, h, queries, k: int):
+    q = _f32(queries)
+    if q.ndim != 2:
+        raise ForgeDbError(-1, "queries must be [nq, dim]")
+    nq = q.shape[0]
+    ids = np.empty((nq, max(k, 1)), np.uint64)
+    d = np.empty((nq, max(k, 1)), np.float32)
+    counts = np.empty(nq, np.uint32)
+    _check(load_library(), fn(h, _ptr(q), nq, q.shape[1], k, _ptr(ids), _ptr(d), _ptr(counts)))
+    return ids[:, :k], d[:, :k], counts
+
+
+def _query_rows(queries) -> np.ndarray:
+    """Accepts [nq, dim] arrays or a sequence of vectors (or objects with .data)."""
+    if isinstance(queries, np.ndarray):
+        return queries
+    return np.asarray([getattr(q, "data", q) for q in queries], np.float32)
+
+
+class BruteForceIndex:
+    """Exact search over all rows in HBM — src/index/brute_force.rs:60-225.
+
+    Distances are bit-identical to DistanceMetric::compute; equal distances
+    keep the earlier row first.
+    """
+
+    def __init__(self, metric: DistanceMetric = DistanceMetric.Euclidean, _handle: int = 0):
+        self._lib = load_library()
+        if _handle:
+            self._h = C.c_void_p(_handle)
+        else:
+            out = C.c_void_p()
+            _check(self._lib, self._lib.fdb_bf_create(int(metric), C.byref(out)))
+            self._h = out
+        self.metric = DistanceMetric(int(self._lib.fdb_bf_metric(self._h)))
+
+    new = classmethod(lambda cls, metric: cls(metric))  # BruteForceIndex::new (:67)
+
+    @classmethod
+    def from_arrays(cls, rows, ids=None, metric: DistanceMetric = DistanceMetric.Euclidean):
+        ix = cls(metric)
+        ix.add_batch(rows, ids)
+        return ix
+
+    def add(self, vector_id: int, data) -> None:
+        """add (:75) / MutableVectorIndex::add (:254-265)."""
+        self.add_batch(_f32(data).reshape(1, -1), np.array([vector_id], np.uint64))
+
+    def add_batch(self, rows, ids=None) -> None:
+        r = _f32(rows)
+        idv = None if ids is None else np.ascontiguousarray(ids, np.uint64)
+        _check(self._lib, self._lib.fdb_bf_add(self._h, _ptr(r), _ptr(idv), r.shape[0], r.shape[1]))
+
+    def remove(self, vector_id: int) -> bool:
+        """MutableVectorIndex::remove (:267-274)."""
+        out = C.c_int()
+        _check(self._lib, self._lib.fdb_bf_remove(self._h, int(vector_id), C.byref(out)))
+        return bool(out.value)
+
+    def __len__(self) -> int:
+        return int(self._lib.fdb_bf_len(self._h))
+
+    def is_empty(self) -> bool:
+        return len(self) == 0
+
+    def dimension(self) -> int:
+        return int(self._lib.fdb_bf_dimension(self._h))
+
+    def export(self):
+        n, dim = len(self), self.dimension()
+        rows = np.empty((n, dim), np.float32)
+        ids = np.empty(n, np.uint64)
+        _check(self._lib, self._lib.fdb_bf_export(self._h, _ptr(rows), _ptr(ids)))
+        return rows, ids
+
+    @classmethod
+    def load(cls, path: str) -> "BruteForceIndex":
+        """Persistable::load (:322-385)."""
+        lib = load_library()
+        out = C.c_void_p()
+        _check(lib, lib.fdb_bf_load(os.fsencode(path), C.byref(out)))
+        return cls(_handle=out.value)
+
+    def save(self, path: str) -> None:
+        """Persistable::save (:278-320)."""
+        _check(self._lib, self._lib.fdb_bf_save(self._h, os.fsencode(path)))
+
+    def close(self) -> None:
+        if self._h is not None and self._h.value:
+            self._lib.fdb_bf_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def search(self, query, k: int) -> List[Tuple[int, float]]:
+        """search (:162-166) -> [(id, distance)] ascending."""
+        return _search_one(self._lib.fdb_bf_search, self._h, query, k)
+
+    search_prefetch = search    # :172-174
+    search_parallel = search    # :180-214: one launch covers every chunk
+
+    def batch_search_arrays(self, queries, k: int):
+        return _search_batch(self._lib.fdb_bf_batch_search, self._h, queries, k)
+
+    def batch_search(self, queries, k: int) -> List[List[Tuple[int, float]]]:
+        """batch_search (:220-225)."""
+        if len(queries) == 0:
+            return []
+        return _rows(*self.batch_search_arrays(_query_rows(queries), k))
+
+    def batch_search_device(self, d_queries: int, nq: int, k: int, d_ids: int, d_dists: int,
+                            d_counts: int, stream: int = 0, timed: bool = False):
+        ms = C.c_float()
+        _check(self._lib, self._lib.fdb_bf_batch_search_device(
+            self._h, C.c_void_p(d_queries), nq, k, C.c_void_p(d_ids), C.c_void_p(d_dists),
+            C.c_void_p(d_counts), C.c_void_p(stream), C.byref(ms) if timed else None))
+        return ms.value if timed else None
+
+
+class IVFIndex:
+    """IVF over full vectors in HBM — src/index/ivf.rs:70-405.
+
+    Lists are CSR in list order: ``list_offsets[nlist+1]`` into ``ids[N]`` and
+    ``rows[N, dim]``.
+    """
+
+    def __init__(self, handle: int):
+        self._lib = load_library()
+        self._h = C.c_void_p(handle)
+        self.nlist = int(self._lib.fdb_ivf_num_partitions(self._h))
+        self._dim = int(self._lib.fdb_ivf_dimension(self._h))
+
+    @classmethod
+    def from_artifacts(cls, centroids, list_offsets, ids, rows,
+                       metric: DistanceMetric = DistanceMetric.Euclidean) -> "IVFIndex":
+        lib = load_library()
+        cen = _f32(centroids)
+        off = np.ascontiguousarray(list_offsets, np.uint64)
+        idv = np.ascontiguousarray(ids, np.uint64)
+        r = _f32(rows)
+        out = C.c_void_p()
+        _check(lib, lib.fdb_ivf_create(_ptr(cen), cen.shape[0], cen.shape[1], _ptr(off), _ptr(idv),
+                                       _ptr(r), int(metric), C.byref(out)))
+        ix = cls(out.value)
+        ix.metric = DistanceMetric(int(metric))
+        return ix
+
+    @classmethod
+    def build(cls, vectors, n_clusters: int, metric: DistanceMetric = DistanceMetric.Euclidean,
+              seed: int = 0, ids=None) -> "IVFIndex":
+        """IVFIndex::build (ivf.rs:91-119), on the GPU, seeded."""
+        lib = load_library()
+        v = _f32(vectors)
+        idv = None if ids is None else np.ascontiguousarray(ids, np.uint64)
+        out = C.c_void_p()
+        _check(lib, lib.fdb_ivf_build(_ptr(v), _ptr(idv), v.shape[0], v.shape[1], n_clusters,
+                                      int(metric), seed, C.byref(out)))
+        ix = cls(out.value)
+        ix.metric = DistanceMetric(int(metric))
+        return ix
+
+    def close(self) -> None:
+        if self._h is not None and self._h.value:
+            self._lib.fdb_ivf_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_nprobe(self, nprobe: int) -> None:
+        """set_nprobe (ivf.rs:125-127): min(nprobe, nlist)."""
+        self._lib.fdb_ivf_set_nprobe(self._h, int(nprobe))
+
+    def nprobe(self) -> int:
+        return int(self._lib.fdb_ivf_nprobe(self._h))
+
+    def __len__(self) -> int:
+        return int(self._lib.fdb_ivf_len(self._h))
+
+    def is_empty(self) -> bool:
+        return len(self) == 0
+
+    def num_partitions(self) -> int:
+        return self.nlist
+
+    def dimension(self) -> int:
+        return self._dim
+
+    def export(self) -> dict:
+        n = len(self)
+        out = dict(centroids=np.empty((self.nlist, self._dim), np.float32),
+                   list_offsets=np.empty(self.nlist + 1, np.uint64),
+                   ids=np.empty(n, np.uint64), rows=np.empty((n, self._dim), np.float32))
+        _check(self._lib, self._lib.fdb_ivf_export(self._h, _ptr(out["centroids"]),
+                                                   _ptr(out["list_offsets"]), _ptr(out["ids"]),
+                                                   _ptr(out["rows"])))
+        return out
+
+    def search(self, query, k: int) -> List[Tuple[int, float]]:
+        """search (ivf.rs:162-216)."""
+        return _search_one(self._lib.fdb_ivf_search, self._h, query, k)
+
+    search_parallel = search  # ivf.rs:245-290
+
+    def batch_search_arrays(self, queries, k: int):
+        return _search_batch(self._lib.fdb_ivf_batch_search, self._h, queries, k)
+
+    def batch_search(self, queries, k: int) -> List[List[Tuple[int, float]]]:
+        """batch_search (ivf.rs:292-297)."""
+        if len(queries) == 0:
+            return []
+        return _rows(*self.batch_search_arrays(_query_rows(queries), k))
+
+    batch_search_optimized = batch_search  # ivf.rs:313-405
+
+    def batch_search_device(self, d_queries: int, nq: int, k: int, d_ids: int, d_dists: int,
+                            d_counts: int, stream: int = 0, timed: bool = False):
+        cm, sm = C.c_float(), C.c_float()
+        _check(self._lib, self._lib.fdb_ivf_batch_search_device(
+            self._h, C.c_void_p(d_queries), nq, k, C.c_void_p(d_ids), C.c_void_p(d_dists),
+            C.c_void_p(d_counts), C.c_void_p(stream), C.byref(cm) if timed else None,
+            C.byref(sm) if timed else None))
+        return (cm.value, sm.value) if timed else None
+
+    def sync(self, stream: int = 0) -> None:
+        _check(self._lib, self._lib.fdb_ivf_sync(self._h, C.c_void_p(stream)))

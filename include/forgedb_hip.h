@@ -180,6 +180,100 @@ FDB_API fdb_status fdb_ivfpq_batch_search_device_timed(fdb_ivfpq* index, const f
                                                        uint32_t* d_out_counts, void* hip_stream,
                                                        float* coarse_ms, float* scan_ms);
 
+/* ------------------------------------------------------------------------ */
+/* Brute force: src/index/brute_force.rs                                    */
+/* ------------------------------------------------------------------------ */
+/* Distances are the metric's AVX2 form (src/distance/simd.rs:290-517, via
+ * DistanceMetric::compute, distance/mod.rs:40-48), bit-identical.  Results
+ * are the k smallest, ascending; equal distances keep the earlier row first
+ * (the strict-< heap replacement of scan_range, brute_force.rs:141-146). */
+typedef struct fdb_bf fdb_bf;
+
+/* BruteForceIndex::new (brute_force.rs:67-72): empty; the first add fixes
+ * the dimension. */
+FDB_API fdb_status fdb_bf_create(uint32_t metric, fdb_bf** out);
+/* add (brute_force.rs:75-80) for n rows [n][dim]; ids may be NULL (ids
+ * len()..len()+n-1).  MutableVectorIndex::add (:254-265):
+ * FDB_ERR_DIMENSION_MISMATCH when dim differs from a non-empty index. */
+FDB_API fdb_status fdb_bf_add(fdb_bf* index, const float* rows, const uint64_t* ids, uint64_t n,
+                              uint32_t dim);
+/* MutableVectorIndex::remove (:267-274): *removed = 1 when a row had this
+ * id; the last row takes its place (VectorStore::swap_remove). */
+FDB_API fdb_status fdb_bf_remove(fdb_bf* index, uint64_t id, int* removed);
+/* len (:83) and dimension (:95; 0 when empty) */
+FDB_API uint64_t fdb_bf_len(const fdb_bf* index);
+FDB_API uint32_t fdb_bf_dimension(const fdb_bf* index);
+FDB_API uint32_t fdb_bf_metric(const fdb_bf* index);
+/* Persistable for BruteForceIndex (:277-385): header + payload
+ * [metric u8][n u64][dim u64][ids][data]. */
+FDB_API fdb_status fdb_bf_load(const char* path, fdb_bf** out);
+FDB_API fdb_status fdb_bf_save(const fdb_bf* index, const char* path);
+FDB_API void fdb_bf_destroy(fdb_bf* index);
+/* Copies rows [len][dim] and ids [len] out (either may be NULL). */
+FDB_API fdb_status fdb_bf_export(const fdb_bf* index, float* rows, uint64_t* ids);
+/* search / search_prefetch / search_parallel (:162-214): one query. */
+FDB_API fdb_status fdb_bf_search(fdb_bf* index, const float* query, uint32_t dim, uint32_t k,
+                                 uint64_t* out_ids, float* out_dists, uint32_t* out_count);
+/* batch_search (:220-225): results [nq][k] in input order. */
+FDB_API fdb_status fdb_bf_batch_search(fdb_bf* index, const float* queries, uint64_t nq,
+                                       uint32_t dim, uint32_t k, uint64_t* out_ids,
+                                       float* out_dists, uint32_t* out_counts);
+/* Device-resident inputs/outputs; enqueues only.  ms (nullable): when given,
+ * waits and returns the duration of the enqueued work (HIP events). */
+FDB_API fdb_status fdb_bf_batch_search_device(fdb_bf* index, const float* d_queries, uint64_t nq,
+                                              uint32_t k, uint64_t* d_out_ids, float* d_out_dists,
+                                              uint32_t* d_out_counts, void* hip_stream, float* ms);
+
+/* ------------------------------------------------------------------------ */
+/* IVF (full vectors): src/index/ivf.rs                                     */
+/* ------------------------------------------------------------------------ */
+/* Coarse: squared L2 to every centroid, stable ascending sort (ties → lower
+ * list id), first nprobe lists (ivf.rs:164-177).  Scan: metric.compute over
+ * every vector of those lists, bit-identical; the k smallest ascending, equal
+ * distances ordered by list-order position. */
+typedef struct fdb_ivf fdb_ivf;
+
+/* From the state IVFIndex::build leaves (ivf.rs:113-118): centroids
+ * [nlist][dim]; list_offsets [nlist+1] into ids [N] and rows [N][dim] in list
+ * order.  nprobe starts at 1. */
+FDB_API fdb_status fdb_ivf_create(const float* centroids, uint32_t nlist, uint32_t dim,
+                                  const uint64_t* list_offsets, const uint64_t* ids,
+                                  const float* rows, uint32_t metric, fdb_ivf** out);
+/* IVFIndex::build (ivf.rs:91-119) on the GPU: k-means over all vectors with
+ * DEFAULT_MAX_ITERATIONS = 100 (constants.rs:32), initialised from the
+ * SplitMix64 stream splitmix64(seed, 1) (the reference draws from an unseeded
+ * thread_rng), then first-minimum assignment; each list keeps input order.
+ * ids may be NULL (0..n-1). */
+FDB_API fdb_status fdb_ivf_build(const float* vectors, const uint64_t* ids, uint64_t n,
+                                 uint32_t dim, uint32_t n_clusters, uint32_t metric, uint64_t seed,
+                                 fdb_ivf** out);
+FDB_API void fdb_ivf_destroy(fdb_ivf* index);
+/* set_nprobe (ivf.rs:125-127): min(nprobe, nlist); nprobe() (:130-132) */
+FDB_API void fdb_ivf_set_nprobe(fdb_ivf* index, uint64_t nprobe);
+FDB_API uint64_t fdb_ivf_nprobe(const fdb_ivf* index);
+/* len (:135), num_partitions (:145), dimension (:150) */
+FDB_API uint64_t fdb_ivf_len(const fdb_ivf* index);
+FDB_API uint32_t fdb_ivf_num_partitions(const fdb_ivf* index);
+FDB_API uint32_t fdb_ivf_dimension(const fdb_ivf* index);
+/* Copies the artifacts back (any pointer may be NULL). */
+FDB_API fdb_status fdb_ivf_export(const fdb_ivf* index, float* centroids, uint64_t* list_offsets,
+                                  uint64_t* ids, float* rows);
+/* search / search_parallel (ivf.rs:162-290): one query; nprobe 0 → empty. */
+FDB_API fdb_status fdb_ivf_search(fdb_ivf* index, const float* query, uint32_t dim, uint32_t k,
+                                  uint64_t* out_ids, float* out_dists, uint32_t* out_count);
+/* batch_search / batch_search_optimized (ivf.rs:292-405): [nq][k]. */
+FDB_API fdb_status fdb_ivf_batch_search(fdb_ivf* index, const float* queries, uint64_t nq,
+                                        uint32_t dim, uint32_t k, uint64_t* out_ids,
+                                        float* out_dists, uint32_t* out_counts);
+/* Device-resident inputs/outputs; enqueues only (a NaN query is reported by
+ * fdb_ivf_sync).  coarse_ms/scan_ms (nullable): when given, waits and returns
+ * the two kernels' durations (HIP events). */
+FDB_API fdb_status fdb_ivf_batch_search_device(fdb_ivf* index, const float* d_queries, uint64_t nq,
+                                               uint32_t k, uint64_t* d_out_ids, float* d_out_dists,
+                                               uint32_t* d_out_counts, void* hip_stream,
+                                               float* coarse_ms, float* scan_ms);
+FDB_API fdb_status fdb_ivf_sync(fdb_ivf* index, void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

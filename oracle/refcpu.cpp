@@ -960,4 +960,26 @@ void fdbo_ivf_batch_search(const float* centroids, int nlist, int dim, const uin
   });
 }
 
+// IVFIndex::build (ivf.rs:91-119): KMeans::new(n_clusters,
+// DEFAULT_MAX_ITERATIONS = 100) fitted on every vector, seeded from
+// splitmix64_at(seed, 1); each vector to its first-minimum squared-L2
+// centroid (min_by, ivf.rs:101-108), lists keeping input order.
+int fdbo_ivf_build(const float* vectors, uint64_t n, int dim, int nlist, uint64_t seed,
+                   int nthreads, float* centroids_out, uint64_t* offsets_out,
+                   uint64_t* order_out) {
+  if (n == 0 || nlist <= 0 || dim <= 0) return -1;
+  if (kmeans_fit(vectors, n, dim, nlist, 100, splitmix64_at(seed, 1), centroids_out, nthreads))
+    return -1;
+  std::vector<int> assign(n);
+  parallel_for(n, nthreads, [&](uint64_t i) {
+    assign[i] = nearest(vectors + i * (uint64_t)dim, centroids_out, nlist, dim);
+  });
+  std::fill(offsets_out, offsets_out + nlist + 1, 0);
+  for (uint64_t i = 0; i < n; ++i) offsets_out[assign[i] + 1]++;
+  for (int l = 0; l < nlist; ++l) offsets_out[l + 1] += offsets_out[l];
+  std::vector<uint64_t> fill(offsets_out, offsets_out + nlist);
+  for (uint64_t i = 0; i < n; ++i) order_out[fill[assign[i]]++] = i;
+  return 0;
+}
+
 }  // extern "C"

@@ -136,6 +136,11 @@ void fdbo_ivf_batch_search(const float* centroids, int nlist, int dim,
                            const float* rows, int metric, uint64_t nprobe,
                            const float* queries, uint64_t nq, int k, int nthreads,
                            uint64_t* out_ids, float* out_dists, int32_t* out_counts);
+/* ivf.rs:91-119 with a seeded k-means: centroids [nlist][dim], offsets
+ * [nlist+1], order [n] = input row of each list-order position; 0 = ok */
+int fdbo_ivf_build(const float* vectors, uint64_t n, int dim, int nlist, uint64_t seed,
+                   int nthreads, float* centroids_out, uint64_t* offsets_out,
+                   uint64_t* order_out);
 
 #ifdef __cplusplus
 }

@@ -88,6 +88,8 @@ def lib() -> C.CDLL:
     L.fdbo_ivf_batch_search.argtypes = [_P, i32, i32, _P, _P, _P, i32, u64, _P, u64, i32, i32,
                                         _P, _P, _P]
     L.fdbo_ivf_batch_search.restype = None
+    L.fdbo_ivf_build.argtypes = [_P, u64, i32, i32, u64, i32, _P, _P, _P]
+    L.fdbo_ivf_build.restype = i32
     _lib = L
     return L
 
@@ -280,3 +282,20 @@ def ivf_batch_search(centroids, list_offsets, ids, rows, metric_id: int, nprobe:
     lib().fdbo_ivf_batch_search(_p(c), c.shape[0], c.shape[1], _p(off), _p(idv), _p(r), metric_id,
                                 nprobe, _p(q), nq, k, nthreads, _p(oid), _p(od), _p(cnt))
     return oid[:, :k], od[:, :k], cnt
+
+
+def splitmix64_at(seed: int, i: int) -> int:
+    return int(lib().fdbo_splitmix64_at(seed, i))
+
+
+def ivf_build(vectors, nlist: int, seed: int, nthreads: int = 0):
+    """IVFIndex::build restated: (centroids, list_offsets, order) where order
+    holds the input row of each list-order position."""
+    v = _f(vectors)
+    n, dim = v.shape
+    cen = np.empty((nlist, dim), np.float32)
+    off = np.empty(nlist + 1, np.uint64)
+    order = np.empty(n, np.uint64)
+    if lib().fdbo_ivf_build(_p(v), n, dim, nlist, seed, nthreads, _p(cen), _p(off), _p(order)):
+        raise ValueError("IVF build needs n >= nlist > 0")
+    return cen, off, order

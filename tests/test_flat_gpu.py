@@ -1,0 +1,240 @@
+"""Brute force and IVF (full vectors): the HIP path through the C ABI against
+the oracle on the same rows and queries.
+
+Bar: distances bit-exact for all five metrics (each kernel reproduces the
+metric's AVX2 operation order); ids identical, exact distance ties ordered by
+row (brute force: the earlier row, as scan_range's strict-< replacement
+keeps it) or by list-order position (IVF).
+"""
+import os
+import struct
+import tempfile
+import zlib
+
+import numpy as np
+import pytest
+
+import refcpu
+
+from forgedb import BruteForceIndex, DistanceMetric, ForgeDbError, IVFIndex, datagen
+
+pytestmark = pytest.mark.gpu
+
+METRICS = list(DistanceMetric)
+NO_ID = np.iinfo(np.uint64).max
+
+
+def check_rows(gi, gd, gc, oi, od, oc, label):
+    assert np.array_equal(gc, oc.astype(np.uint32)), f"{label}: counts {gc} vs {oc}"
+    for q in range(len(gc)):
+        c = int(oc[q])
+        assert np.array_equal(gd[q, :c], od[q, :c]), f"{label} q{q}: {gd[q, :c]} vs {od[q, :c]}"
+        assert np.array_equal(gi[q, :c], oi[q, :c]), f"{label} q{q}: ids {gi[q, :c]} vs {oi[q, :c]}"
+        assert np.all(gi[q, c:] == NO_ID) and np.all(np.isinf(gd[q, c:]))
+
+
+def bf_pair(rows, ids, metric, queries, k):
+    g = BruteForceIndex.from_arrays(rows, ids, metric)
+    out = g.batch_search_arrays(queries, k)
+    ref = refcpu.bf_batch_search(rows, ids, int(metric), queries, k)
+    return out, ref
+
+
+@pytest.fixture(scope="module")
+def bf_small():
+    base, queries = datagen.workload("bf_small")  # 10k x 128 U[0,1), 100 queries
+    return base, queries, np.arange(len(base), dtype=np.uint64)
+
+
+@pytest.mark.parametrize("metric", METRICS, ids=[m.name for m in METRICS])
+def test_bf_small_parity(bf_small, metric):
+    print(f"bf 10k x 128, 100 queries, k 10, {metric.name}", flush=True)
+    base, queries, ids = bf_small
+    (gi, gd, gc), (oi, od, oc) = bf_pair(base, ids, metric, queries, 10)
+    check_rows(gi, gd, gc, oi, od, oc, metric.name)
+
+
+@pytest.mark.parametrize("metric", [DistanceMetric.Cosine, DistanceMetric.DotProduct])
+def test_bf_normalised_parity(metric):
+    print(f"bf normalised 60k x 128, 48 queries, k 100, {metric.name}", flush=True)
+    base, queries = datagen.workload("bf_norm", n=60_000, nq=48)
+    ids = np.arange(len(base), dtype=np.uint64) * 3 + 7
+    (gi, gd, gc), (oi, od, oc) = bf_pair(base, ids, metric, queries, 100)
+    check_rows(gi, gd, gc, oi, od, oc, metric.name)
+
+
+@pytest.mark.parametrize("dim,n,nq,k", [(1, 300, 5, 4), (7, 1000, 17, 64), (8, 513, 3, 65),
+                                        (13, 2000, 33, 1), (100, 777, 20, 1000),
+                                        (130, 3000, 16, 256), (96, 50, 4, 100),
+                                        (2048, 600, 3, 5)])
+def test_bf_shapes(dim, n, nq, k):
+    print(f"bf shape dim={dim} n={n} nq={nq} k={k}", flush=True)
+    rng = np.random.default_rng(dim * 1000 + n)
+    rows = rng.standard_normal((n, dim)).astype(np.float32)
+    queries = rng.standard_normal((nq, dim)).astype(np.float32)
+    ids = rng.permutation(n).astype(np.uint64)
+    for metric in METRICS:
+        (gi, gd, gc), (oi, od, oc) = bf_pair(rows, ids, metric, queries, k)
+        check_rows(gi, gd, gc, oi, od, oc, f"dim{dim} {metric.name}")
+
+
+def test_bf_ties_keep_the_earlier_row():
+    print("bf exact ties", flush=True)
+    rng = np.random.default_rng(4)
+    uniq = rng.integers(0, 3, (40, 16)).astype(np.float32)
+    rows = uniq[rng.integers(0, 40, 5000)]  # many duplicate rows
+    queries = uniq[:10]
+    ids = np.arange(5000, dtype=np.uint64)
+    for metric in METRICS:
+        (gi, gd, gc), (oi, od, oc) = bf_pair(rows, ids, metric, queries, 50)
+        check_rows(gi, gd, gc, oi, od, oc, f"ties {metric.name}")
+
+
+def test_bf_single_search_and_kat():
+    print("bf single search + brute_force.rs KAT", flush=True)
+    # brute_force.rs:434-455: rows [i;4], i = 0..9, remove id 5, query [5;4]
+    g = BruteForceIndex(DistanceMetric.Euclidean)
+    for i in range(10):
+        g.add(i, [float(i)] * 4)
+    assert len(g) == 10 and g.dimension() == 4
+    assert g.remove(5) and not g.remove(5)
+    res = g.search([5.0] * 4, 10)
+    assert len(res) == 9 and 5 not in [i for i, _ in res]
+    assert res[0][1] == pytest.approx(2.0)
+    rows, ids = g.export()
+    assert ids.tolist() == [0, 1, 2, 3, 4, 9, 6, 7, 8]  # swap_remove moved the last row
+    oid, od = refcpu.bf_search(rows, ids, 0, np.full(4, 5.0, np.float32), 10)
+    assert [i for i, _ in res] == oid.tolist() and [d for _, d in res] == od.tolist()
+    # add after a search re-uploads
+    g.add(100, [5.0] * 4)
+    assert g.search([5.0] * 4, 1) == [(100, 0.0)]
+
+
+def test_bf_edges_and_errors():
+    print("bf edges", flush=True)
+    g = BruteForceIndex(DistanceMetric.Cosine)
+    assert g.search([1.0, 2.0], 3) == [] and g.dimension() == 0
+    rows = np.array([[0, 0, 0], [1, 0, 0], [0, 2, 0]], np.float32)
+    g.add_batch(rows)
+    # zero vector: cosine distance 0 (simd.rs:511-516)
+    assert g.search([0.0, 0.0, 0.0], 3) == [(0, 0.0), (1, 0.0), (2, 0.0)]
+    assert g.search([1.0, 0.0, 0.0], 0) == []
+    ids, d, c = g.batch_search_arrays(np.zeros((0, 3), np.float32), 5)
+    assert ids.shape == (0, 5)
+    with pytest.raises(ForgeDbError) as e:
+        g.search([1.0, 2.0], 3)
+    assert e.value.kind == "DimensionMismatch"
+    with pytest.raises(ForgeDbError) as e:
+        g.add_batch(np.ones((2, 4), np.float32))
+    assert e.value.kind == "DimensionMismatch"
+    with pytest.raises(ForgeDbError):
+        BruteForceIndex(7)
+    res = g.search([1.0, 1.0, 0.0], 10)
+    assert len(res) == 3
+
+
+def test_bf_save_load_bytes():
+    print("bf save/load", flush=True)
+    rng = np.random.default_rng(2)
+    rows = rng.standard_normal((257, 9)).astype(np.float32)
+    ids = rng.permutation(257).astype(np.uint64) + 1000
+    g = BruteForceIndex.from_arrays(rows, ids, DistanceMetric.Manhattan)
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "bf.fdb")
+        g.save(path)
+        raw = open(path, "rb").read()
+        # brute_force.rs:278-320 payload, persistence/format.rs header
+        payload = bytes([4]) + struct.pack("<QQ", 257, 9) + ids.tobytes() + rows.tobytes()
+        header = b"FORGEDB\0" + struct.pack("<IIII", 1, 4, 0, zlib.crc32(payload))
+        assert raw == header + payload
+        h = BruteForceIndex.load(path)
+        assert h.metric == DistanceMetric.Manhattan and len(h) == 257
+        q = rng.standard_normal((5, 9)).astype(np.float32)
+        a, b = g.batch_search_arrays(q, 7), h.batch_search_arrays(q, 7)
+        assert all(np.array_equal(x, y) for x, y in zip(a, b))
+        bad = bytearray(raw)
+        bad[-1] ^= 1
+        open(path, "wb").write(bytes(bad))
+        with pytest.raises(ForgeDbError) as e:
+            BruteForceIndex.load(path)
+        assert e.value.kind == "ChecksumMismatch"
+
+
+# ---- IVF ----------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def ivf_small():
+    """Gaussian-mixture rows (dim 96), 128 lists built by the oracle."""
+    base, queries = datagen.workload("ivf_flat", n=24_000, nq=64)
+    cen, off, order = refcpu.ivf_build(base, 128, seed=5)
+    return dict(base=base, queries=queries, cen=cen, off=off, ids=order.astype(np.uint64),
+                rows=base[order])
+
+
+def ivf_pair(s, metric, nprobe, k, queries=None):
+    q = s["queries"] if queries is None else queries
+    g = IVFIndex.from_artifacts(s["cen"], s["off"], s["ids"], s["rows"], metric)
+    g.set_nprobe(nprobe)
+    out = g.batch_search_arrays(q, k)
+    ref = refcpu.ivf_batch_search(s["cen"], s["off"], s["ids"], s["rows"], int(metric), g.nprobe(),
+                                  q, k)
+    return g, out, ref
+
+
+@pytest.mark.parametrize("metric", METRICS, ids=[m.name for m in METRICS])
+@pytest.mark.parametrize("nprobe,k", [(1, 10), (8, 100), (32, 100), (128, 7)])
+def test_ivf_parity(ivf_small, metric, nprobe, k):
+    print(f"ivf 24k x 96, nlist 128, nprobe {nprobe}, k {k}, {metric.name}", flush=True)
+    _, (gi, gd, gc), (oi, od, oc) = ivf_pair(ivf_small, metric, nprobe, k)
+    check_rows(gi, gd, gc, oi, od, oc, f"{metric.name} nprobe {nprobe}")
+
+
+def test_ivf_single_search_nprobe_rules(ivf_small):
+    print("ivf single search, nprobe 0 / clamp", flush=True)
+    g, (gi, gd, gc), _ = ivf_pair(ivf_small, DistanceMetric.Euclidean, 4, 20)
+    for q in range(5):
+        res = g.search(ivf_small["queries"][q], 20)
+        assert [i for i, _ in res] == gi[q, :gc[q]].tolist()
+        assert [d for _, d in res] == gd[q, :gc[q]].tolist()
+    g.set_nprobe(0)  # take(0): no lists (ivf.rs:175)
+    assert g.search(ivf_small["queries"][0], 5) == []
+    assert np.all(g.batch_search_arrays(ivf_small["queries"][:3], 5)[2] == 0)
+    g.set_nprobe(10_000)  # ivf.rs:125-127
+    assert g.nprobe() == 128
+    assert g.num_partitions() == 128 and len(g) == 24_000 and g.dimension() == 96
+    with pytest.raises(ForgeDbError) as e:
+        g.search(np.ones(95, np.float32), 3)
+    assert e.value.kind == "DimensionMismatch"
+
+
+def test_ivf_ragged_lists_and_ties():
+    print("ivf ragged lists, empty lists, ties", flush=True)
+    rng = np.random.default_rng(9)
+    uniq = rng.integers(-2, 3, (30, 11)).astype(np.float32)
+    rows = uniq[rng.integers(0, 30, 3001)]
+    cen = rng.standard_normal((17, 11)).astype(np.float32) * 2
+    cen[5] = 1000.0  # an empty list
+    lens = np.bincount(rng.integers(0, 16, 3001), minlength=17)
+    lens[5], lens[16] = 0, lens[5] + lens[16]
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.uint64)
+    s = dict(cen=cen, off=off, ids=np.arange(3001, dtype=np.uint64)[::-1].copy(), rows=rows,
+             queries=uniq[:12])
+    for metric in METRICS:
+        for nprobe, k in ((3, 40), (17, 300)):
+            _, (gi, gd, gc), (oi, od, oc) = ivf_pair(s, metric, nprobe, k)
+            check_rows(gi, gd, gc, oi, od, oc, f"ragged {metric.name} {nprobe}")
+
+
+def test_ivf_build_parity():
+    print("ivf build 12k x 96, nlist 64 vs the oracle", flush=True)
+    base, queries = datagen.workload("ivf_flat", n=12_000, nq=16)
+    g = IVFIndex.build(base, 64, DistanceMetric.Manhattan, seed=21)
+    art = g.export()
+    cen, off, order = refcpu.ivf_build(base, 64, seed=21)
+    assert np.array_equal(art["centroids"], cen)
+    assert np.array_equal(art["list_offsets"], off)
+    assert np.array_equal(art["ids"], order)
+    assert np.array_equal(art["rows"], base[order])
+    g.set_nprobe(6)
+    gi, gd, gc = g.batch_search_arrays(queries, 10)
+    oi, od, oc = refcpu.ivf_batch_search(cen, off, order, base[order], 4, 6, queries, 10)
+    check_rows(gi, gd, gc, oi, od, oc, "built")

@@ -297,3 +297,45 @@ def test_splitmix64_known_values():
         0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
     s = int(datagen.seeds(3)[0])
     assert int(datagen.splitmix64(s, 12345, 1)[0]) == refcpu.lib().fdbo_splitmix64_at(s, 12345)
+
+
+# ---- IVF (full vectors) ------------------------------------------------------
+def _small_ivf(seed=3, n=1500, dim=20, nlist=12):
+    rng = np.random.default_rng(seed)
+    x = (rng.random((n, dim)) * 4).astype(np.float32)
+    cen, off, order = refcpu.ivf_build(x, nlist, seed=11)
+    return x, cen, off, order
+
+
+def test_ivf_build_is_kmeans_then_first_minimum_assignment():
+    # ivf.rs:91-119: centroids = KMeans(n_clusters, 100).fit(all vectors);
+    # each vector in the list of its first-minimum centroid, input order kept
+    x, cen, off, order = _small_ivf()
+    assert np.array_equal(cen, refcpu.kmeans_fit(x, 12, 100, refcpu.splitmix64_at(11, 1)))
+    assert sorted(order.tolist()) == list(range(len(x)))
+    for l in range(12):
+        members = order[int(off[l]):int(off[l + 1])]
+        assert np.all(np.diff(members.astype(np.int64)) > 0)
+        for i in members[:40]:
+            d = [refcpu.dist("l2sq", x[i], c) for c in cen]
+            assert int(np.argmin(d)) == l  # np.argmin returns the first minimum
+
+
+def test_ivf_search_is_brute_force_over_probed_lists():
+    x, cen, off, order = _small_ivf()
+    rows, ids = x[order], order.astype(np.uint64)
+    rng = np.random.default_rng(5)
+    for m in (EUC, EUC2, COS, DOT, L1):
+        q = (rng.random(20) * 4).astype(np.float32)
+        for nprobe in (0, 1, 3, 12):
+            oi, od, oc = refcpu.ivf_batch_search(cen, off, ids, rows, m, nprobe, q[None], 9)
+            probes = refcpu.ivf_probes(cen, q, nprobe)
+            # stable sort of centroid distances (ivf.rs:164-177)
+            cd = np.array([refcpu.dist("l2sq", q, c) for c in cen], np.float32)
+            assert probes.tolist() == np.argsort(cd, kind="stable")[:nprobe].tolist()
+            pos = [p for l in probes for p in range(int(off[l]), int(off[l + 1]))]
+            d = np.array([refcpu.metric(m, q, rows[p]) for p in pos], np.float32)
+            srt = sorted(range(len(pos)), key=lambda j: (d[j], pos[j]))[:9]
+            assert int(oc[0]) == len(srt)
+            assert np.array_equal(od[0, :len(srt)], d[srt])
+            assert np.array_equal(oi[0, :len(srt)], ids[[pos[j] for j in srt]])
