@@ -1,23 +1,35 @@
-"""Batch IVF-PQ search throughput on one MI355X.
+"""Batch search throughput on one MI355X.
 
-Workload (the configuration the headline metric is quoted on): IVF-PQ over
-1,000,000 x 128 f32 vectors with non-negative integer components drawn from a
-1024-component Gaussian mixture (per-dim std 20, clipped to [0, 255]);
-nlist = 1024 k-means lists, M = 16 subvectors x 8 dims, 256 codewords each;
-nprobe = 16; 10,000 queries from the same mixture; k = 10; Euclidean.
+Default workload (the configuration the headline metric is quoted on):
+IVF-PQ over 1,000,000 x 128 f32 vectors with non-negative integer components
+drawn from a 1024-component Gaussian mixture (per-dim std 20, clipped to
+[0, 255]); nlist = 1024 k-means lists, M = 16 subvectors x 8 dims, 256
+codewords each; nprobe = 16; 10,000 queries from the same mixture; k = 10;
+Euclidean.
 
-A step is one batch_search of all 10,000 queries with the queries, the index
-and the outputs resident in HBM: coarse selection + fused LUT/ADC/top-k scan.
-The index is built on the GPU first (IVFPQIndex::build, seeded).
+A step is one batch_search of all queries with the queries, the index and the
+outputs resident in HBM.  For IVF-PQ that is coarse selection + the fused
+LUT/ADC/top-k scan; the index is built on the GPU first (seeded).
 
-The roofline object covers the dominant kernel (the fused scan).  Its
-achieved figure is the algorithmic code bytes (sum over queries of the sizes
-of its 16 probed lists, times M = 16 bytes) divided by the scan kernel's mean
-duration measured with HIP events on the stream it runs on.
+The roofline object covers the dominant kernel.  IVF-PQ: the algorithmic code
+bytes (sum over queries of the sizes of its probed lists, times M bytes)
+divided by the scan kernel's mean duration, measured with HIP events on the
+stream it runs on.
 
-cpu_baseline: the oracle (a C++ restatement of the reference's
-batch_search_parallel with its AVX2 kernels) on a bounded query sample, on
-the host cores of the same machine.
+Other workloads (--workload), each measured the same way with its own
+roofline:
+  bf_10k        brute force 10,000 x 128 U[0,1), 100 queries, k 10, L2^2
+  bf_1m_cosine  brute force 1,000,000 x 128 normalised Gaussian, 10,000
+  bf_1m_dot     queries, k 100 (cosine / dot product); flops 2*Q*N*D
+  ivf_1m_l2     IVF (full vectors) 1,000,000 x 96 Gaussian mixture, nlist
+  ivf_1m_l1     4096, nprobe 32, 10,000 queries, k 100 (Euclidean /
+                Manhattan); bytes sum over queries of scanned rows * D * 4
+  ivfpq_10m     IVF-PQ 10,000,000 x 96 Gaussian mixture, nlist 4096,
+                M 32 x 3, nprobe 64, 10,000 queries, k 100
+
+cpu_baseline: the oracle (a C++ restatement of the reference's CPU path with
+its AVX2 kernels) on a bounded query sample, on the host cores of the same
+machine.
 """
 import argparse
 import json
@@ -28,8 +40,40 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "forge-db_amd"))
 
-METRIC = "batch QPS at k=10, IVF-PQ 1M×128 nprobe=16; ADC-scan HBM GB/s"
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+
+WORKLOADS = {
+    "ivfpq_1m": dict(kind="ivfpq", data="ivfpq_int", n=1_000_000, nq=10_000, nlist=1024, M=16,
+                     nprobe=16, k=10, metric=0,
+                     metric_name="batch QPS at k=10, IVF-PQ 1M×128 nprobe=16; ADC-scan HBM GB/s",
+                     desc="IVF-PQ 1Mx128 integer Gaussian mixture (1024 comps, std 20), nlist 1024, "
+                          "M 16x8, nprobe 16, Q 10000, k 10, Euclidean"),
+    "ivfpq_10m": dict(kind="ivfpq", data="ivfpq_large", n=10_000_000, nq=10_000, nlist=4096, M=32,
+                      nprobe=64, k=100, metric=0,
+                      metric_name="batch QPS at k=100, IVF-PQ 10M×96 M=32x3 nprobe=64",
+                      desc="IVF-PQ 10Mx96 Gaussian mixture (4096 comps), nlist 4096, M 32x3, "
+                           "nprobe 64, Q 10000, k 100, Euclidean"),
+    "bf_10k": dict(kind="bf", data="bf_small", n=10_000, nq=100, k=10, metric=1,
+                   metric_name="batch QPS at k=10, brute force 10k×128 L2²",
+                   desc="BruteForce 10kx128 U[0,1), Q 100, k 10, EuclideanSquared"),
+    "bf_1m_cosine": dict(kind="bf", data="bf_norm", n=1_000_000, nq=10_000, k=100, metric=2,
+                         metric_name="batch QPS at k=100, brute force 1M×128 cosine",
+                         desc="BruteForce 1Mx128 normalised Gaussian, Q 10000, k 100, Cosine"),
+    "bf_1m_dot": dict(kind="bf", data="bf_norm", n=1_000_000, nq=10_000, k=100, metric=3,
+                      metric_name="batch QPS at k=100, brute force 1M×128 dot product",
+                      desc="BruteForce 1Mx128 normalised Gaussian, Q 10000, k 100, DotProduct"),
+    "ivf_1m_l2": dict(kind="ivf", data="ivf_flat", n=1_000_000, nq=10_000, nlist=4096, nprobe=32,
+                      k=100, metric=0,
+                      metric_name="batch QPS at k=100, IVF-flat 1M×96 nprobe=32 Euclidean",
+                      desc="IVF 1Mx96 Gaussian mixture (4096 comps), nlist 4096, nprobe 32, "
+                           "Q 10000, k 100, Euclidean"),
+    "ivf_1m_l1": dict(kind="ivf", data="ivf_flat", n=1_000_000, nq=10_000, nlist=4096, nprobe=32,
+                      k=100, metric=4,
+                      metric_name="batch QPS at k=100, IVF-flat 1M×96 nprobe=32 Manhattan",
+                      desc="IVF 1Mx96 Gaussian mixture (4096 comps), nlist 4096, nprobe 32, "
+                           "Q 10000, k 100, Manhattan"),
+}
 
 
 def log(*a):
@@ -46,9 +90,10 @@ def cpu_model():
     return "unknown"
 
 
-def read_traffic():
-    """HBM bytes per scan launch from the committed rocprofv3 --pmc summary, if any."""
-    p = os.path.join(ROOT, "profiles", "ivfpq_scan_1Mx128_traffic.txt")
+def read_traffic(name):
+    """HBM bytes per launch of the dominant kernel from a committed
+    rocprofv3 --pmc summary (profiles/<name>), if present."""
+    p = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(p):
         return None
     for line in open(p):
@@ -57,14 +102,260 @@ def read_traffic():
     return None
 
 
+class Runner:
+    """Device buffers, the timed loop and kernel timing shared by workloads."""
+
+    def __init__(self, args, queries, k):
+        import torch
+        self.torch = torch
+        self.args = args
+        self.dev = torch.device("cuda:0")
+        self.stream = torch.cuda.Stream(device=self.dev)
+        self.sptr = self.stream.cuda_stream
+        self.nq = queries.shape[0]
+        self.k = k
+        self.q_d = torch.from_numpy(queries).to(self.dev)
+        self.ids_d = torch.empty((self.nq, k), dtype=torch.int64, device=self.dev)
+        self.dist_d = torch.empty((self.nq, k), dtype=torch.float32, device=self.dev)
+        self.cnt_d = torch.empty(self.nq, dtype=torch.int32, device=self.dev)
+        torch.cuda.synchronize()
+
+    def ptrs(self):
+        return (self.q_d.data_ptr(), self.nq, self.k, self.ids_d.data_ptr(),
+                self.dist_d.data_ptr(), self.cnt_d.data_ptr(), self.sptr)
+
+    def timed_loop(self, step, sync):
+        torch = self.torch
+        for _ in range(self.args.warmup):
+            step()
+        sync()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(self.args.steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        sync()
+        return (t1 - t0) * 1e3 / self.args.steps
+
+    def ids(self):
+        import numpy as np
+        return self.ids_d.cpu().numpy().view(np.uint64)
+
+
+def agreement(a, b, k):
+    import numpy as np
+    return float(np.mean([len(set(a[q].tolist()) & set(b[q].tolist())) / k for q in range(len(a))]))
+
+
+def cpu_sample(run, nq, seconds, probe_n):
+    """Times run(m) on a probe of probe_n queries, then on a sample sized for
+    about `seconds` of CPU work; returns (sample, seconds, result)."""
+    t = time.perf_counter()
+    run(probe_n)
+    per_q = (time.perf_counter() - t) / probe_n
+    sample = int(min(nq, max(probe_n, seconds / max(per_q, 1e-9))))
+    t = time.perf_counter()
+    out = run(sample)
+    return sample, time.perf_counter() - t, out
+
+
+def bench_ivfpq(args, w, base, queries):
+    import numpy as np
+    from forgedb import LUT_EXACT, LUT_FAST, IVFPQIndex
+
+    nlist, M, nprobe, k = w["nlist"], w["M"], w["nprobe"], w["k"]
+    t = time.time()
+    index = IVFPQIndex.build(base, nlist, M, seed=args.seed)
+    log(f"[bench] GPU build (k-means {nlist}, PQ {M}x256, encode) in {time.time() - t:.1f}s")
+    index.set_nprobe(nprobe)
+    r = Runner(args, queries, k)
+    nq = r.nq
+
+    def step():
+        index.batch_search_device(*r.ptrs())
+
+    def sync():
+        index.sync(r.sptr)
+
+    ms_per_step = r.timed_loop(step, sync)
+    log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step, {nq / ms_per_step * 1e3:,.0f} QPS")
+
+    def kernel_times():
+        coarse, scan = [], []
+        for _ in range(args.timing_reps):
+            c, s = index.batch_search_device(*r.ptrs(), timed=True)
+            coarse.append(c)
+            scan.append(s)
+        return float(np.mean(coarse)), float(np.mean(scan))
+
+    coarse_ms, scan_ms = kernel_times()
+    exact_ids = r.ids().copy()
+
+    # the opt-in fast LUT mode, timed the same way (distances within ~1e-6)
+    index.set_lut_mode(LUT_FAST)
+    fast_ms = r.timed_loop(step, sync)
+    _, fast_scan_ms = kernel_times()
+    fast_agree = agreement(r.ids(), exact_ids, k)
+    index.set_lut_mode(LUT_EXACT)
+    step()
+    sync()
+    log(f"[bench] fast LUT mode: {fast_ms:.3f} ms/step, {nq / fast_ms * 1e3:,.0f} QPS, scan "
+        f"{fast_scan_ms:.3f} ms; id agreement with exact mode {fast_agree:.6f}")
+
+    lists, _ = index.probe(queries, nprobe)
+    sizes = np.diff(index.list_offsets().astype(np.int64))
+    scanned = int(sizes[lists].sum())
+    code_bytes = scanned * M
+    achieved = code_bytes / (scan_ms / 1e3) / 1e9
+    log(f"[bench] coarse {coarse_ms:.3f} ms, scan {scan_ms:.3f} ms; {scanned / nq:,.0f} codes "
+        f"per query; {code_bytes / 1e9:.3f} GB of codes -> {achieved:,.0f} GB/s")
+    dsub = base.shape[1] // M
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": read_traffic(f"ivfpq_scan_{args.workload_tag}_traffic.txt"),
+            "kernel": f"ivfpq_scan_kernel<{M},{dsub},...>", "kernel_ms": round(scan_ms, 4),
+            "algorithmic_bytes": code_bytes, "coarse_ms": round(coarse_ms, 4)}
+    extra = {"fast_lut": {"value": round(nq / fast_ms * 1e3, 1), "ms_per_step": round(fast_ms, 4),
+                          "scan_ms": round(fast_scan_ms, 4),
+                          "achieved_gbs": round(code_bytes / (fast_scan_ms / 1e3) / 1e9, 1),
+                          "id_agreement_with_exact": round(fast_agree, 6)}}
+
+    cpu = None
+    if not args.no_cpu:
+        import refcpu  # CPU baseline leg only
+        art = index.export()
+        oracle = refcpu.IvfPq.create(art["centroids"], art["codebooks"], art["list_offsets"],
+                                     art["ids"], art["codes"])
+        oracle.set_nprobe(nprobe)
+        threads = min(16, os.cpu_count() or 1)
+        sample, cpu_s, (oi, _, _) = cpu_sample(
+            lambda m: oracle.batch_search(queries[:m], k, parallel=True, nthreads=threads),
+            nq, args.cpu_seconds, min(nq, 200))
+        agree = agreement(exact_ids[:sample], oi, k)
+        cpu = {"value": round(sample / cpu_s, 1), "unit": "queries/s", "cores": threads,
+               "kind": "port",
+               "sample": f"first {sample} of the {nq} queries, batch_search_parallel "
+                         f"(chunks of 4), {cpu_s:.1f} s on {cpu_model()}",
+               "gpu_id_agreement": round(agree, 6)}
+        log(f"[bench] CPU baseline {sample / cpu_s:,.0f} QPS on {threads} threads "
+            f"({sample} queries in {cpu_s:.1f}s); id agreement {agree:.6f}")
+    cfg = {"n": base.shape[0], "nq": nq, "nlist": nlist, "M": M, "nprobe": nprobe, "k": k}
+    return ms_per_step, roof, cpu, cfg, extra
+
+
+def bench_bf(args, w, base, queries):
+    import numpy as np
+    from forgedb import BruteForceIndex, DistanceMetric
+
+    k, metric = w["k"], DistanceMetric(w["metric"])
+    t = time.time()
+    index = BruteForceIndex.from_arrays(base, None, metric)
+    r = Runner(args, queries, k)
+    nq = r.nq
+
+    def step():
+        index.batch_search_device(*r.ptrs())
+
+    step()  # uploads the rows
+    r.torch.cuda.synchronize()
+    log(f"[bench] brute-force index resident in {time.time() - t:.1f}s")
+    ms_per_step = r.timed_loop(step, lambda: None)
+    log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step, {nq / ms_per_step * 1e3:,.0f} QPS")
+    kms = float(np.mean([index.batch_search_device(*r.ptrs(), timed=True)
+                         for _ in range(args.timing_reps)]))
+    flops = 2.0 * nq * base.shape[0] * base.shape[1]
+    achieved = flops / (kms / 1e3) / 1e12
+    log(f"[bench] search kernels {kms:.3f} ms -> {achieved:.1f} TFLOP/s (2*Q*N*D)")
+    roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": None,
+            "kernel": "flat_topk_kernel + merge_parts_kernel", "kernel_ms": round(kms, 4),
+            "algorithmic_flops": flops}
+    gpu_ids = r.ids().copy()
+    cpu = None
+    if not args.no_cpu:
+        import refcpu  # CPU baseline leg only
+        threads = min(16, os.cpu_count() or 1)
+        ids = np.arange(base.shape[0], dtype=np.uint64)
+        sample, cpu_s, (oi, _, _) = cpu_sample(
+            lambda m: refcpu.bf_batch_search(base, ids, int(metric), queries[:m], k, threads),
+            nq, args.cpu_seconds, min(nq, 16))
+        agree = agreement(gpu_ids[:sample], oi, k)
+        cpu = {"value": round(sample / cpu_s, 1), "unit": "queries/s", "cores": threads,
+               "kind": "port",
+               "sample": f"first {sample} of the {nq} queries, batch_search (queries in "
+                         f"parallel), {cpu_s:.1f} s on {cpu_model()}",
+               "gpu_id_agreement": round(agree, 6)}
+        log(f"[bench] CPU baseline {sample / cpu_s:,.1f} QPS on {threads} threads "
+            f"({sample} queries in {cpu_s:.1f}s); id agreement {agree:.6f}")
+    cfg = {"n": base.shape[0], "nq": nq, "k": k, "metric": metric.name}
+    return ms_per_step, roof, cpu, cfg, {}
+
+
+def bench_ivf(args, w, base, queries):
+    import numpy as np
+    from forgedb import DistanceMetric, IVFIndex
+
+    nlist, nprobe, k, metric = w["nlist"], w["nprobe"], w["k"], DistanceMetric(w["metric"])
+    t = time.time()
+    index = IVFIndex.build(base, nlist, metric, seed=args.seed)
+    log(f"[bench] GPU build (k-means {nlist}, 100 iterations max) in {time.time() - t:.1f}s")
+    index.set_nprobe(nprobe)
+    r = Runner(args, queries, k)
+    nq = r.nq
+
+    def step():
+        index.batch_search_device(*r.ptrs())
+
+    ms_per_step = r.timed_loop(step, lambda: index.sync(r.sptr))
+    log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step, {nq / ms_per_step * 1e3:,.0f} QPS")
+    times = [index.batch_search_device(*r.ptrs(), timed=True) for _ in range(args.timing_reps)]
+    coarse_ms = float(np.mean([c for c, _ in times]))
+    scan_ms = float(np.mean([s for _, s in times]))
+    lists = index.probe(queries, nprobe)
+    sizes = np.diff(index.export()["list_offsets"].astype(np.int64))
+    scanned = int(sizes[lists].sum())
+    row_bytes = scanned * base.shape[1] * 4
+    achieved = row_bytes / (scan_ms / 1e3) / 1e9
+    log(f"[bench] coarse {coarse_ms:.3f} ms, scan {scan_ms:.3f} ms; {scanned / nq:,.0f} rows per "
+        f"query; {row_bytes / 1e9:.2f} GB of rows -> {achieved:,.0f} GB/s")
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "ivf_flat_scan_kernel", "kernel_ms": round(scan_ms, 4),
+            "algorithmic_bytes": row_bytes, "coarse_ms": round(coarse_ms, 4)}
+    gpu_ids = r.ids().copy()
+    cpu = None
+    if not args.no_cpu:
+        import refcpu  # CPU baseline leg only
+        art = index.export()
+        threads = min(16, os.cpu_count() or 1)
+        sample, cpu_s, (oi, _, _) = cpu_sample(
+            lambda m: refcpu.ivf_batch_search(art["centroids"], art["list_offsets"], art["ids"],
+                                              art["rows"], int(metric), nprobe, queries[:m], k,
+                                              threads),
+            nq, args.cpu_seconds, min(nq, 200))
+        agree = agreement(gpu_ids[:sample], oi, k)
+        cpu = {"value": round(sample / cpu_s, 1), "unit": "queries/s", "cores": threads,
+               "kind": "port",
+               "sample": f"first {sample} of the {nq} queries, batch_search (queries in "
+                         f"parallel), {cpu_s:.1f} s on {cpu_model()}",
+               "gpu_id_agreement": round(agree, 6)}
+        log(f"[bench] CPU baseline {sample / cpu_s:,.0f} QPS on {threads} threads "
+            f"({sample} queries in {cpu_s:.1f}s); id agreement {agree:.6f}")
+    cfg = {"n": base.shape[0], "nq": nq, "nlist": nlist, "nprobe": nprobe, "k": k,
+           "metric": metric.name}
+    return ms_per_step, roof, cpu, cfg, {}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=1)
-    ap.add_argument("--n", type=int, default=1_000_000)
-    ap.add_argument("--nq", type=int, default=10_000)
+    ap.add_argument("--workload", default="ivfpq_1m", choices=sorted(WORKLOADS))
+    ap.add_argument("--n", type=int, default=None, help="override the base size")
+    ap.add_argument("--nq", type=int, default=None, help="override the query count")
     ap.add_argument("--timing-reps", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target wall time of the CPU baseline sample")
@@ -77,32 +368,20 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path "
               f"(asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
-    import numpy as np
     import torch
 
-    from forgedb import LUT_EXACT, LUT_FAST, IVFPQIndex, datagen
+    from forgedb import datagen
 
-    nlist, M, nprobe, k = 1024, 16, 16, 10
+    w = WORKLOADS[args.workload]
+    args.workload_tag = {"ivfpq_1m": "1Mx128", "ivfpq_10m": "10Mx96"}.get(args.workload, "")
     t = time.time()
-    base, queries = datagen.workload("ivfpq_int", n=args.n, nq=args.nq)
-    log(f"[bench] generated {base.shape} base, {queries.shape} queries in {time.time() - t:.1f}s")
-    t = time.time()
-    index = IVFPQIndex.build(base, nlist, M, seed=args.seed)
-    log(f"[bench] GPU build (k-means {nlist}, PQ {M}x256, encode) in {time.time() - t:.1f}s")
-    index.set_nprobe(nprobe)
-
-    dev = torch.device("cuda:0")
-    stream = torch.cuda.Stream(device=dev)
-    nq = queries.shape[0]
-    q_d = torch.from_numpy(queries).to(dev)
-    ids_d = torch.empty((nq, k), dtype=torch.int64, device=dev)
-    dist_d = torch.empty((nq, k), dtype=torch.float32, device=dev)
-    cnt_d = torch.empty(nq, dtype=torch.int32, device=dev)
-    torch.cuda.synchronize()
-    sptr = stream.cuda_stream
+    base, queries = datagen.workload(w["data"], n=args.n or w["n"], nq=args.nq or w["nq"])
+    log(f"[bench] {args.workload}: generated {base.shape} base, {queries.shape} queries in "
+        f"{time.time() - t:.1f}s")
     if args.calibrate_copy:
-        src = torch.empty(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda:0")  # 1 GiB
         dst = torch.empty_like(src)
         src.fill_(1.0)
         torch.cuda.synchronize()
@@ -111,96 +390,12 @@ def main():
         del src, dst
         log("[bench] calibration copy: 1 GiB device to device")
 
-    def step():
-        index.batch_search_device(q_d.data_ptr(), nq, k, ids_d.data_ptr(), dist_d.data_ptr(),
-                                  cnt_d.data_ptr(), sptr)
-
-    for _ in range(args.warmup):
-        step()
-    index.sync(sptr)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    index.sync(sptr)
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
-    qps = nq / (ms_per_step / 1e3)
-    log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step, {qps:,.0f} QPS")
-
-    def kernel_times():
-        coarse, scan = [], []
-        for _ in range(args.timing_reps):
-            c, s = index.batch_search_device(q_d.data_ptr(), nq, k, ids_d.data_ptr(),
-                                             dist_d.data_ptr(), cnt_d.data_ptr(), sptr, timed=True)
-            coarse.append(c)
-            scan.append(s)
-        return float(np.mean(coarse)), float(np.mean(scan))
-
-    coarse_ms, scan_ms = kernel_times()
-    exact_ids = ids_d.cpu().numpy().view(np.uint64).copy()
-
-    # the opt-in fast LUT mode, timed the same way (distances within ~1e-6)
-    index.set_lut_mode(LUT_FAST)
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    fast_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    _, fast_scan_ms = kernel_times()
-    fast_ids = ids_d.cpu().numpy().view(np.uint64)
-    fast_agree = float(np.mean([len(set(fast_ids[q].tolist()) & set(exact_ids[q].tolist())) / k
-                                for q in range(nq)]))
-    index.set_lut_mode(LUT_EXACT)
-    index.batch_search_device(q_d.data_ptr(), nq, k, ids_d.data_ptr(), dist_d.data_ptr(),
-                              cnt_d.data_ptr(), sptr)
-    index.sync(sptr)
-    log(f"[bench] fast LUT mode: {fast_ms:.3f} ms/step, {nq / fast_ms * 1e3:,.0f} QPS, scan "
-        f"{fast_scan_ms:.3f} ms; id agreement with exact mode {fast_agree:.6f}")
-
-    lists, _ = index.probe(queries, nprobe)
-    sizes = np.diff(index.list_offsets().astype(np.int64))
-    scanned = int(sizes[lists].sum())
-    code_bytes = scanned * M
-    achieved = code_bytes / (scan_ms / 1e3) / 1e9
-    log(f"[bench] coarse {coarse_ms:.3f} ms, scan {scan_ms:.3f} ms; {scanned / nq:,.0f} codes "
-        f"per query; {code_bytes / 1e9:.3f} GB of codes -> {achieved:,.0f} GB/s")
-
-    cpu = None
-    if not args.no_cpu:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import refcpu  # CPU baseline leg only
-        art = index.export()
-        oracle = refcpu.IvfPq.create(art["centroids"], art["codebooks"], art["list_offsets"],
-                                     art["ids"], art["codes"])
-        oracle.set_nprobe(nprobe)
-        threads = min(16, os.cpu_count() or 1)
-        probe_n = min(nq, 200)
-        t = time.perf_counter()
-        oracle.batch_search(queries[:probe_n], k, parallel=True, nthreads=threads)
-        per_q = (time.perf_counter() - t) / probe_n
-        sample = int(min(nq, max(probe_n, args.cpu_seconds / max(per_q, 1e-9))))
-        t = time.perf_counter()
-        oi, od, oc = oracle.batch_search(queries[:sample], k, parallel=True, nthreads=threads)
-        cpu_s = time.perf_counter() - t
-        cpu_qps = sample / cpu_s
-        gi = ids_d[:sample].cpu().numpy().view(np.uint64)
-        agree = float(np.mean([len(set(gi[q].tolist()) & set(oi[q].tolist())) / k
-                               for q in range(sample)]))
-        cpu = {"value": round(cpu_qps, 1), "unit": "queries/s", "cores": threads, "kind": "port",
-               "sample": f"first {sample} of the {nq} queries, batch_search_parallel "
-                         f"(chunks of 4), {cpu_s:.1f} s on {cpu_model()}",
-               "gpu_id_agreement": round(agree, 6)}
-        log(f"[bench] CPU baseline {cpu_qps:,.0f} QPS on {threads} threads "
-            f"({sample} queries in {cpu_s:.1f}s); id agreement {agree:.6f}")
-
+    fn = {"ivfpq": bench_ivfpq, "bf": bench_bf, "ivf": bench_ivf}[w["kind"]]
+    ms_per_step, roof, cpu, cfg, extra = fn(args, w, base, queries)
+    nq = queries.shape[0]
     line = {
-        "metric": METRIC,
-        "value": round(qps, 1),
+        "metric": w["metric_name"],
+        "value": round(nq / ms_per_step * 1e3, 1),
         "unit": "queries/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -211,20 +406,11 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "IVF-PQ 1Mx128 integer Gaussian mixture (1024 comps, std 20), "
-                               "nlist 1024, M 16x8, nprobe 16, Q 10000, k 10, Euclidean",
-                   "n": args.n, "nq": nq, "nlist": nlist, "M": M, "nprobe": nprobe, "k": k},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(),
-                     "kernel": "ivfpq_scan_kernel<16,8,1,0>", "kernel_ms": round(scan_ms, 4),
-                     "algorithmic_bytes": code_bytes, "coarse_ms": round(coarse_ms, 4)},
-        "fast_lut": {"value": round(nq / fast_ms * 1e3, 1), "ms_per_step": round(fast_ms, 4),
-                     "scan_ms": round(fast_scan_ms, 4),
-                     "achieved_gbs": round(code_bytes / (fast_scan_ms / 1e3) / 1e9, 1),
-                     "id_agreement_with_exact": round(fast_agree, 6)},
+        "config": dict({"workload": w["desc"]}, **cfg),
+        "roofline": roof,
         "cpu_baseline": cpu,
     }
+    line.update(extra)
     print(json.dumps(line), flush=True)
 
 

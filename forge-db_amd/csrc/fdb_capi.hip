@@ -496,6 +496,16 @@ fdb_status fdb_ivf_batch_search_device(fdb_ivf* h, const float* d_queries, uint6
   });
 }
 
+fdb_status fdb_ivf_probe(fdb_ivf* h, const float* queries, uint64_t nq, uint32_t dim, uint32_t nprobe,
+                         int32_t* out_lists) {
+  return guarded([&] {
+    IvfFlatIndex* ix = impl_of(h);
+    if (nq && (!queries || !out_lists)) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (dim != ix->dim()) throw Error(FDB_ERR_DIMENSION_MISMATCH, "query dimension does not match the index");
+    ix->probe(queries, nq, nprobe, out_lists);
+  });
+}
+
 fdb_status fdb_ivf_sync(fdb_ivf* h, void* stream) {
   return guarded([&] {
     if (impl_of(h)->sync((hipStream_t)stream))

@@ -799,6 +799,19 @@ void IvfFlatIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_i
   }
 }
 
+void IvfFlatIndex::probe(const float* qs, uint64_t nq, uint32_t nprobe, int32_t* lists) {
+  if (nq == 0 || nprobe == 0) return;
+  std::lock_guard<std::mutex> g(mu_);
+  if (nprobe > nlist_) throw Error(FDB_ERR_INVALID_ARGUMENT, "nprobe above nlist");
+  if (nprobe > 1024) throw Error(FDB_ERR_UNSUPPORTED, "nprobe above 1024");
+  q_.upload(qs, nq * dim_, stream_);
+  probes_.reserve(nq * nprobe);
+  FDB_HIP(launch_coarse_select(q_.p, nq, (int)dim_, centT_.p, (int)nlist_, (int)nprobe, probes_.p,
+                               nullptr, err_.p, stream_));
+  FDB_HIP(hipMemcpyAsync(lists, probes_.p, 4 * nq * nprobe, hipMemcpyDeviceToHost, stream_));
+  FDB_HIP(hipStreamSynchronize(stream_));
+}
+
 bool IvfFlatIndex::sync(hipStream_t s) {
   std::lock_guard<std::mutex> g(mu_);
   FDB_HIP(hipStreamSynchronize(s ? s : stream_));

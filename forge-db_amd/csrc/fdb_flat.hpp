@@ -146,6 +146,9 @@ class IvfFlatIndex {
   void batch_search_device(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids,
                            float* d_dists, uint32_t* d_counts, hipStream_t s, float* coarse_ms = nullptr,
                            float* scan_ms = nullptr);
+  // the nprobe nearest lists per query, ascending by (squared L2, list id)
+  // (the stable sort of ivf.rs:164-177)
+  void probe(const float* qs, uint64_t nq, uint32_t nprobe, int32_t* lists);
   // waits for s (null: own stream); true if a device search saw a NaN since
   // the last sync (the flag is cleared)
   bool sync(hipStream_t s);

@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "fdb_ivf_create", "fdb_ivf_build", "fdb_ivf_destroy", "fdb_ivf_set_nprobe", "fdb_ivf_nprobe",
     "fdb_ivf_len", "fdb_ivf_num_partitions", "fdb_ivf_dimension", "fdb_ivf_export",
     "fdb_ivf_search", "fdb_ivf_batch_search", "fdb_ivf_batch_search_device", "fdb_ivf_sync",
+    "fdb_ivf_probe",
 )
 
 LUT_EXACT, LUT_FAST = 0, 1
@@ -137,6 +138,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fdb_ivf_batch_search": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, _P, _P, _P],
         "fdb_ivf_batch_search_device": [_P, _P, C.c_uint64, C.c_uint32, _P, _P, _P, _P, _P, _P],
         "fdb_ivf_sync": [_P, _P],
+        "fdb_ivf_probe": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, _P],
     }
     for name, args in sig.items():
         f = getattr(lib, name)
@@ -616,3 +618,11 @@ class IVFIndex:
 
     def sync(self, stream: int = 0) -> None:
         _check(self._lib, self._lib.fdb_ivf_sync(self._h, C.c_void_p(stream)))
+
+    def probe(self, queries, nprobe: int) -> np.ndarray:
+        """Coarse step: lists [nq, nprobe] i32, nearest first."""
+        q = _f32(queries)
+        lists = np.empty((q.shape[0], nprobe), np.int32)
+        _check(self._lib, self._lib.fdb_ivf_probe(self._h, _ptr(q), q.shape[0], q.shape[1], nprobe,
+                                                  _ptr(lists)))
+        return lists

@@ -19,6 +19,9 @@ Workloads (seeds 0xF0DB0000 + 16*cfg + {1 base, 2 query, 3 centres}):
 """
 from __future__ import annotations
 
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 
 M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
@@ -70,11 +73,24 @@ def normal_f64(seed: int, count: int, start_pair: int = 0) -> np.ndarray:
     return out[:count]
 
 
-def _chunked_rows(n: int, dim: int, fn, chunk_rows: int = 1 << 16) -> np.ndarray:
+def _chunked_rows(n: int, dim: int, fn, chunk_rows: int = 1 << 15) -> np.ndarray:
+    """Row blocks are pure functions of their range, so they are generated on
+    a thread pool (numpy's ufuncs release the GIL); the result does not
+    depend on the number of workers."""
     out = np.empty((n, dim), np.float32)
-    for s in range(0, n, chunk_rows):
+
+    def block(s):
         e = min(n, s + chunk_rows)
         out[s:e] = fn(s, e)
+
+    starts = range(0, n, chunk_rows)
+    workers = min(16, os.cpu_count() or 1, max(1, len(starts)))
+    if workers == 1:
+        for s in starts:
+            block(s)
+    else:
+        with ThreadPoolExecutor(workers) as pool:
+            list(pool.map(block, starts))
     return out
 
 

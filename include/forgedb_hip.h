@@ -273,6 +273,10 @@ FDB_API fdb_status fdb_ivf_batch_search_device(fdb_ivf* index, const float* d_qu
                                                uint32_t* d_out_counts, void* hip_stream,
                                                float* coarse_ms, float* scan_ms);
 FDB_API fdb_status fdb_ivf_sync(fdb_ivf* index, void* hip_stream);
+/* Coarse step alone (ivf.rs:164-177): the nprobe (<= nlist) nearest lists
+ * per query, ascending by (squared L2, list id). */
+FDB_API fdb_status fdb_ivf_probe(fdb_ivf* index, const float* queries, uint64_t nq, uint32_t dim,
+                                 uint32_t nprobe, int32_t* out_lists);
 
 #ifdef __cplusplus
 }
