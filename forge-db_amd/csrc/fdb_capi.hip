@@ -422,6 +422,20 @@ fdb_status fdb_bf_batch_search_device(fdb_bf* h, const float* d_queries, uint64_
   });
 }
 
+fdb_status fdb_bf_set_search_mode(fdb_bf* h, uint32_t mode) {
+  return guarded([&] {
+    if (mode > 2) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown search mode");
+    impl_of(h)->set_screen_mode((int)mode);
+  });
+}
+
+fdb_status fdb_bf_last_fallbacks(fdb_bf* h, void* stream, uint64_t* out) {
+  return guarded([&] {
+    if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    *out = impl_of(h)->last_fallbacks((hipStream_t)stream);
+  });
+}
+
 /* ---- IVF ------------------------------------------------------------------ */
 
 fdb_status fdb_ivf_create(const float* centroids, uint32_t nlist, uint32_t dim,

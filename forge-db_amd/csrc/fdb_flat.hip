@@ -175,6 +175,11 @@ __global__ __launch_bounds__(kT) void flat_topk_kernel(FlatTopkArgs a) {
   const uint32_t chunk = blockIdx.x;
   const uint64_t q0 = (uint64_t)blockIdx.y * kQB;
   const int dim = a.dim;
+  if (a.flags) {  // re-run only tiles holding a flagged query (uniform exit)
+    bool any = false;
+    for (int t = 0; t < kQB; ++t) any |= (q0 + t < a.nq) && a.flags[q0 + t] != 0;
+    if (!any) return;
+  }
   for (int e = tid; e < kQB * dim; e += kT) {
     const int qq = e / dim;
     const int d = e - qq * dim;
@@ -235,9 +240,11 @@ __global__ __launch_bounds__(64) void merge_parts_kernel(const float* __restrict
                                                          const uint64_t* __restrict__ ids,
                                                          uint64_t* __restrict__ out_ids,
                                                          float* __restrict__ out_d,
-                                                         uint32_t* __restrict__ out_c) {
+                                                         uint32_t* __restrict__ out_c,
+                                                         const int* __restrict__ flags) {
   const uint64_t q = blockIdx.x;
   const int lane = threadIdx.x;
+  if (flags && flags[q] == 0) return;
   WaveTopK<R> tk;
   tk.init(k);
   const uint64_t total = (uint64_t)nparts * k;
@@ -336,6 +343,231 @@ __global__ __launch_bounds__(kT) void ivf_flat_scan_kernel(IvfFlatScanArgs a) {
   if (lane == 0) a.out_counts[q] = count;
 }
 
+// ---------------------------------------------------------------------------
+// MFMA screening for dot product, cosine and (squared) Euclidean.
+//
+// mfma_screen_kernel: approximate distances from v_mfma_f32_32x32x2f32
+// (query tile 32 x dim times 32 rows per wave, so 128 rows per workgroup
+// step), turned into the metric's value with exact norms, and the K' = 64*RS
+// smallest per query kept in wave-resident WaveTopK lists (each wave owns 8
+// of the 32 queries).  The product sums the dimensions in some order of the
+// matrix unit's choosing, so it differs from the reference's order by at most
+// eps (see screen_eps); the rescore kernel computes exact distances for the
+// K' candidates and checks that no row outside them can enter the top k.
+// ---------------------------------------------------------------------------
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int kSQ = 32;    // queries per screening workgroup
+constexpr int kSRows = 128;  // rows per workgroup step
+
+// Reference-order distance of one query (LDS, natural order) to one row
+// (global, natural order), computed by a single lane.
+template <int MET>
+__device__ __forceinline__ float exact_lane(const float* __restrict__ q, const float* __restrict__ x,
+                                            int dim, float qn, float rn) {
+  const int d8 = dim / 8;
+  float total = 0.0f;
+  if (d8 > 0) {
+    float ch[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) ch[l] = 0.0f;
+    for (int i = 0; i < d8; ++i) {
+      const float4 x0 = *reinterpret_cast<const float4*>(x + 8 * i);
+      const float4 x1 = *reinterpret_cast<const float4*>(x + 8 * i + 4);
+      const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int l = 0; l < 8; ++l) ch[l] = chain_step<MET>(ch[l], q[8 * i + l], xv[l]);
+    }
+    total = ch[0];
+#pragma unroll
+    for (int l = 1; l < 8; ++l) total = total + ch[l];
+  }
+  for (int i = 8 * d8; i < dim; ++i) total = tail_step<MET>(total, q[i], x[i]);
+  return finish<MET>(total, qn, rn);
+}
+
+// Screening value: the metric's distance (squared for Euclidean) from an
+// approximate dot product s.
+template <int MET>
+__device__ __forceinline__ float screen_value(float s, float qn, float rn) {
+  if constexpr (MET == FDB_METRIC_DOT_PRODUCT) {
+    return -s;
+  } else if constexpr (MET == FDB_METRIC_COSINE) {
+    const float np = __builtin_sqrtf(qn * rn);
+    return np == 0.0f ? 0.0f : 1.0f - s / np;
+  } else {
+    return __builtin_fmaf(-2.0f, s, qn + rn);
+  }
+}
+
+// Bound on |screen value - reference value| for one query (squared domain
+// for Euclidean), with u = 2^-24 and g = dim*u/(1 - dim*u) the classic
+// bound for a dim-term float sum:
+//   dot:     both sums within g*sum|q_i x_i| <= g*|q|*max|x| of the exact dot
+//   cosine:  the same over np ~ |q||x|, plus the division and 1 - x roundings
+//   L2^2:    norms and dot each within g of their magnitudes; the
+//            reference's sum of squares within (g + 3u) of the exact value
+// with 10% slack and a floor for flushed denormal products.
+__device__ __forceinline__ float screen_eps(int met, int dim, float qn, float rnmax) {
+  const float u = 5.9604645e-8f;
+  const float g = dim * u / (1.0f - dim * u);
+  if (met == FDB_METRIC_DOT_PRODUCT) return 2.2f * g * __builtin_sqrtf(qn) * __builtin_sqrtf(rnmax) + 1e-30f;
+  if (met == FDB_METRIC_COSINE) return 2.2f * g + 16.0f * u + 1e-30f;
+  return (4.4f * g + 12.0f * u) * (qn + rnmax) + 1e-30f;
+}
+
+template <int MET, int RS>
+__global__ __launch_bounds__(kT) void mfma_screen_kernel(ScreenArgs a) {
+  extern __shared__ float sm[];
+  const int dim = a.dim;
+  float* qT = sm;                     // [dim][kSQ], dimension rows permuted as dataT
+  float* S = sm + dim * kSQ;          // [kSQ][kSRows] screening values of one step
+  float* qn_s = S + kSQ * kSRows;     // [kSQ]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const uint64_t q0 = (uint64_t)blockIdx.x * kSQ;
+  const uint32_t chunk = blockIdx.y;
+  for (int e = tid; e < kSQ * dim; e += kT) {
+    const int qq = e / dim;
+    const int d = e - qq * dim;
+    qT[perm_row(d, dim) * kSQ + qq] = (q0 + qq < a.nq) ? a.queries[(q0 + qq) * (uint64_t)dim + d] : 0.0f;
+  }
+  if (tid < kSQ) qn_s[tid] = (q0 + tid < a.nq) ? a.q_norm[q0 + tid] : 0.0f;
+  WaveTopK<RS> tk[kSQ / 4];
+#pragma unroll
+  for (int t = 0; t < kSQ / 4; ++t) tk[t].init(a.kp);
+  __syncthreads();
+  const int half = lane >> 5;
+  const int col = lane & 31;
+  const int kh = dim >> 1;  // lanes of half h take dimension rows h*kh .. h*kh+kh-1
+  const float* __restrict__ ap = qT + half * kh * kSQ + col;
+  const uint64_t r0 = (uint64_t)chunk * a.chunk_rows;
+  const uint64_t r1 = std::min<uint64_t>(a.n, r0 + a.chunk_rows);
+  for (uint64_t base = r0; base < r1; base += kSRows) {
+    const uint64_t row = base + wave * 32 + col;  // < ld: base < n, ld a multiple of 256
+    const float* __restrict__ bp = a.dataT + (uint64_t)half * kh * a.ld + row;
+    v16f acc = {};
+    int j = 0;
+    for (; j + 8 <= kh; j += 8) {  // 8 row loads in flight, then 8 products
+      float av[8], bv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        bv[u] = bp[(uint64_t)(j + u) * a.ld];
+        av[u] = ap[(j + u) * kSQ];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u], bv[u], acc, 0, 0, 0);
+    }
+    for (; j < kh; ++j)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ap[j * kSQ], bp[(uint64_t)j * a.ld], acc, 0, 0, 0);
+    const bool in = row < r1;
+    const float rn = in ? a.row_norm[row] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qi = 8 * (r >> 2) + 4 * half + (r & 3);  // D[qi][col] lives in register r
+      const float v = screen_value<MET>(acc[r], qn_s[qi], rn);
+      S[qi * kSRows + wave * 32 + col] = in ? v : f_inf();
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < kSQ / 4; ++t) {
+      const int qi = wave * (kSQ / 4) + t;
+#pragma unroll
+      for (int h2 = 0; h2 < kSRows / 64; ++h2) {
+        const uint64_t key = base + h2 * 64 + lane;
+        const bool ok = key < r1;
+        tk[t].offer(ok ? S[qi * kSRows + h2 * 64 + lane] : f_inf(), ok ? (uint32_t)key : kNoPos);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = 0; t < kSQ / 4; ++t) {
+    const uint64_t q = q0 + wave * (kSQ / 4) + t;
+    if (q >= a.nq) continue;
+    const uint64_t o = (q * a.nchunks + chunk) * (uint64_t)a.kp;
+#pragma unroll
+    for (int r = 0; r < RS; ++r) {
+      a.part_d[o + r * 64 + lane] = tk[t].d[r];
+      a.part_key[o + r * 64 + lane] = tk[t].p[r];
+    }
+  }
+}
+
+// One wave per query: exact reference-order distances of its K' = 64*RS
+// screened candidates, their k smallest (WaveTopK<RK>), and the check that
+// the candidates hold the exact top k: with a' the K'-th screening value
+// (every other row screens at a' or above, so its exact distance is at least
+// a' - eps), the list is final when a' - eps exceeds the k-th exact distance
+// (for Euclidean: the k-th squared distance times 1 + 8u, so that no
+// square root can round onto it).  Otherwise the query is flagged for the
+// exact scan.
+template <int MET, int RS, int RK>
+__global__ __launch_bounds__(64) void rescore_kernel(RescoreArgs a) {
+  extern __shared__ float qv[];  // [dim]
+  const uint64_t q = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int dim = a.dim;
+  for (int d = lane; d < dim; d += 64) qv[d] = a.queries[q * dim + d];
+  __syncthreads();
+  const int kp = 64 * RS;
+  const uint32_t cnt = a.cand_counts[q];
+  const float qn = a.q_norm[q];
+  constexpr int EM = (MET == FDB_METRIC_EUCLIDEAN) ? FDB_METRIC_EUCLIDEAN_SQUARED : MET;
+  WaveTopK<RK> tk;
+  tk.init(a.k);
+#pragma unroll
+  for (int r = 0; r < RS; ++r) {
+    const uint32_t s = r * 64 + lane;
+    const bool valid = s < cnt;
+    const uint32_t key = valid ? (uint32_t)a.cand_keys[q * kp + s] : kNoPos;
+    float e = f_inf();
+    if (valid) e = exact_lane<MET>(qv, a.rows + (uint64_t)key * dim, dim, qn, a.row_norm[key]);
+    tk.offer(e, key);
+  }
+  const uint32_t kk = (uint32_t)a.k < cnt ? (uint32_t)a.k : cnt;
+  bool ok = true;
+  if (cnt >= (uint32_t)kp && kk > 0) {
+    const float aK = a.cand_d[q * kp + kp - 1];
+    const int s = (int)kk - 1;
+    // the k-th exact pair, in the screening domain
+    float v = tk.d[0];
+    uint32_t w = tk.p[0];
+#pragma unroll
+    for (int r = 1; r < RK; ++r) {
+      const bool sel = r <= (s >> 6);
+      v = sel ? tk.d[r] : v;
+      w = sel ? tk.p[r] : w;
+    }
+    if constexpr (MET == FDB_METRIC_EUCLIDEAN) {
+      const uint32_t wk = readlane_u(w, s & 63);
+      float e2 = 0.0f;
+      if (lane == (s & 63)) e2 = exact_lane<EM>(qv, a.rows + (uint64_t)wk * dim, dim, qn, 0.0f);
+      v = readlane_f(e2, s & 63) * (1.0f + 8.0f * 5.9604645e-8f);
+    } else {
+      v = readlane_f(v, s & 63);
+    }
+    ok = aK - screen_eps(MET, dim, qn, a.rnmax) > v;
+  }
+  uint32_t count = 0;
+#pragma unroll
+  for (int r = 0; r < RK; ++r) {
+    const int s = r * 64 + lane;
+    const bool valid = s < a.k && tk.p[r] != kNoPos;
+    count += (uint32_t)__popcll(__ballot(valid));
+    if (s < a.k) {
+      a.out_ids[q * a.k + s] = valid ? a.ids[tk.p[r]] : ~0ull;
+      a.out_d[q * a.k + s] = valid ? tk.d[r] : f_inf();
+    }
+  }
+  if (lane == 0) {
+    a.out_counts[q] = count;
+    a.flags[q] = ok ? 0 : 1;
+    if (!ok) atomicAdd(a.fallbacks, 1u);
+  }
+}
+
 int regs_k(int k) {
   int r = (k + 63) / 64, p = 1;
   while (p < r) p <<= 1;
@@ -378,7 +610,20 @@ void* pick_metric(int metric, int R, bool ivf) {
   return nullptr;
 }
 
+template <int MET>
+void* pick_screen(int RS) {
+  return RS == 1 ? (void*)mfma_screen_kernel<MET, 1> : (void*)mfma_screen_kernel<MET, 2>;
+}
+
+template <int MET>
+void* pick_rescore(int RS, int RK) {
+  if (RS == 1) return (void*)rescore_kernel<MET, 1, 1>;
+  return RK == 1 ? (void*)rescore_kernel<MET, 2, 1> : (void*)rescore_kernel<MET, 2, 2>;
+}
+
 unsigned nblocks(uint64_t n, unsigned t) { return (unsigned)((n + t - 1) / t); }
+
+__global__ void clear_u32(uint32_t* p) { *p = 0; }
 
 __global__ void fill_empty(uint64_t n, uint32_t k, uint64_t* ids, float* d, uint32_t* c) {
   const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -428,11 +673,11 @@ hipError_t launch_flat_topk(const FlatTopkArgs& a, hipStream_t s) {
 
 hipError_t launch_merge_parts(const float* pd, const uint32_t* pk, uint64_t nq, uint32_t nparts, int k,
                               const uint64_t* ids, uint64_t* out_ids, float* out_d, uint32_t* out_c,
-                              hipStream_t s) {
+                              hipStream_t s, const int* flags) {
   if (nq == 0) return hipSuccess;
 #define FDB_MP(R)                                                                                 \
   hipLaunchKernelGGL(merge_parts_kernel<R>, dim3((unsigned)nq), dim3(64), 0, s, pd, pk, nq, nparts, \
-                     k, ids, out_ids, out_d, out_c);                                             \
+                     k, ids, out_ids, out_d, out_c, flags);                                      \
   break;
   switch (regs_k(k)) {
     case 1: FDB_MP(1)
@@ -444,6 +689,47 @@ hipError_t launch_merge_parts(const float* pd, const uint32_t* pk, uint64_t nq, 
   }
 #undef FDB_MP
   return hipGetLastError();
+}
+
+hipError_t launch_mfma_screen(const ScreenArgs& a, hipStream_t s) {
+  if (a.nq == 0 || a.nchunks == 0) return hipSuccess;
+  if ((a.kp != 64 && a.kp != 128) || a.dim <= 0 || a.dim > 512 || a.dim % 4 != 0 || a.ld % 256 != 0 ||
+      a.chunk_rows % 256 != 0)
+    return hipErrorInvalidValue;
+  const int RS = a.kp / 64;
+  void* fn = nullptr;
+  switch (a.metric) {
+    case FDB_METRIC_EUCLIDEAN:
+    case FDB_METRIC_EUCLIDEAN_SQUARED: fn = pick_screen<FDB_METRIC_EUCLIDEAN_SQUARED>(RS); break;
+    case FDB_METRIC_COSINE: fn = pick_screen<FDB_METRIC_COSINE>(RS); break;
+    case FDB_METRIC_DOT_PRODUCT: fn = pick_screen<FDB_METRIC_DOT_PRODUCT>(RS); break;
+    default: return hipErrorInvalidValue;
+  }
+  const size_t lds = sizeof(float) * ((size_t)a.dim * kSQ + kSQ * kSRows + kSQ);
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  void* args[] = {(void*)&a};
+  return hipLaunchKernel(fn, dim3((unsigned)((a.nq + kSQ - 1) / kSQ), a.nchunks), dim3(kT), args, lds, s);
+}
+
+hipError_t launch_rescore(const RescoreArgs& a, uint64_t nq, hipStream_t s) {
+  if (nq == 0) return hipSuccess;
+  if ((a.kp != 64 && a.kp != 128) || a.k <= 0 || a.k > a.kp || a.dim <= 0 || a.dim > 512 ||
+      a.dim % 4 != 0)
+    return hipErrorInvalidValue;
+  const int RS = a.kp / 64, RK = regs_k(a.k);
+  void* fn = nullptr;
+  switch (a.metric) {
+    case FDB_METRIC_EUCLIDEAN: fn = pick_rescore<FDB_METRIC_EUCLIDEAN>(RS, RK); break;
+    case FDB_METRIC_EUCLIDEAN_SQUARED: fn = pick_rescore<FDB_METRIC_EUCLIDEAN_SQUARED>(RS, RK); break;
+    case FDB_METRIC_COSINE: fn = pick_rescore<FDB_METRIC_COSINE>(RS, RK); break;
+    case FDB_METRIC_DOT_PRODUCT: fn = pick_rescore<FDB_METRIC_DOT_PRODUCT>(RS, RK); break;
+    default: return hipErrorInvalidValue;
+  }
+  void* args[] = {(void*)&a};
+  return hipLaunchKernel(fn, dim3((unsigned)nq), dim3(64), args, sizeof(float) * a.dim, s);
 }
 
 hipError_t launch_ivf_flat_scan(const IvfFlatScanArgs& a, hipStream_t s) {
@@ -504,16 +790,17 @@ void BruteForceIndex::sync_device() {
   const uint64_t n = h_ids_.size();
   ld_ = std::max<uint64_t>(256, (n + 255) / 256 * 256);
   if (n) {
-    DevBuf<float> d_rows;
-    d_rows.upload(h_rows_.data(), n * dim_, stream_);
+    rows_.upload(h_rows_.data(), n * dim_, stream_);
     dataT_.reserve(ld_ * dim_);
-    FDB_HIP(launch_transpose_rows(d_rows.p, n, (int)dim_, ld_, dataT_.p, stream_));
-    if (metric_ == FDB_METRIC_COSINE) {
-      row_norm_.reserve(n);
-      FDB_HIP(launch_row_norms(d_rows.p, n, (int)dim_, row_norm_.p, stream_));
-    }
+    FDB_HIP(launch_transpose_rows(rows_.p, n, (int)dim_, ld_, dataT_.p, stream_));
+    row_norm_.reserve(n);
+    FDB_HIP(launch_row_norms(rows_.p, n, (int)dim_, row_norm_.p, stream_));
     ids_.upload(h_ids_.data(), n, stream_);
+    std::vector<float> rn(n);
+    FDB_HIP(hipMemcpyAsync(rn.data(), row_norm_.p, 4 * n, hipMemcpyDeviceToHost, stream_));
     FDB_HIP(hipStreamSynchronize(stream_));
+    rnmax_ = 0.0f;
+    for (float v : rn) rnmax_ = std::max(rnmax_, v);  // NaN rows leave it unchanged
   }
   n_dev_ = n;
   dirty_ = false;
@@ -526,10 +813,22 @@ BruteForceIndex::~BruteForceIndex() {
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
+// Automatic mode screens when there are at least 2^26 (query, row) pairs;
+// below that the launch sequence costs more than the exact scan.
+bool BruteForceIndex::screen_applies(uint64_t nq, uint32_t k) const {
+  const bool shape = metric_ != FDB_METRIC_MANHATTAN && dim_ % 4 == 0 && dim_ <= 512 && k + 16 <= 128 &&
+                     n_dev_ > 64;
+  if (!shape || screen_mode_ == 1) return false;
+  return screen_mode_ == 2 || nq * n_dev_ >= (1ull << 26);
+}
+
 void BruteForceIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids,
                           float* d_dists, uint32_t* d_counts, hipStream_t s) {
   if (nq == 0) return;
   const uint64_t n = n_dev_;
+  fallbacks_.reserve(1);
+  hipLaunchKernelGGL(clear_u32, dim3(1), dim3(1), 0, s, fallbacks_.p);
+  FDB_HIP(hipGetLastError());
   if (k == 0 || n == 0) {
     hipLaunchKernelGGL(fill_empty, dim3(nblocks(nq * std::max<uint32_t>(k, 1), 256)), dim3(256), 0, s,
                        nq, k, d_ids, d_dists, d_counts);
@@ -537,14 +836,26 @@ void BruteForceIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* 
     return;
   }
   if (k > 1024) throw Error(FDB_ERR_UNSUPPORTED, "k above 1024");
-  if (metric_ == FDB_METRIC_COSINE) {
+  const bool screen = screen_applies(nq, k);
+  if (metric_ == FDB_METRIC_COSINE || screen) {
     qn_.reserve(nq);
     FDB_HIP(launch_row_norms(d_qs, nq, dim_, qn_.p, s));
   }
-  // Query slices of at most 65535 tiles (the grid's y limit).  Per slice,
-  // row chunks: enough workgroups to fill the GPU; the partial lists are
-  // capped at 512 MB in all and at 2^20 entries per query (one wave merges
-  // them).
+  if (screen) {
+    run_screen(d_qs, nq, k, d_ids, d_dists, d_counts, s);
+  } else {
+    run_exact(d_qs, nq, k, d_ids, d_dists, d_counts, s, nullptr);
+  }
+}
+
+// Exact VALU scan.  With flags, only queries flagged nonzero are rewritten
+// (the fallback of the screening path).  Query slices of at most 65535 tiles
+// (the grid's y limit).  Per slice, row chunks: enough workgroups to fill the
+// GPU; the partial lists are capped at 512 MB in all and at 2^20 entries per
+// query (one wave merges them).
+void BruteForceIndex::run_exact(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids,
+                                float* d_dists, uint32_t* d_counts, hipStream_t s, const int* flags) {
+  const uint64_t n = n_dev_;
   const uint64_t slice = 65535ull * kQB;
   for (uint64_t q0 = 0; q0 < nq; q0 += slice) {
     const uint64_t m = std::min(slice, nq - q0);
@@ -573,10 +884,84 @@ void BruteForceIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* 
     a.k = (int)k;
     a.part_d = part_d_.p;
     a.part_key = part_k_.p;
+    a.flags = flags ? flags + q0 : nullptr;
     FDB_HIP(launch_flat_topk(a, s));
     FDB_HIP(launch_merge_parts(part_d_.p, part_k_.p, m, nchunks, (int)k, ids_.p, d_ids + q0 * k,
-                               d_dists + q0 * k, d_counts + q0, s));
+                               d_dists + q0 * k, d_counts + q0, s, a.flags));
   }
+}
+
+// MFMA screening, exact rescoring of K' candidates, exact scan of the
+// queries whose check failed.  Query slices of at most 65536; per slice,
+// row chunks for about 2048 workgroups, partial lists capped at 512 MB.
+void BruteForceIndex::run_screen(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids,
+                                 float* d_dists, uint32_t* d_counts, hipStream_t s) {
+  const uint64_t n = n_dev_;
+  const int kp = (k + 16 <= 64) ? 64 : 128;
+  flags_.reserve(nq);
+  const uint64_t slice = 65536;
+  for (uint64_t q0 = 0; q0 < nq; q0 += slice) {
+    const uint64_t m = std::min(slice, nq - q0);
+    const uint64_t qtiles = (m + kSQ - 1) / kSQ;
+    uint64_t want = std::max<uint64_t>(1, 2048 / qtiles);
+    want = std::min<uint64_t>(want, std::max<uint64_t>(1, (512ull << 20) / (m * kp * 8)));
+    uint64_t chunk_rows = (n + want - 1) / want;
+    chunk_rows = std::max<uint64_t>(256, (chunk_rows + 255) / 256 * 256);
+    const uint32_t nchunks = (uint32_t)((n + chunk_rows - 1) / chunk_rows);
+    part_d_.reserve(m * nchunks * kp);
+    part_k_.reserve(m * nchunks * kp);
+    cand_d_.reserve(m * kp);
+    cand_k_.reserve(m * kp);
+    cand_c_.reserve(m);
+    ScreenArgs a{};
+    a.queries = d_qs + q0 * dim_;
+    a.nq = m;
+    a.dim = (int)dim_;
+    a.dataT = dataT_.p;
+    a.ld = ld_;
+    a.n = n;
+    a.row_norm = row_norm_.p;
+    a.q_norm = qn_.p + q0;
+    a.chunk_rows = chunk_rows;
+    a.nchunks = nchunks;
+    a.metric = (int)metric_;
+    a.kp = kp;
+    a.part_d = part_d_.p;
+    a.part_key = part_k_.p;
+    FDB_HIP(launch_mfma_screen(a, s));
+    FDB_HIP(launch_merge_parts(part_d_.p, part_k_.p, m, nchunks, kp, nullptr, cand_k_.p, cand_d_.p,
+                               cand_c_.p, s));
+    RescoreArgs r{};
+    r.queries = a.queries;
+    r.dim = (int)dim_;
+    r.rows = rows_.p;
+    r.row_norm = row_norm_.p;
+    r.q_norm = a.q_norm;
+    r.rnmax = rnmax_;
+    r.cand_keys = cand_k_.p;
+    r.cand_d = cand_d_.p;
+    r.cand_counts = cand_c_.p;
+    r.kp = kp;
+    r.metric = (int)metric_;
+    r.k = (int)k;
+    r.ids = ids_.p;
+    r.out_ids = d_ids + q0 * k;
+    r.out_d = d_dists + q0 * k;
+    r.out_counts = d_counts + q0;
+    r.flags = flags_.p + q0;
+    r.fallbacks = fallbacks_.p;
+    FDB_HIP(launch_rescore(r, m, s));
+  }
+  run_exact(d_qs, nq, k, d_ids, d_dists, d_counts, s, flags_.p);
+}
+
+uint64_t BruteForceIndex::last_fallbacks(hipStream_t s) {
+  std::lock_guard<std::mutex> g(mu_);
+  if (!fallbacks_.p) return 0;
+  FDB_HIP(hipStreamSynchronize(s ? s : stream_));
+  uint32_t v = 0;
+  FDB_HIP(hipMemcpy(&v, fallbacks_.p, 4, hipMemcpyDeviceToHost));
+  return v;
 }
 
 uint32_t BruteForceIndex::search(const float* q, uint32_t k, uint64_t* ids, float* dists) {

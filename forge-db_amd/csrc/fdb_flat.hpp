@@ -37,14 +37,61 @@ struct FlatTopkArgs {
   int k;
   float* part_d;
   uint32_t* part_key;
+  const int* flags;  // nullable: [nq]; tiles without a nonzero flag return at once
 };
 hipError_t launch_flat_topk(const FlatTopkArgs& a, hipStream_t s);
 
 // Merge [nq][nparts][k] partial lists into [nq][k] ascending (ties: smaller
 // key), keys mapped to ids through ids (nullable: keys are the ids).
+// flags (nullable): only queries with a nonzero flag are written.
 hipError_t launch_merge_parts(const float* part_d, const uint32_t* part_key, uint64_t nq,
                               uint32_t nparts, int k, const uint64_t* ids, uint64_t* out_ids,
-                              float* out_d, uint32_t* out_counts, hipStream_t s);
+                              float* out_d, uint32_t* out_counts, hipStream_t s,
+                              const int* flags = nullptr);
+
+// MFMA screening (dot, cosine, squared L2): per (32-query tile, row chunk)
+// the K' = kp smallest screening values; grid x = query tiles, y = chunks.
+struct ScreenArgs {
+  const float* queries;  // [nq][dim]
+  uint64_t nq;
+  int dim;  // a multiple of 4, <= 512
+  const float* dataT;
+  uint64_t ld, n;
+  const float* row_norm;  // [n] reference-order squared norms
+  const float* q_norm;    // [nq]
+  uint64_t chunk_rows;    // a multiple of 256
+  uint32_t nchunks;
+  int metric;
+  int kp;  // 64 or 128
+  float* part_d;
+  uint32_t* part_key;
+};
+hipError_t launch_mfma_screen(const ScreenArgs& a, hipStream_t s);
+
+// Exact rescoring of screened candidates ([nq][kp], ascending, as merged):
+// writes the k smallest exact results, flags [nq] (1 = the candidates may
+// miss a top-k row) and adds the number of flagged queries to *fallbacks.
+struct RescoreArgs {
+  const float* queries;
+  int dim;
+  const float* rows;  // [n][dim] row-major
+  const float* row_norm;
+  const float* q_norm;
+  float rnmax;  // the largest row norm (squared)
+  const uint64_t* cand_keys;
+  const float* cand_d;
+  const uint32_t* cand_counts;
+  int kp;
+  int metric;
+  int k;
+  const uint64_t* ids;
+  uint64_t* out_ids;
+  float* out_d;
+  uint32_t* out_counts;
+  int* flags;
+  uint32_t* fallbacks;
+};
+hipError_t launch_rescore(const RescoreArgs& a, uint64_t nq, hipStream_t s);
 
 // IVF-flat scan: per query, probes [nq][np] lists of list-blocked data
 // (list p: block [dim][lld_p] at boff[p] floats, rows start at row_off[p]).
@@ -98,10 +145,23 @@ class BruteForceIndex {
   void batch_search_device(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids,
                            float* d_dists, uint32_t* d_counts, hipStream_t s, float* ms = nullptr);
 
+  // 0 = automatic (MFMA screening where it applies), 1 = exact VALU scan
+  // only, 2 = screening where it applies
+  void set_screen_mode(int m) { screen_mode_ = m; }
+  int screen_mode() const { return screen_mode_; }
+  // queries of the last search that the screening check sent to the exact
+  // scan (waits for the stream s, null: own stream)
+  uint64_t last_fallbacks(hipStream_t s);
+
  private:
   void sync_device();  // re-uploads the rows after add/remove (caller holds mu_)
   void run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids, float* d_dists,
            uint32_t* d_counts, hipStream_t s);
+  void run_exact(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids, float* d_dists,
+                 uint32_t* d_counts, hipStream_t s, const int* flags);
+  void run_screen(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids, float* d_dists,
+                  uint32_t* d_counts, hipStream_t s);
+  bool screen_applies(uint64_t nq, uint32_t k) const;
 
   uint32_t dim_ = 0, metric_;
   std::vector<float> h_rows_;
@@ -110,13 +170,17 @@ class BruteForceIndex {
   uint64_t n_dev_ = 0;  // rows resident on the device
   hipStream_t stream_ = nullptr;
   std::mutex mu_;
-  DevBuf<float> dataT_, row_norm_;
+  DevBuf<float> dataT_, row_norm_, rows_;
   DevBuf<uint64_t> ids_;
   uint64_t ld_ = 0;
+  float rnmax_ = 0.0f;
+  int screen_mode_ = 0;
   // scratch
-  DevBuf<float> q_, qn_, part_d_, out_d_;
-  DevBuf<uint32_t> part_k_, out_c_;
-  DevBuf<uint64_t> out_i_;
+  DevBuf<float> q_, qn_, part_d_, out_d_, cand_d_;
+  DevBuf<uint32_t> part_k_, out_c_, cand_c_;
+  DevBuf<uint64_t> out_i_, cand_k_;
+  DevBuf<int> flags_;
+  DevBuf<uint32_t> fallbacks_;
   hipEvent_t ev_[2] = {nullptr, nullptr};
 };
 

@@ -224,6 +224,22 @@ FDB_API fdb_status fdb_bf_batch_search_device(fdb_bf* index, const float* d_quer
                                               uint32_t k, uint64_t* d_out_ids, float* d_out_dists,
                                               uint32_t* d_out_counts, void* hip_stream, float* ms);
 
+/* Search strategy (no counterpart in the reference, whose scan is one
+ * loop):
+ *   FDB_BF_AUTO (default) and FDB_BF_SCREEN: for dot product, cosine and
+ *     (squared) Euclidean with dim a multiple of 4 (<= 512) and k <= 112,
+ *     an MFMA fp32 pass screens K' = 64 or 128 candidates per query, their
+ *     distances are recomputed exactly in the reference's order, and a
+ *     rounding-error bound proves that no other row can enter the top k;
+ *     queries where it cannot be proved are rescanned exactly.  Results are
+ *     identical to FDB_BF_EXACT.
+ *   FDB_BF_EXACT: the exact-order VALU scan for every query.
+ * fdb_bf_last_fallbacks reports how many queries of the last search were
+ * rescanned (it waits for hip_stream; NULL = the handle's own stream). */
+enum { FDB_BF_AUTO = 0, FDB_BF_EXACT = 1, FDB_BF_SCREEN = 2 };
+FDB_API fdb_status fdb_bf_set_search_mode(fdb_bf* index, uint32_t mode);
+FDB_API fdb_status fdb_bf_last_fallbacks(fdb_bf* index, void* hip_stream, uint64_t* out);
+
 /* ------------------------------------------------------------------------ */
 /* IVF (full vectors): src/index/ivf.rs                                     */
 /* ------------------------------------------------------------------------ */

@@ -16,7 +16,8 @@ import pytest
 
 import refcpu
 
-from forgedb import BruteForceIndex, DistanceMetric, ForgeDbError, IVFIndex, datagen
+from forgedb import (BF_EXACT, BF_SCREEN, BruteForceIndex, DistanceMetric, ForgeDbError, IVFIndex,
+                     datagen)
 
 pytestmark = pytest.mark.gpu
 
@@ -33,8 +34,13 @@ def check_rows(gi, gd, gc, oi, od, oc, label):
         assert np.all(gi[q, c:] == NO_ID) and np.all(np.isinf(gd[q, c:]))
 
 
-def bf_pair(rows, ids, metric, queries, k):
-    g = BruteForceIndex.from_arrays(rows, ids, metric)
+MODES = [BF_EXACT, BF_SCREEN]
+MODE_IDS = ["exact", "screen"]
+
+
+def bf_pair(rows, ids, metric, queries, k, mode=BF_EXACT, index=None):
+    g = index or BruteForceIndex.from_arrays(rows, ids, metric)
+    g.set_search_mode(mode)
     out = g.batch_search_arrays(queries, k)
     ref = refcpu.bf_batch_search(rows, ids, int(metric), queries, k)
     return out, ref
@@ -46,21 +52,51 @@ def bf_small():
     return base, queries, np.arange(len(base), dtype=np.uint64)
 
 
+@pytest.mark.parametrize("mode", MODES, ids=MODE_IDS)
 @pytest.mark.parametrize("metric", METRICS, ids=[m.name for m in METRICS])
-def test_bf_small_parity(bf_small, metric):
-    print(f"bf 10k x 128, 100 queries, k 10, {metric.name}", flush=True)
+def test_bf_small_parity(bf_small, metric, mode):
+    print(f"bf 10k x 128, 100 queries, k 10, {metric.name}, mode {mode}", flush=True)
     base, queries, ids = bf_small
-    (gi, gd, gc), (oi, od, oc) = bf_pair(base, ids, metric, queries, 10)
+    (gi, gd, gc), (oi, od, oc) = bf_pair(base, ids, metric, queries, 10, mode)
     check_rows(gi, gd, gc, oi, od, oc, metric.name)
 
 
-@pytest.mark.parametrize("metric", [DistanceMetric.Cosine, DistanceMetric.DotProduct])
-def test_bf_normalised_parity(metric):
-    print(f"bf normalised 60k x 128, 48 queries, k 100, {metric.name}", flush=True)
-    base, queries = datagen.workload("bf_norm", n=60_000, nq=48)
+@pytest.mark.parametrize("mode", MODES, ids=MODE_IDS)
+@pytest.mark.parametrize("metric", [DistanceMetric.Cosine, DistanceMetric.DotProduct,
+                                    DistanceMetric.Euclidean])
+def test_bf_normalised_parity(metric, mode):
+    print(f"bf normalised 60k x 128, 200 queries, k 100, {metric.name}, mode {mode}", flush=True)
+    base, queries = datagen.workload("bf_norm", n=60_000, nq=200)
     ids = np.arange(len(base), dtype=np.uint64) * 3 + 7
-    (gi, gd, gc), (oi, od, oc) = bf_pair(base, ids, metric, queries, 100)
+    g = BruteForceIndex.from_arrays(base, ids, metric)
+    (gi, gd, gc), (oi, od, oc) = bf_pair(base, ids, metric, queries, 100, mode, index=g)
     check_rows(gi, gd, gc, oi, od, oc, metric.name)
+    if mode == BF_SCREEN:
+        fb = g.last_fallbacks()
+        print(f"  screening fallbacks: {fb} of 200", flush=True)
+        assert fb < 20  # the screen decides nearly every query by itself
+
+
+def test_bf_screen_fallback_on_near_ties():
+    print("bf screening: near-tied rows force the exact rescan", flush=True)
+    dim = 64
+    q = np.zeros(dim, np.float32)
+    q[0] = 1.0
+    ids = np.arange(4000, dtype=np.uint64)
+    for metric in (DistanceMetric.Cosine, DistanceMetric.DotProduct, DistanceMetric.EuclideanSquared):
+        # 300 rows within 1e-4 of scale * q: their distances to q differ by
+        # far less than the screening error bound
+        rng = np.random.default_rng(12)
+        rows = rng.standard_normal((4000, dim)).astype(np.float32)
+        scale = 10.0 if metric == DistanceMetric.DotProduct else 1.0
+        near = np.tile(q * scale, (300, 1))
+        near[np.arange(300), rng.integers(1, dim, 300)] = rng.uniform(-1e-4, 1e-4, 300)
+        rows[rng.choice(4000, 300, replace=False)] = near
+        queries = np.stack([q, rows[5]])
+        g = BruteForceIndex.from_arrays(rows, ids, metric)
+        (gi, gd, gc), (oi, od, oc) = bf_pair(rows, ids, metric, queries, 20, BF_SCREEN, index=g)
+        check_rows(gi, gd, gc, oi, od, oc, f"near ties {metric.name}")
+        assert g.last_fallbacks() >= 1, metric.name
 
 
 @pytest.mark.parametrize("dim,n,nq,k", [(1, 300, 5, 4), (7, 1000, 17, 64), (8, 513, 3, 65),
@@ -74,8 +110,10 @@ def test_bf_shapes(dim, n, nq, k):
     queries = rng.standard_normal((nq, dim)).astype(np.float32)
     ids = rng.permutation(n).astype(np.uint64)
     for metric in METRICS:
-        (gi, gd, gc), (oi, od, oc) = bf_pair(rows, ids, metric, queries, k)
-        check_rows(gi, gd, gc, oi, od, oc, f"dim{dim} {metric.name}")
+        g = BruteForceIndex.from_arrays(rows, ids, metric)
+        for mode in MODES:
+            (gi, gd, gc), (oi, od, oc) = bf_pair(rows, ids, metric, queries, k, mode, index=g)
+            check_rows(gi, gd, gc, oi, od, oc, f"dim{dim} {metric.name} mode {mode}")
 
 
 def test_bf_ties_keep_the_earlier_row():
@@ -86,8 +124,10 @@ def test_bf_ties_keep_the_earlier_row():
     queries = uniq[:10]
     ids = np.arange(5000, dtype=np.uint64)
     for metric in METRICS:
-        (gi, gd, gc), (oi, od, oc) = bf_pair(rows, ids, metric, queries, 50)
-        check_rows(gi, gd, gc, oi, od, oc, f"ties {metric.name}")
+        g = BruteForceIndex.from_arrays(rows, ids, metric)
+        for mode in MODES:
+            (gi, gd, gc), (oi, od, oc) = bf_pair(rows, ids, metric, queries, 50, mode, index=g)
+            check_rows(gi, gd, gc, oi, od, oc, f"ties {metric.name} mode {mode}")
 
 
 def test_bf_single_search_and_kat():
