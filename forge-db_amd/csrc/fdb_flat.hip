@@ -473,6 +473,7 @@ __global__ __launch_bounds__(kT) void mfma_screen_kernel(ScreenArgs a) {
 #pragma unroll
     for (int t = 0; t < kSQ / 4; ++t) {
       const int qi = wave * (kSQ / 4) + t;
+      if (q0 + qi >= a.nq) break;  // padding queries of the last tile
 #pragma unroll
       for (int h2 = 0; h2 < kSRows / 64; ++h2) {
         const uint64_t key = base + h2 * 64 + lane;
