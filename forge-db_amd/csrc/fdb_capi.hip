@@ -294,6 +294,45 @@ fdb_status fdb_ivfpq_encode(fdb_ivfpq* h, const float* residuals, uint64_t nq, u
   });
 }
 
+fdb_status fdb_ivfpq_search_filtered(fdb_ivfpq* h, const float* queries, uint64_t nq, uint32_t dim,
+                                     uint32_t k, const uint64_t* allowed, uint64_t n_allowed,
+                                     uint64_t* out_ids, float* out_dists, uint32_t* out_counts) {
+  return guarded([&] {
+    IvfPqIndex* ix = H(h);
+    if (nq && (!queries || !out_counts || (k && (!out_ids || !out_dists))))
+      throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    if (n_allowed && !allowed) throw Error(FDB_ERR_INVALID_ARGUMENT, "null allowed ids");
+    if (dim != ix->dim()) throw Error(FDB_ERR_DIMENSION_MISMATCH, "query dimension does not match the index");
+    ix->search_filtered(queries, nq, k, allowed, n_allowed, out_ids, out_dists, out_counts);
+  });
+}
+
+fdb_status fdb_ivfpq_delete(fdb_ivfpq* h, uint64_t id, int* deleted) {
+  return guarded([&] {
+    const bool r = H(h)->remove(id);
+    if (deleted) *deleted = r ? 1 : 0;
+  });
+}
+
+fdb_status fdb_ivfpq_insert(fdb_ivfpq* h, const float* vectors, const uint64_t* ids, uint64_t n,
+                            uint32_t dim) {
+  return guarded([&] {
+    IvfPqIndex* ix = H(h);
+    if (n && !vectors) throw Error(FDB_ERR_INVALID_ARGUMENT, "null vectors");
+    if (dim != ix->dim()) throw Error(FDB_ERR_DIMENSION_MISMATCH, "vector dimension does not match the index");
+    ix->insert(vectors, ids, n);
+  });
+}
+
+fdb_status fdb_ivfpq_compact(fdb_ivfpq* h) {
+  return guarded([&] { H(h)->compact(); });
+}
+
+uint64_t fdb_ivfpq_len(const fdb_ivfpq* h) { return (h && h->impl) ? h->impl->live_len() : 0; }
+uint64_t fdb_ivfpq_num_tombstones(const fdb_ivfpq* h) {
+  return (h && h->impl) ? h->impl->num_tombstones() : 0;
+}
+
 /* ---- brute force ---------------------------------------------------------- */
 
 fdb_status fdb_bf_create(uint32_t metric, fdb_bf** out) {

@@ -110,6 +110,29 @@ hipError_t launch_rerank(const float* queries, uint64_t nq, int dim, const float
 
 unsigned blocks_for(uint64_t n, unsigned t) { return (unsigned)((n + t - 1) / t); }
 
+// The first k of fetch_k sorted candidates per query (the reference's
+// truncate(k) after sorting its candidate heap).
+__global__ void truncate_kernel(const uint64_t* __restrict__ cid, const float* __restrict__ cd,
+                                const uint32_t* __restrict__ ccnt, uint64_t nq, uint32_t fetch_k,
+                                uint32_t k, uint64_t* __restrict__ ids, float* __restrict__ d,
+                                uint32_t* __restrict__ cnt) {
+  const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= nq * k) return;
+  const uint64_t q = e / k, s = e - q * k;
+  ids[e] = cid[q * fetch_k + s];
+  d[e] = cd[q * fetch_k + s];
+  if (s == 0) cnt[q] = ccnt[q] < k ? ccnt[q] : k;
+}
+
+hipError_t launch_truncate(const uint64_t* cid, const float* cd, const uint32_t* ccnt, uint64_t nq,
+                           uint32_t fetch_k, uint32_t k, uint64_t* ids, float* d, uint32_t* cnt,
+                           hipStream_t s) {
+  if (nq == 0 || k == 0) return hipSuccess;
+  hipLaunchKernelGGL(truncate_kernel, dim3(blocks_for(nq * k, 256)), dim3(256), 0, s, cid, cd, ccnt, nq,
+                     fetch_k, k, ids, d, cnt);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 // Members of each cluster in ascending point order (a stable counting sort).
@@ -217,15 +240,186 @@ IvfPqIndex::IvfPqIndex(IvfPqArtifacts&& art) : host_(std::move(art)) {
   codebooks_.upload(host_.codebooks.data(), host_.codebooks.size(), stream_);
   cbnorm_.reserve((size_t)host_.M * 256);
   FDB_HIP(launch_codebook_norms(codebooks_.p, host_.M, host_.dsub, cbnorm_.p, stream_));
-  std::vector<uint32_t> off32(host_.offsets.begin(), host_.offsets.end());
-  off_.upload(off32.data(), off32.size(), stream_);
-  codes_.upload(host_.codes.data(), std::max<size_t>(host_.codes.size(), 16), stream_);
-  ids_.upload(host_.ids.data(), std::max<size_t>(host_.ids.size(), 1), stream_);
-  if (host_.has_originals) originals_.upload(host_.originals.data(), host_.originals.size(), stream_);
+  tomb_.assign(host_.nlist, {});
+  upload_lists();
   err_.reserve(1);
   hipLaunchKernelGGL(clear_int_kernel, dim3(1), dim3(1), 0, stream_, err_.p);
   FDB_HIP(hipGetLastError());
   FDB_HIP(hipStreamSynchronize(stream_));
+}
+
+void IvfPqIndex::upload_lists() {
+  std::vector<uint32_t> off32(host_.offsets.begin(), host_.offsets.end());
+  off_.upload(off32.data(), off32.size(), stream_);
+  codes_.reserve(std::max<size_t>(host_.codes.size(), 16));
+  if (!host_.codes.empty())
+    FDB_HIP(hipMemcpyAsync(codes_.p, host_.codes.data(), host_.codes.size(), hipMemcpyHostToDevice,
+                           stream_));
+  ids_.upload(host_.ids.data(), std::max<size_t>(host_.ids.size(), 1), stream_);
+  if (host_.has_originals && !host_.originals.empty())
+    originals_.upload(host_.originals.data(), host_.originals.size(), stream_);
+  live_dirty_ = true;
+  FDB_HIP(hipStreamSynchronize(stream_));
+}
+
+const uint32_t* IvfPqIndex::live_bitmap() {
+  if (n_tomb_ == 0) return nullptr;
+  if (live_dirty_) {
+    const uint64_t N = host_.ids.size();
+    std::vector<uint32_t> bits((N + 31) / 32, 0xFFFFFFFFu);
+    for (uint32_t l = 0; l < host_.nlist; ++l) {
+      if (tomb_[l].empty()) continue;
+      for (uint64_t p = host_.offsets[l]; p < host_.offsets[l + 1]; ++p)
+        if (tomb_[l].count(host_.ids[p])) bits[p >> 5] &= ~(1u << (p & 31));
+    }
+    live_.upload(bits.data(), std::max<size_t>(bits.size(), 1), stream_);
+    FDB_HIP(hipStreamSynchronize(stream_));
+    live_dirty_ = false;
+  }
+  return live_.p;
+}
+
+void IvfPqIndex::throw_if_nan() {
+  int flag = 0;
+  FDB_HIP(hipMemcpy(&flag, err_.p, 4, hipMemcpyDeviceToHost));
+  if (flag) {
+    hipLaunchKernelGGL(clear_int_kernel, dim3(1), dim3(1), 0, stream_, err_.p);
+    FDB_HIP(hipStreamSynchronize(stream_));
+    throw Error(FDB_ERR_NAN, "NaN centroid distance (a query contains NaN)");
+  }
+}
+
+bool IvfPqIndex::remove(uint64_t id) {
+  std::lock_guard<std::mutex> g(mu_);
+  for (uint32_t l = 0; l < host_.nlist; ++l) {
+    if (tomb_[l].count(id)) continue;
+    for (uint64_t p = host_.offsets[l]; p < host_.offsets[l + 1]; ++p)
+      if (host_.ids[p] == id) {
+        tomb_[l].insert(id);
+        ++n_tomb_;
+        live_dirty_ = true;
+        return true;
+      }
+  }
+  return false;
+}
+
+void IvfPqIndex::compact() {
+  std::lock_guard<std::mutex> g(mu_);
+  if (n_tomb_ == 0) return;
+  const uint32_t M = host_.M, dim = host_.dim;
+  std::vector<uint64_t> offs(host_.nlist + 1, 0), ids;
+  std::vector<uint8_t> codes;
+  std::vector<float> orig;
+  ids.reserve(host_.ids.size());
+  codes.reserve(host_.codes.size());
+  for (uint32_t l = 0; l < host_.nlist; ++l) {
+    for (uint64_t p = host_.offsets[l]; p < host_.offsets[l + 1]; ++p) {
+      if (tomb_[l].count(host_.ids[p])) continue;
+      ids.push_back(host_.ids[p]);
+      codes.insert(codes.end(), &host_.codes[p * M], &host_.codes[p * M] + M);
+      if (host_.has_originals)
+        orig.insert(orig.end(), &host_.originals[p * dim], &host_.originals[p * dim] + dim);
+    }
+    offs[l + 1] = ids.size();
+    tomb_[l].clear();
+  }
+  host_.offsets.swap(offs);
+  host_.ids.swap(ids);
+  host_.codes.swap(codes);
+  if (host_.has_originals) host_.originals.swap(orig);
+  n_tomb_ = 0;
+  upload_lists();
+}
+
+void IvfPqIndex::insert(const float* vectors, const uint64_t* ids, uint64_t n) {
+  if (n == 0) return;
+  std::lock_guard<std::mutex> g(mu_);
+  const uint32_t M = host_.M, dim = host_.dim;
+  for (uint64_t i = 0; i < n * dim; ++i)
+    if (std::isnan(vectors[i])) throw Error(FDB_ERR_NAN, "NaN in the vectors to insert");
+  if (host_.ids.size() + n >= 0xFFFFFFFFull) throw Error(FDB_ERR_UNSUPPORTED, "more than 2^32-2 vectors");
+  // nearest list (first minimum) and the residual code, on the GPU
+  DevBuf<float> d_vec;
+  DevBuf<int32_t> d_assign;
+  DevBuf<uint64_t> d_rows;
+  DevBuf<uint8_t> d_codes;
+  std::vector<uint64_t> rows(n);
+  for (uint64_t i = 0; i < n; ++i) rows[i] = i;
+  d_vec.upload(vectors, n * dim, stream_);
+  d_rows.upload(rows.data(), n, stream_);
+  d_assign.reserve(n);
+  d_codes.reserve(n * M);
+  FDB_HIP(launch_assign(d_vec.p, n, dim, centT_.p, host_.nlist, d_assign.p, stream_));
+  FDB_HIP(launch_pq_encode(d_vec.p, d_rows.p, d_assign.p, n, dim, centroids_.p, codebooks_.p, M,
+                           host_.dsub, d_codes.p, stream_));
+  std::vector<int32_t> assign(n);
+  std::vector<uint8_t> newc(n * M);
+  FDB_HIP(hipMemcpyAsync(assign.data(), d_assign.p, 4 * n, hipMemcpyDeviceToHost, stream_));
+  FDB_HIP(hipMemcpyAsync(newc.data(), d_codes.p, n * M, hipMemcpyDeviceToHost, stream_));
+  FDB_HIP(hipStreamSynchronize(stream_));
+  // each list: its old entries, then the new ones in input order
+  std::vector<uint32_t> off, members;
+  group_members(assign, (int)host_.nlist, off, members);
+  std::vector<uint64_t> offs(host_.nlist + 1, 0), nids;
+  std::vector<uint8_t> codes;
+  std::vector<float> orig;
+  nids.reserve(host_.ids.size() + n);
+  codes.reserve(host_.codes.size() + n * M);
+  for (uint32_t l = 0; l < host_.nlist; ++l) {
+    const uint64_t s = host_.offsets[l], e = host_.offsets[l + 1];
+    nids.insert(nids.end(), host_.ids.begin() + s, host_.ids.begin() + e);
+    codes.insert(codes.end(), host_.codes.begin() + s * M, host_.codes.begin() + e * M);
+    if (host_.has_originals)
+      orig.insert(orig.end(), host_.originals.begin() + s * dim, host_.originals.begin() + e * dim);
+    for (uint32_t t = off[l]; t < off[l + 1]; ++t) {
+      const uint64_t i = members[t];
+      const uint64_t id = ids ? ids[i] : host_.ids.size() + i;
+      nids.push_back(id);
+      codes.insert(codes.end(), &newc[i * M], &newc[i * M] + M);
+      if (host_.has_originals) orig.insert(orig.end(), vectors + i * dim, vectors + (i + 1) * dim);
+      n_tomb_ -= tomb_[l].erase(id);
+    }
+    offs[l + 1] = nids.size();
+  }
+  host_.offsets.swap(offs);
+  host_.ids.swap(nids);
+  host_.codes.swap(codes);
+  if (host_.has_originals) host_.originals.swap(orig);
+  upload_lists();
+}
+
+void IvfPqIndex::search_filtered(const float* qs, uint64_t nq, uint32_t k, const uint64_t* allowed,
+                                 uint64_t n_allowed, uint64_t* ids, float* dists, uint32_t* counts) {
+  if (nq == 0) return;
+  std::lock_guard<std::mutex> g(mu_);
+  const uint32_t kk = std::max<uint32_t>(k, 1);
+  out_ids_.reserve(nq * kk);
+  out_d_.reserve(nq * kk);
+  out_cnt_.reserve(nq);
+  // search_filtered probes take(nprobe): 0 lists when nprobe is 0 (:717-731);
+  // no allowed id: no results (:700-703)
+  uint32_t np = (uint32_t)std::min<uint64_t>(nprobe(), host_.nlist);
+  if (n_allowed == 0) np = 0;
+  q_.upload(qs, nq * host_.dim, stream_);
+  const uint32_t* live = live_bitmap();
+  const uint64_t N = host_.ids.size();
+  if (np > 0) {
+    std::vector<uint64_t> sorted(allowed, allowed + n_allowed);
+    std::sort(sorted.begin(), sorted.end());
+    allow_.upload(sorted.data(), sorted.size(), stream_);
+    filt_.reserve(std::max<uint64_t>((N + 31) / 32, 1));
+    FDB_HIP(launch_filter_bitmap(ids_.p, N, allow_.p, n_allowed, live, filt_.p, stream_));
+  }
+  run(q_.p, nq, k, np, kAdcGroups4, out_ids_.p, out_d_.p, out_cnt_.p, stream_, nullptr, nullptr,
+      filt_.p, 4);
+  if (k) {
+    FDB_HIP(hipMemcpyAsync(ids, out_ids_.p, 8 * nq * k, hipMemcpyDeviceToHost, stream_));
+    FDB_HIP(hipMemcpyAsync(dists, out_d_.p, 4 * nq * k, hipMemcpyDeviceToHost, stream_));
+  }
+  FDB_HIP(hipMemcpyAsync(counts, out_cnt_.p, 4 * nq, hipMemcpyDeviceToHost, stream_));
+  FDB_HIP(hipStreamSynchronize(stream_));
+  throw_if_nan();
 }
 
 IvfPqIndex::~IvfPqIndex() {
@@ -254,7 +448,7 @@ void IvfPqIndex::enable_reranking(const float* v, uint64_t factor) {
 
 void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, int order,
                      uint64_t* d_ids, float* d_dists, uint32_t* d_counts, hipStream_t s,
-                     float* coarse_ms, float* scan_ms) {
+                     float* coarse_ms, float* scan_ms, const uint32_t* live, uint32_t fetch_mult) {
   if (nq == 0) return;
   if (k == 0 || np == 0) {
     hipLaunchKernelGGL(fill_empty_kernel, dim3(blocks_for(nq * std::max<uint32_t>(k, 1), 256)),
@@ -265,8 +459,10 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
     return;
   }
   const bool rerank = host_.has_originals;
-  const uint64_t fetch = rerank ? (uint64_t)k * host_.rerank_factor : k;
-  if (fetch > 1024) throw Error(FDB_ERR_UNSUPPORTED, "k * rerank_factor above 1024");
+  const uint64_t fetch = (rerank ? (uint64_t)k * host_.rerank_factor : k) * fetch_mult;
+  if (fetch > 1024) throw Error(FDB_ERR_UNSUPPORTED, "candidates per query (k * rerank factor) above 1024");
+  // without reranking the kept candidates are truncated to k below
+  const bool trunc = !rerank && fetch > k;
   if (np > 1024 && np < host_.nlist) throw Error(FDB_ERR_UNSUPPORTED, "nprobe above 1024");
   probes_.reserve(nq * np);
   const bool timed = coarse_ms || scan_ms;
@@ -302,7 +498,8 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
   a.order = order;
   a.lut_mode = lut_mode();
   a.cbnorm = cbnorm_.p;
-  if (rerank) {
+  a.live = live;
+  if (rerank || trunc) {
     cand_ids_.reserve(nq * fetch);
     cand_d_.reserve(nq * fetch);
     cand_pos_.reserve(nq * fetch);
@@ -321,6 +518,9 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
   if (rerank)
     FDB_HIP(launch_rerank(d_qs, nq, (int)host_.dim, originals_.p, ids_.p, cand_pos_.p, cand_cnt_.p,
                           (uint32_t)fetch, k, d_ids, d_dists, d_counts, s));
+  else if (trunc)
+    FDB_HIP(launch_truncate(cand_ids_.p, cand_d_.p, cand_cnt_.p, nq, (uint32_t)fetch, k, d_ids, d_dists,
+                            d_counts, s));
   if (timed) {
     FDB_HIP(hipEventRecord(ev_[2], s));
     FDB_HIP(hipEventSynchronize(ev_[2]));
@@ -337,7 +537,8 @@ uint32_t IvfPqIndex::search(const float* q, uint32_t k, uint64_t* ids, float* di
   out_ids_.reserve(kk);
   out_d_.reserve(kk);
   out_cnt_.reserve(1);
-  run(q_.p, 1, k, np, kAdcGroups4, out_ids_.p, out_d_.p, out_cnt_.p, stream_, nullptr, nullptr);
+  run(q_.p, 1, k, np, kAdcGroups4, out_ids_.p, out_d_.p, out_cnt_.p, stream_, nullptr, nullptr,
+      live_bitmap());
   uint32_t cnt = 0;
   if (k) {
     FDB_HIP(hipMemcpyAsync(ids, out_ids_.p, 8 * (size_t)k, hipMemcpyDeviceToHost, stream_));
@@ -366,7 +567,8 @@ void IvfPqIndex::batch_search(const float* qs, uint64_t nq, uint32_t k, uint64_t
   out_ids_.reserve(nq * kk);
   out_d_.reserve(nq * kk);
   out_cnt_.reserve(nq);
-  run(q_.p, nq, k, np, kAdcLanes8, out_ids_.p, out_d_.p, out_cnt_.p, stream_, nullptr, nullptr);
+  run(q_.p, nq, k, np, kAdcLanes8, out_ids_.p, out_d_.p, out_cnt_.p, stream_, nullptr, nullptr,
+      live_bitmap());
   if (k) {
     FDB_HIP(hipMemcpyAsync(ids, out_ids_.p, 8 * nq * k, hipMemcpyDeviceToHost, stream_));
     FDB_HIP(hipMemcpyAsync(dists, out_d_.p, 4 * nq * k, hipMemcpyDeviceToHost, stream_));
@@ -387,7 +589,8 @@ void IvfPqIndex::batch_search_device(const float* d_qs, uint64_t nq, uint32_t k,
                                      float* coarse_ms, float* scan_ms) {
   std::lock_guard<std::mutex> g(mu_);
   const uint32_t np = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(nprobe(), host_.nlist));
-  run(d_qs, nq, k, np, kAdcLanes8, d_ids, d_dists, d_counts, s ? s : stream_, coarse_ms, scan_ms);
+  run(d_qs, nq, k, np, kAdcLanes8, d_ids, d_dists, d_counts, s ? s : stream_, coarse_ms, scan_ms,
+      live_bitmap());
 }
 
 bool IvfPqIndex::sync(hipStream_t s) {

@@ -4,6 +4,8 @@
 
 #include <atomic>
 #include <mutex>
+#include <unordered_set>
+#include <vector>
 
 #include "fdb_format.hpp"
 #include "fdb_host.hpp"
@@ -49,12 +51,39 @@ class IvfPqIndex {
   void probe(const float* qs, uint64_t nq, uint32_t nprobe, int32_t* lists, float* dists);
   void encode(const float* residuals, uint64_t nq, uint8_t* codes);
 
+  // search_filtered (ivf_pq.rs:692-831) for each of nq queries: only list
+  // positions whose id is in allowed (n_allowed ids, any order) and not
+  // tombstoned are scanned, with 4 * fetch_k candidates kept per query.
+  void search_filtered(const float* qs, uint64_t nq, uint32_t k, const uint64_t* allowed,
+                       uint64_t n_allowed, uint64_t* ids, float* dists, uint32_t* counts);
+  // delete (ivf_pq.rs:1786-1804): tombstones id in the first list holding it
+  // untombstoned; false when there is none.
+  bool remove(uint64_t id);
+  // insert_batch (ivf_pq.rs:1731-1776): nearest list, residual encoded with
+  // the codebooks, appended in input order; the id leaves that list's
+  // tombstones.  With reranking on, the vectors join the originals.
+  void insert(const float* vectors, const uint64_t* ids, uint64_t n);
+  // compact (ivf_pq.rs:1828-1851): drops tombstoned entries.
+  void compact();
+  // num_tombstones (:1807-1812); len() = entries - tombstones (:1088-1094)
+  uint64_t num_tombstones() const { return n_tomb_; }
+  uint64_t live_len() const { return host_.ids.size() - n_tomb_; }
+
   hipStream_t stream() const { return stream_; }
 
  private:
-  // the device pipeline: coarse selection, fused scan, optional rerank
+  // the device pipeline: coarse selection, fused scan, optional rerank.
+  // live: bitmap of scannable list positions (nullable); fetch_mult scales
+  // the candidates kept per query before reranking/truncation.
   void run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, int order, uint64_t* d_ids,
-           float* d_dists, uint32_t* d_counts, hipStream_t s, float* coarse_ms, float* scan_ms);
+           float* d_dists, uint32_t* d_counts, hipStream_t s, float* coarse_ms, float* scan_ms,
+           const uint32_t* live = nullptr, uint32_t fetch_mult = 1);
+  // tombstone bitmap for the scan, rebuilt after changes (caller holds mu_);
+  // null when nothing is tombstoned
+  const uint32_t* live_bitmap();
+  // re-uploads ids, codes, offsets and originals after the lists changed
+  void upload_lists();
+  void throw_if_nan();
 
   IvfPqArtifacts host_;
   std::atomic<uint64_t> nprobe_{1};
@@ -66,6 +95,14 @@ class IvfPqIndex {
   DevBuf<uint32_t> off_;
   DevBuf<uint8_t> codes_;
   DevBuf<uint64_t> ids_;
+
+  // tombstones per list (PartitionData::tombstones, ivf_pq.rs:190) and the
+  // bitmap of untombstoned list positions
+  std::vector<std::unordered_set<uint64_t>> tomb_;
+  uint64_t n_tomb_ = 0;
+  bool live_dirty_ = false;
+  DevBuf<uint32_t> live_, filt_;
+  DevBuf<uint64_t> allow_;
 
   // per-call scratch, guarded by mu_
   DevBuf<float> q_, probe_d_, cand_d_, out_d_;

@@ -229,10 +229,17 @@ struct GroupLists {
 // the end re-reads the list's last code (len > 0) and carries key kNoPos.
 // FAST: the LUT holds |cb|^2 - 2<r, cb> and base = |r|^2 is added to every
 // sum; otherwise base is unused (exact mode adds nothing).
+// live (nullable): bitmap over list positions; a clear bit skips the code
+// (tombstones, filters).
+__device__ __forceinline__ bool live_at(const uint32_t* __restrict__ live, uint32_t i) {
+  return (live[i >> 5] >> (i & 31)) & 1u;
+}
+
 template <int MT, int ORDER, int R, int NW, int U, int J, int FAST>
 __device__ __forceinline__ void scan_list(const float* __restrict__ lut, uint32_t start, uint32_t len,
                                           float base, uint32_t w0, int lane,
-                                          const uint8_t* __restrict__ codes, WaveTopK<R>& tk) {
+                                          const uint8_t* __restrict__ codes,
+                                          const uint32_t* __restrict__ live, WaveTopK<R>& tk) {
   const uint32_t nb = (len + 63) / 64;
   const uint32_t last = start + len - 1;
   for (uint32_t b0 = w0; b0 < nb; b0 += (uint32_t)(NW * U)) {
@@ -241,9 +248,11 @@ __device__ __forceinline__ void scan_list(const float* __restrict__ lut, uint32_
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t i = start + (b0 + (uint32_t)(u * NW)) * 64 + (uint32_t)lane;
-      const bool valid = i <= last;  // also false for a batch past nb
+      const bool in = i <= last;  // also false for a batch past nb
+      const uint32_t ic = in ? i : last;
+      const bool valid = in && (live == nullptr || live_at(live, ic));
       key[u] = valid ? i : kNoPos;
-      load_code<MT>(codes, valid ? i : last, w[u]);
+      load_code<MT>(codes, ic, w[u]);
     }
     float dist[U];
 #pragma unroll
@@ -259,12 +268,13 @@ __device__ __forceinline__ void scan_list(const float* __restrict__ lut, uint32_
 template <int MT, int ORDER, int R, int NW, int U, int GMAX, int J, int FAST>
 __device__ __forceinline__ void scan_group(const float* __restrict__ lut, const float* __restrict__ rr,
                                            const GroupLists<GMAX>& gl, uint32_t w0, int lane,
-                                           const uint8_t* __restrict__ codes, WaveTopK<R>& tk) {
+                                           const uint8_t* __restrict__ codes,
+                                           const uint32_t* __restrict__ live, WaveTopK<R>& tk) {
   if (J < gl.ng && gl.len[J] > 0)
     scan_list<MT, ORDER, R, NW, U, J, FAST>(lut, gl.start[J], gl.len[J], FAST ? rr[J] : 0.0f, w0,
-                                            lane, codes, tk);
+                                            lane, codes, live, tk);
   if constexpr (J + 1 < GMAX)
-    scan_group<MT, ORDER, R, NW, U, GMAX, J + 1, FAST>(lut, rr, gl, w0, lane, codes, tk);
+    scan_group<MT, ORDER, R, NW, U, GMAX, J + 1, FAST>(lut, rr, gl, w0, lane, codes, live, tk);
 }
 
 // One workgroup per query.  MT/DT: compile-time M and dsub (0 = runtime, then
@@ -373,7 +383,7 @@ void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
     __syncthreads();
 
     if constexpr (MT > 0) {
-      scan_group<MT, ORDER, R, NW, U, GMAX, 0, FAST>(lut, s_rr, gl, w0, lane, a.codes, tk);
+      scan_group<MT, ORDER, R, NW, U, GMAX, 0, FAST>(lut, s_rr, gl, w0, lane, a.codes, a.live, tk);
     } else {
       // generic shape: lists one after another, one code per lane
       for (int j = 0; j < ng; ++j) {
@@ -385,7 +395,7 @@ void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
           const uint32_t i = base + tid;
           float dist = f_inf();
           uint32_t key = kNoPos;
-          if (i < e) {
+          if (i < e && (a.live == nullptr || live_at(a.live, i))) {
             key = i;
             dist = adc_sum_rt<ORDER>(L, a.codes + (uint64_t)i * M, M);
           }
@@ -654,6 +664,43 @@ __global__ __launch_bounds__(kThreads) void codebook_norms_kernel(const float* _
   out[e] = s;
 }
 }  // namespace
+
+namespace {
+// One thread per bitmap word: 32 positions, each id looked up by binary
+// search in the sorted allowed list.
+__global__ __launch_bounds__(256) void filter_bitmap_kernel(const uint64_t* __restrict__ ids, uint64_t n,
+                                                            const uint64_t* __restrict__ allowed,
+                                                            uint64_t n_allowed,
+                                                            const uint32_t* __restrict__ live,
+                                                            uint32_t* __restrict__ out) {
+  const uint64_t w = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (w >= (n + 31) / 32) return;
+  uint32_t word = 0;
+  for (int b = 0; b < 32; ++b) {
+    const uint64_t p = w * 32 + b;
+    if (p >= n) break;
+    if (live && !((live[w] >> b) & 1u)) continue;
+    const uint64_t id = ids[p];
+    uint64_t lo = 0, hi = n_allowed;  // first allowed entry >= id
+    while (lo < hi) {
+      const uint64_t mid = (lo + hi) >> 1;
+      if (allowed[mid] < id) lo = mid + 1; else hi = mid;
+    }
+    if (lo < n_allowed && allowed[lo] == id) word |= 1u << b;
+  }
+  out[w] = word;
+}
+}  // namespace
+
+hipError_t launch_filter_bitmap(const uint64_t* ids, uint64_t n, const uint64_t* allowed,
+                                uint64_t n_allowed, const uint32_t* live, uint32_t* out,
+                                hipStream_t stream) {
+  const uint64_t words = (n + 31) / 32;
+  if (words == 0) return hipSuccess;
+  hipLaunchKernelGGL(filter_bitmap_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream,
+                     ids, n, allowed, n_allowed, live, out);
+  return hipGetLastError();
+}
 
 hipError_t launch_codebook_norms(const float* codebooks, int M, int dsub, float* out,
                                  hipStream_t stream) {

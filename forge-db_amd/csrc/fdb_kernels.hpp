@@ -59,8 +59,15 @@ struct IvfPqScanArgs {
   float* out_dists;
   uint32_t* out_pos;  // nullable: list positions of the results
   uint32_t* out_counts;
+  const uint32_t* live;  // nullable: bitmap over list positions, clear bit = skip
 };
 hipError_t launch_ivfpq_scan(const IvfPqScanArgs& a, hipStream_t stream);
+
+// Bitmap over n list positions: bit p = (live == nullptr or live bit p) and
+// ids[p] is in allowed (sorted ascending, n_allowed entries).
+hipError_t launch_filter_bitmap(const uint64_t* ids, uint64_t n, const uint64_t* allowed,
+                                uint64_t n_allowed, const uint32_t* live, uint32_t* out,
+                                hipStream_t stream);
 
 // |cb_mj|^2 for every codeword: [M*256]
 hipError_t launch_codebook_norms(const float* codebooks, int M, int dsub, float* out,

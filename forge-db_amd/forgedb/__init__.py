@@ -43,6 +43,8 @@ EXPORTED_SYMBOLS = (
     "fdb_ivfpq_search", "fdb_ivfpq_batch_search", "fdb_ivfpq_batch_search_device",
     "fdb_ivfpq_sync", "fdb_ivfpq_probe", "fdb_ivfpq_encode",
     "fdb_ivfpq_batch_search_device_timed", "fdb_ivfpq_set_lut_mode", "fdb_ivfpq_lut_mode",
+    "fdb_ivfpq_search_filtered", "fdb_ivfpq_delete", "fdb_ivfpq_insert", "fdb_ivfpq_compact",
+    "fdb_ivfpq_len", "fdb_ivfpq_num_tombstones",
     "fdb_bf_create", "fdb_bf_add", "fdb_bf_remove", "fdb_bf_len", "fdb_bf_dimension",
     "fdb_bf_metric", "fdb_bf_load", "fdb_bf_save", "fdb_bf_destroy", "fdb_bf_export",
     "fdb_bf_search", "fdb_bf_batch_search", "fdb_bf_batch_search_device",
@@ -124,6 +126,11 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fdb_ivfpq_probe": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, _P, _P],
         "fdb_ivfpq_encode": [_P, _P, C.c_uint64, C.c_uint32, _P],
         "fdb_ivfpq_set_lut_mode": [_P, C.c_uint32],
+        "fdb_ivfpq_search_filtered": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, _P, C.c_uint64, _P,
+                                      _P, _P],
+        "fdb_ivfpq_delete": [_P, C.c_uint64, _P],
+        "fdb_ivfpq_insert": [_P, _P, _P, C.c_uint64, C.c_uint32],
+        "fdb_ivfpq_compact": [_P],
         "fdb_bf_create": [C.c_uint32, _P],
         "fdb_bf_add": [_P, _P, _P, C.c_uint64, C.c_uint32],
         "fdb_bf_remove": [_P, C.c_uint64, _P],
@@ -156,7 +163,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
     lib.fdb_ivfpq_nprobe.restype = C.c_uint64
     lib.fdb_ivfpq_lut_mode.argtypes = [_P]
     lib.fdb_ivfpq_lut_mode.restype = C.c_uint32
-    for name, res in (("fdb_bf_destroy", None), ("fdb_bf_len", C.c_uint64),
+    for name, res in (("fdb_ivfpq_len", C.c_uint64), ("fdb_ivfpq_num_tombstones", C.c_uint64),
+                      ("fdb_bf_destroy", None), ("fdb_bf_len", C.c_uint64),
                       ("fdb_bf_dimension", C.c_uint32), ("fdb_bf_metric", C.c_uint32),
                       ("fdb_ivf_destroy", None), ("fdb_ivf_nprobe", C.c_uint64),
                       ("fdb_ivf_len", C.c_uint64), ("fdb_ivf_num_partitions", C.c_uint32),
@@ -285,7 +293,51 @@ class IVFPQIndex:
         return {f: getattr(d, f) for f, _ in _Desc._fields_}
 
     def __len__(self) -> int:
+        """len (ivf_pq.rs:1088-1094): entries minus tombstones."""
+        return int(self._lib.fdb_ivfpq_len(self._h))
+
+    def len_with_tombstones(self) -> int:
         return int(self.describe()["n_vectors"])
+
+    def num_tombstones(self) -> int:
+        return int(self._lib.fdb_ivfpq_num_tombstones(self._h))
+
+    def delete(self, vector_id: int) -> bool:
+        """delete (ivf_pq.rs:1786-1804)."""
+        out = C.c_int()
+        _check(self._lib, self._lib.fdb_ivfpq_delete(self._h, int(vector_id), C.byref(out)))
+        return bool(out.value)
+
+    def insert_batch(self, vectors, ids=None) -> None:
+        """insert_batch (ivf_pq.rs:1731-1776)."""
+        v = _f32(vectors)
+        idv = None if ids is None else np.ascontiguousarray(ids, np.uint64)
+        _check(self._lib, self._lib.fdb_ivfpq_insert(self._h, _ptr(v), _ptr(idv), v.shape[0],
+                                                     v.shape[1]))
+
+    def compact(self) -> None:
+        """compact (ivf_pq.rs:1828-1851)."""
+        _check(self._lib, self._lib.fdb_ivfpq_compact(self._h))
+
+    def search_filtered_arrays(self, queries, k: int, allowed_ids):
+        """search_filtered per query; the filter given as the admitted ids."""
+        q = _f32(queries)
+        if q.ndim == 1:
+            q = q.reshape(1, -1)
+        allow = np.ascontiguousarray(allowed_ids, np.uint64)
+        nq = q.shape[0]
+        ids = np.empty((nq, max(k, 1)), np.uint64)
+        d = np.empty((nq, max(k, 1)), np.float32)
+        counts = np.empty(nq, np.uint32)
+        _check(self._lib, self._lib.fdb_ivfpq_search_filtered(
+            self._h, _ptr(q), nq, q.shape[1], k, _ptr(allow), allow.shape[0], _ptr(ids), _ptr(d),
+            _ptr(counts)))
+        return ids[:, :k], d[:, :k], counts
+
+    def search_filtered(self, query, k: int, allowed_ids) -> List[Tuple[int, float]]:
+        """search_filtered (ivf_pq.rs:692-831) -> [(id, dist)] ascending."""
+        ids, d, c = self.search_filtered_arrays(query, k, allowed_ids)
+        return [(int(ids[0, j]), float(d[0, j])) for j in range(int(c[0]))]
 
     def enable_reranking(self, vectors_list_order, rerank_factor: int) -> None:
         """enable_reranking (ivf_pq.rs:513-517); vectors given in list order."""

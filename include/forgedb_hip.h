@@ -171,6 +171,35 @@ FDB_API fdb_status fdb_ivfpq_probe(fdb_ivfpq* index, const float* queries, uint6
 FDB_API fdb_status fdb_ivfpq_encode(fdb_ivfpq* index, const float* residuals, uint64_t nq,
                                     uint32_t dim, uint8_t* out_codes);
 
+/* search_filtered (ivf_pq.rs:692-831) for nq queries (nq = 1 is the
+ * reference call): the metadata filter arrives already evaluated, as the
+ * n_allowed vector ids it admits (MetadataStore::filter_bitmap mapped back to
+ * ids, any order); only untombstoned entries with an admitted id are
+ * scanned.  Like the reference: nprobe lists (0 when nprobe is 0), the
+ * search() ADC order, 4 * k (* rerank_factor) candidates kept, then rerank
+ * or truncation to k; no admitted id gives no results. */
+FDB_API fdb_status fdb_ivfpq_search_filtered(fdb_ivfpq* index, const float* queries, uint64_t nq,
+                                             uint32_t dim, uint32_t k, const uint64_t* allowed_ids,
+                                             uint64_t n_allowed, uint64_t* out_ids,
+                                             float* out_dists, uint32_t* out_counts);
+/* delete (ivf_pq.rs:1786-1804): tombstones id in the first list that holds it
+ * untombstoned; *deleted = 1 then, else 0.  Searches skip every entry of
+ * that list with this id.  Tombstones are not saved (SerializablePartition
+ * carries none, :222-243). */
+FDB_API fdb_status fdb_ivfpq_delete(fdb_ivfpq* index, uint64_t id, int* deleted);
+/* insert_batch (ivf_pq.rs:1731-1776): n vectors [n][dim] with ids (NULL:
+ * len_with_tombstones()..+n-1) go to their nearest list (first minimum),
+ * their residuals encoded with the codebooks, appended in input order; an
+ * inserted id leaves that list's tombstones.  With reranking enabled the
+ * vectors become the originals of the new entries. */
+FDB_API fdb_status fdb_ivfpq_insert(fdb_ivfpq* index, const float* vectors, const uint64_t* ids,
+                                    uint64_t n, uint32_t dim);
+/* compact (ivf_pq.rs:1828-1851): removes tombstoned entries. */
+FDB_API fdb_status fdb_ivfpq_compact(fdb_ivfpq* index);
+/* len (:1088-1094, entries minus tombstones) and num_tombstones (:1807) */
+FDB_API uint64_t fdb_ivfpq_len(const fdb_ivfpq* index);
+FDB_API uint64_t fdb_ivfpq_num_tombstones(const fdb_ivfpq* index);
+
 /* Kernel timing for measurement: runs one batch_search_device and returns the
  * durations in ms of the coarse and scan kernels (HIP events on the stream
  * they run on). */

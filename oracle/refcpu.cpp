@@ -15,6 +15,7 @@
 #include <map>
 #include <queue>
 #include <thread>
+#include <unordered_set>
 #include <vector>
 
 namespace {
@@ -545,7 +546,15 @@ struct fdbo_ivfpq {
   std::atomic<uint64_t> nprobe{1};
   std::vector<float> originals;  // [N][dim] list order, when reranking is on
   uint64_t rerank_factor = 1;
+  // PartitionData::tombstones (ivf_pq.rs:190): ids per list; sized on first use
+  std::vector<std::unordered_set<uint64_t>> tomb;
 };
+
+namespace {
+inline bool tombstoned(const fdbo_ivfpq* h, int list, uint64_t id) {
+  return !h->tomb.empty() && h->tomb[list].count(id) != 0;
+}
+}  // namespace
 
 fdbo_ivfpq* fdbo_ivfpq_create(const float* centroids, int nlist, int dim, const float* codebooks,
                               int M, const uint64_t* list_offsets, const uint64_t* ids,
@@ -774,6 +783,7 @@ int fdbo_ivfpq_search(const fdbo_ivfpq* h, const float* q, int k, uint64_t* out_
     // threshold read once per list (:638-642)
     const Threshold th = threshold_of(heap, fetch_k);
     for (uint64_t j = h->offsets[p]; j < h->offsets[p + 1]; ++j) {
+      if (tombstoned(h, p, h->ids[j])) continue;  // :657-659
       float dist = adc_groups4(lut.data(), &h->codes[j * h->M], h->M);
       if (item_lt(dist, j, th.d, th.pos) || heap.size() < fetch_k) {
         heap.push({j, dist});
@@ -817,6 +827,7 @@ void fdbo_ivfpq_batch_search(const fdbo_ivfpq* h, const float* queries, uint64_t
     const bool use_batch = qidx.size() >= 4;
     std::vector<float> dists(qidx.size());
     for (uint64_t j = h->offsets[p]; j < h->offsets[p + 1]; ++j) {
+      if (tombstoned(h, p, h->ids[j])) continue;  // :960-963
       const uint8_t* code = &h->codes[j * M];
       if (use_batch) {
         adc_batch(refs.data(), (int)refs.size(), code, M, dists.data());
@@ -837,6 +848,104 @@ void fdbo_ivfpq_batch_search(const fdbo_ivfpq* h, const float* queries, uint64_t
   for (uint64_t qi = 0; qi < nq; ++qi)
     out_counts[qi] = finish(h, queries + qi * dim, heaps[qi], k, out_ids + qi * (uint64_t)k,
                             out_dists + qi * (uint64_t)k);
+}
+
+// search_filtered, ivf_pq.rs:692-831: the filter as the set of admitted ids.
+// Heap of 4 * fetch_k, threshold read once per list, tombstoned and
+// unadmitted entries skipped, then rerank or truncation.
+int fdbo_ivfpq_search_filtered(const fdbo_ivfpq* h, const float* q, int k, const uint64_t* allowed,
+                               uint64_t n_allowed, uint64_t* out_ids, float* out_dists) {
+  if (n_allowed == 0) return 0;  // :700-703
+  std::unordered_set<uint64_t> allow(allowed, allowed + n_allowed);
+  const uint64_t fetch_k = h->originals.empty() ? (uint64_t)k : (uint64_t)k * h->rerank_factor;
+  const uint64_t filter_fetch_k = fetch_k * 4;  // :712
+  uint64_t nprobe = h->nprobe.load(std::memory_order_relaxed);
+  std::vector<int32_t> lists(h->nlist);
+  int np = select_probes(h, q, nprobe, lists.data(), nullptr);
+  PosHeap heap;
+  std::vector<float> resid(h->dim), lut((size_t)h->M * 256);
+  for (int pi = 0; pi < np; ++pi) {
+    int p = lists[pi];
+    const float* c = &h->centroids[(size_t)p * h->dim];
+    for (int j = 0; j < h->dim; ++j) resid[j] = q[j] - c[j];
+    pq_lut(h->codebooks.data(), h->M, h->dsub, resid.data(), lut.data());
+    const Threshold th = threshold_of(heap, filter_fetch_k);
+    for (uint64_t j = h->offsets[p]; j < h->offsets[p + 1]; ++j) {
+      if (tombstoned(h, p, h->ids[j]) || !allow.count(h->ids[j])) continue;
+      float dist = adc_groups4(lut.data(), &h->codes[j * h->M], h->M);
+      if (item_lt(dist, j, th.d, th.pos) || heap.size() < filter_fetch_k) {
+        heap.push({j, dist});
+        if (heap.size() > filter_fetch_k) heap.pop();
+      }
+    }
+  }
+  return finish(h, q, heap, k, out_ids, out_dists);
+}
+
+// delete, ivf_pq.rs:1786-1804
+int fdbo_ivfpq_delete(fdbo_ivfpq* h, uint64_t id) {
+  if (h->tomb.empty()) h->tomb.resize(h->nlist);
+  for (int l = 0; l < h->nlist; ++l) {
+    if (h->tomb[l].count(id)) continue;
+    for (uint64_t j = h->offsets[l]; j < h->offsets[l + 1]; ++j)
+      if (h->ids[j] == id) {
+        h->tomb[l].insert(id);
+        return 1;
+      }
+  }
+  return 0;
+}
+
+uint64_t fdbo_ivfpq_num_tombstones(const fdbo_ivfpq* h) {
+  uint64_t n = 0;
+  for (auto& t : h->tomb) n += t.size();
+  return n;
+}
+
+// insert_batch, ivf_pq.rs:1731-1776, one vector at a time in input order
+void fdbo_ivfpq_insert(fdbo_ivfpq* h, const float* vectors, const uint64_t* ids, uint64_t n) {
+  if (h->tomb.empty()) h->tomb.resize(h->nlist);
+  const int dim = h->dim, M = h->M;
+  std::vector<float> resid(dim);
+  std::vector<uint8_t> code(M);
+  for (uint64_t i = 0; i < n; ++i) {
+    const float* v = vectors + i * (uint64_t)dim;
+    const int l = nearest(v, h->centroids.data(), h->nlist, dim);
+    const float* c = &h->centroids[(size_t)l * dim];
+    for (int j = 0; j < dim; ++j) resid[j] = v[j] - c[j];
+    pq_encode(h->codebooks.data(), M, h->dsub, resid.data(), code.data());
+    const uint64_t at = h->offsets[l + 1];
+    h->ids.insert(h->ids.begin() + at, ids[i]);
+    h->codes.insert(h->codes.begin() + at * M, code.begin(), code.end());
+    if (!h->originals.empty())
+      h->originals.insert(h->originals.begin() + at * dim, v, v + dim);
+    for (int t = l + 1; t <= h->nlist; ++t) h->offsets[t]++;
+    h->tomb[l].erase(ids[i]);
+  }
+}
+
+// compact, ivf_pq.rs:1828-1851
+void fdbo_ivfpq_compact(fdbo_ivfpq* h) {
+  if (h->tomb.empty()) return;
+  const int dim = h->dim, M = h->M;
+  std::vector<uint64_t> offs(h->nlist + 1, 0), ids;
+  std::vector<uint8_t> codes;
+  std::vector<float> orig;
+  for (int l = 0; l < h->nlist; ++l) {
+    for (uint64_t j = h->offsets[l]; j < h->offsets[l + 1]; ++j) {
+      if (h->tomb[l].count(h->ids[j])) continue;
+      ids.push_back(h->ids[j]);
+      codes.insert(codes.end(), &h->codes[j * M], &h->codes[j * M] + M);
+      if (!h->originals.empty())
+        orig.insert(orig.end(), &h->originals[j * dim], &h->originals[j * dim] + dim);
+    }
+    offs[l + 1] = ids.size();
+    h->tomb[l].clear();
+  }
+  h->offsets.swap(offs);
+  h->ids.swap(ids);
+  h->codes.swap(codes);
+  if (!h->originals.empty()) h->originals.swap(orig);
 }
 
 // batch_search_parallel, ivf_pq.rs:1060-1084

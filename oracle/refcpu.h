@@ -106,6 +106,14 @@ int fdbo_ivfpq_search(const fdbo_ivfpq* h, const float* q, int k,
 void fdbo_ivfpq_batch_search(const fdbo_ivfpq* h, const float* queries, uint64_t nq,
                              int k, uint64_t* out_ids, float* out_dists,
                              int32_t* out_counts);
+/* search_filtered (:692-831), the filter as admitted ids; returns count */
+int fdbo_ivfpq_search_filtered(const fdbo_ivfpq* h, const float* q, int k, const uint64_t* allowed,
+                               uint64_t n_allowed, uint64_t* out_ids, float* out_dists);
+/* delete (:1786-1804), insert_batch (:1731-1776), compact (:1828-1851) */
+int fdbo_ivfpq_delete(fdbo_ivfpq* h, uint64_t id);
+uint64_t fdbo_ivfpq_num_tombstones(const fdbo_ivfpq* h);
+void fdbo_ivfpq_insert(fdbo_ivfpq* h, const float* vectors, const uint64_t* ids, uint64_t n);
+void fdbo_ivfpq_compact(fdbo_ivfpq* h);
 /* batch_search_parallel (:1060-1084) on nthreads (0 = all cores) */
 void fdbo_ivfpq_batch_search_parallel(const fdbo_ivfpq* h, const float* queries,
                                       uint64_t nq, int k, int nthreads,

@@ -90,6 +90,16 @@ def lib() -> C.CDLL:
     L.fdbo_ivf_batch_search.restype = None
     L.fdbo_ivf_build.argtypes = [_P, u64, i32, i32, u64, i32, _P, _P, _P]
     L.fdbo_ivf_build.restype = i32
+    L.fdbo_ivfpq_search_filtered.argtypes = [_P, _P, i32, _P, u64, _P, _P]
+    L.fdbo_ivfpq_search_filtered.restype = i32
+    L.fdbo_ivfpq_delete.argtypes = [_P, u64]
+    L.fdbo_ivfpq_delete.restype = i32
+    L.fdbo_ivfpq_num_tombstones.argtypes = [_P]
+    L.fdbo_ivfpq_num_tombstones.restype = u64
+    L.fdbo_ivfpq_insert.argtypes = [_P, _P, _P, u64]
+    L.fdbo_ivfpq_insert.restype = None
+    L.fdbo_ivfpq_compact.argtypes = [_P]
+    L.fdbo_ivfpq_compact.restype = None
     _lib = L
     return L
 
@@ -192,7 +202,13 @@ class IvfPq:
         except Exception:
             pass
 
+    def _reshape(self):
+        nl, dm, M, n = C.c_int(), C.c_int(), C.c_int(), C.c_uint64()
+        lib().fdbo_ivfpq_shape(self.h, C.byref(nl), C.byref(dm), C.byref(M), C.byref(n))
+        self.n = n.value
+
     def export(self) -> dict:
+        self._reshape()  # insert / compact change the entry count
         dsub = self.dim // self.M
         out = dict(centroids=np.empty((self.nlist, self.dim), np.float32),
                    codebooks=np.empty((self.M, 256, dsub), np.float32),
@@ -225,6 +241,29 @@ class IvfPq:
         d = np.empty(max(k, 1), np.float32)
         cnt = lib().fdbo_ivfpq_search(self.h, _p(q), k, _p(ids), _p(d))
         return ids[:cnt], d[:cnt]
+
+    def search_filtered(self, q, k: int, allowed_ids):
+        q = _f(q)
+        allow = np.ascontiguousarray(allowed_ids, np.uint64)
+        ids = np.empty(max(k * 4 * 64, 1), np.uint64)
+        d = np.empty(max(k * 4 * 64, 1), np.float32)
+        cnt = lib().fdbo_ivfpq_search_filtered(self.h, _p(q), k, _p(allow), allow.shape[0], _p(ids),
+                                               _p(d))
+        return ids[:cnt], d[:cnt]
+
+    def delete(self, vector_id: int) -> bool:
+        return bool(lib().fdbo_ivfpq_delete(self.h, int(vector_id)))
+
+    def num_tombstones(self) -> int:
+        return int(lib().fdbo_ivfpq_num_tombstones(self.h))
+
+    def insert(self, vectors, ids):
+        v = _f(vectors)
+        idv = np.ascontiguousarray(ids, np.uint64)
+        lib().fdbo_ivfpq_insert(self.h, _p(v), _p(idv), v.shape[0])
+
+    def compact(self):
+        lib().fdbo_ivfpq_compact(self.h)
 
     def batch_search(self, queries, k: int, parallel: bool = False, nthreads: int = 0):
         q = _f(queries)

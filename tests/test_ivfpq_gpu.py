@@ -251,3 +251,93 @@ def test_fast_lut_unsupported_shape():
         gx.set_lut_mode(1)
     assert e.value.kind == "Unsupported"
     assert gx.lut_mode() == 0
+
+
+# ---- tombstones, insert, compact, filtered search ------------------------------
+def fresh_pair(small_ivfpq, rerank=False):
+    art = small_ivfpq["art"]
+    gx = gpu_index(art)
+    ox = refcpu.IvfPq.create(art["centroids"], art["codebooks"], art["list_offsets"], art["ids"],
+                             art["codes"])
+    if rerank:
+        orig = small_ivfpq["base"][art["ids"].astype(np.int64)]
+        gx.enable_reranking(orig, 4)
+        ox.enable_reranking(orig, 4)
+    return gx, ox
+
+
+def check_single(gx, ox, queries, k, label):
+    for q, qv in enumerate(queries):
+        got = gx.search(qv, k)
+        oi, od = ox.search(qv, k)
+        assert [i for i, _ in got] == oi.tolist(), f"{label} q{q}"
+        assert np.array_equal(np.array([d for _, d in got], np.float32), od), f"{label} q{q}"
+
+
+def test_tombstone_parity(small_ivfpq):
+    print("delete -> search parity (batch and single)", flush=True)
+    gx, ox = fresh_pair(small_ivfpq)
+    q = small_ivfpq["queries"]
+    gx.set_nprobe(16)
+    ox.set_nprobe(16)
+    # the ids nearest to the first queries, so deleting them changes results
+    gi, _, _ = gx.batch_search_arrays(q[:8], 5)
+    victims = sorted(set(int(x) for x in gi.ravel()))[:20] + [10 ** 12]
+    for v in victims:
+        assert gx.delete(v) == ox.delete(v), v
+    assert gx.num_tombstones() == ox.num_tombstones() == 20
+    assert len(gx) == 20_000 - 20 and gx.len_with_tombstones() == 20_000
+    check_batch(gx, ox, q, 10, "tombstones")
+    check_single(gx, ox, q[:16], 10, "tombstones single")
+    gx.compact()
+    ox.compact()
+    a, b = gx.export(), ox.export()
+    for key in ("list_offsets", "ids", "codes"):
+        assert np.array_equal(a[key], b[key]), key
+    assert gx.num_tombstones() == 0 and len(gx) == 20_000 - 20
+    check_batch(gx, ox, q, 10, "compacted")
+
+
+def test_insert_parity(small_ivfpq):
+    print("insert_batch parity (assignment, codes, searches, un-tombstoning)", flush=True)
+    gx, ox = fresh_pair(small_ivfpq)
+    q = small_ivfpq["queries"]
+    rng = np.random.default_rng(6)
+    new = np.clip(q[:40] + rng.normal(0, 3, q[:40].shape), 0, 255).astype(np.float32)
+    ids = np.arange(500_000, 500_040, dtype=np.uint64)
+    assert gx.delete(3) and ox.delete(3)
+    ids[7] = 3  # re-inserting a deleted id lifts that list's tombstone
+    gx.insert_batch(new, ids)
+    ox.insert(new, ids)
+    a, b = gx.export(), ox.export()
+    for key in ("list_offsets", "ids", "codes"):
+        assert np.array_equal(a[key], b[key]), key
+    assert gx.num_tombstones() == ox.num_tombstones()
+    for nprobe in (4, 16):
+        gx.set_nprobe(nprobe)
+        ox.set_nprobe(nprobe)
+        check_batch(gx, ox, q, 10, f"inserted np{nprobe}")
+
+
+@pytest.mark.parametrize("rerank", [False, True], ids=["adc", "rerank"])
+def test_search_filtered_parity(small_ivfpq, rerank):
+    print(f"search_filtered parity rerank={rerank}", flush=True)
+    gx, ox = fresh_pair(small_ivfpq, rerank)
+    q = small_ivfpq["queries"][:24]
+    rng = np.random.default_rng(9)
+    for nprobe, n_allowed in ((16, 3000), (4, 200), (64, 50), (0, 3000), (8, 0)):
+        gx.set_nprobe(nprobe)
+        ox.set_nprobe(nprobe)
+        allowed = rng.choice(20_000, n_allowed, replace=False).astype(np.uint64)
+        if n_allowed:
+            assert gx.delete(int(allowed[0])) == ox.delete(int(allowed[0]))
+        k = 5 if rerank else 10
+        gi, gd, gc = gx.search_filtered_arrays(q, k, allowed)
+        for j, qv in enumerate(q):
+            oi, od = ox.search_filtered(qv, k, allowed)
+            label = f"filtered np{nprobe} n{n_allowed} q{j}"
+            assert int(gc[j]) == len(oi), label
+            assert gi[j, :len(oi)].tolist() == oi.tolist(), label
+            assert np.array_equal(gd[j, :len(oi)], od), label
+        assert gx.search_filtered(q[0], k, allowed) == [(int(i), float(d)) for i, d in
+                                                         zip(*ox.search_filtered(q[0], k, allowed))]

@@ -339,3 +339,81 @@ def test_ivf_search_is_brute_force_over_probed_lists():
             assert int(oc[0]) == len(srt)
             assert np.array_equal(od[0, :len(srt)], d[srt])
             assert np.array_equal(oi[0, :len(srt)], ids[[pos[j] for j in srt]])
+
+
+# ---- tombstones, insert, compact, filtered search (ivf_pq.rs:692-831, 1731-1851)
+def _small_pq(seed=4):
+    from forgedb import datagen
+    base, queries = datagen.workload("ivfpq_int", n=3000, nq=12)
+    ix = refcpu.IvfPq.build(base, nlist=16, M=16, seed=seed)
+    return base, queries, ix
+
+
+def _brute_adc(ix, q, allowed_pos, k):
+    """k smallest groups-of-4 ADC over the given list positions, in
+    (distance, position) order, as search() ranks them at nprobe = nlist."""
+    art = ix.export()
+    off = art["list_offsets"].astype(np.int64)
+    lst = np.searchsorted(off, np.arange(len(art["ids"])), side="right") - 1
+    luts = {}
+    out = []
+    for p in allowed_pos:
+        l = int(lst[p])
+        if l not in luts:
+            luts[l] = refcpu.pq_lut(art["codebooks"], np.asarray(q, np.float32) - art["centroids"][l])
+        out.append((refcpu.adc("groups4", luts[l], art["codes"][p]), p))
+    out.sort()
+    return [(int(art["ids"][p]), d) for d, p in out[:k]]
+
+
+def test_search_skips_tombstones_and_matches_compaction():
+    base, queries, ix = _small_pq()
+    ix.set_nprobe(16)
+    assert ix.delete(7) and not ix.delete(7) and ix.delete(100)
+    assert ix.num_tombstones() == 2
+    art = ix.export()
+    live = [p for p in range(len(art["ids"])) if int(art["ids"][p]) not in (7, 100)]
+    for q in queries[:4]:
+        ids, d = ix.search(q, 10)
+        want = _brute_adc(ix, q, live, 10)
+        assert [int(i) for i in ids] == [i for i, _ in want]
+        assert np.array_equal(d, np.array([x for _, x in want], np.float32))
+    bi, bd, bc = ix.batch_search(queries, 10)
+    ix.compact()
+    assert ix.num_tombstones() == 0 and len(ix.export()["ids"]) == 2998
+    ci, cd, cc = ix.batch_search(queries, 10)
+    assert np.array_equal(bd, cd) and np.array_equal(bc, cc)
+    assert 7 not in set(ci.ravel().tolist()) and 100 not in set(ci.ravel().tolist())
+
+
+def test_insert_goes_to_nearest_list_with_residual_code():
+    base, queries, ix = _small_pq()
+    art0 = ix.export()
+    new = (queries[:5] + 1.0).astype(np.float32)
+    ix.insert(new, np.arange(90000, 90005, dtype=np.uint64))
+    art = ix.export()
+    for i in range(5):
+        d = [refcpu.dist("l2sq", new[i], c) for c in art["centroids"]]
+        l = int(np.argmin(d))  # first minimum
+        s, e = int(art["list_offsets"][l]), int(art["list_offsets"][l + 1])
+        pos = s + list(art["ids"][s:e]).index(90000 + i)
+        assert np.array_equal(art["codes"][pos],
+                              refcpu.pq_encode(art["codebooks"], new[i] - art["centroids"][l]))
+    assert len(art["ids"]) == len(art0["ids"]) + 5
+
+
+def test_search_filtered_is_brute_force_over_admitted_live_entries():
+    base, queries, ix = _small_pq()
+    ix.set_nprobe(16)
+    art = ix.export()
+    rng = np.random.default_rng(3)
+    allowed = rng.choice(3000, 400, replace=False).astype(np.uint64)
+    ix.delete(int(allowed[0]))
+    aset = set(int(a) for a in allowed[1:])
+    pos = [p for p in range(len(art["ids"])) if int(art["ids"][p]) in aset]
+    for q in queries[:4]:
+        ids, d = ix.search_filtered(q, 10, allowed)
+        want = _brute_adc(ix, q, pos, 10)
+        assert [int(i) for i in ids] == [i for i, _ in want]
+        assert np.array_equal(d, np.array([x for _, x in want], np.float32))
+    assert len(ix.search_filtered(queries[0], 10, np.array([], np.uint64))[0]) == 0
