@@ -169,6 +169,7 @@ def bench_ivfpq(args, w, base, queries):
     index = IVFPQIndex.build(base, nlist, M, seed=args.seed)
     log(f"[bench] GPU build (k-means {nlist}, PQ {M}x256, encode) in {time.time() - t:.1f}s")
     index.set_nprobe(nprobe)
+    index.set_coarse_mode({"auto": 0, "exact": 1, "screen": 2}[args.coarse])
     r = Runner(args, queries, k)
     nq = r.nq
 
@@ -301,6 +302,7 @@ def bench_ivf(args, w, base, queries):
     index = IVFIndex.build(base, nlist, metric, seed=args.seed)
     log(f"[bench] GPU build (k-means {nlist}, 100 iterations max) in {time.time() - t:.1f}s")
     index.set_nprobe(nprobe)
+    index.set_coarse_mode({"auto": 0, "exact": 1, "screen": 2}[args.coarse])
     r = Runner(args, queries, k)
     nq = r.nq
 
@@ -350,8 +352,9 @@ def bench_ivf(args, w, base, queries):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10,
+                    help="untimed steps first (the GPU clock settles over the first ~10)")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--workload", default="ivfpq_1m", choices=sorted(WORKLOADS))
     ap.add_argument("--n", type=int, default=None, help="override the base size")
@@ -360,6 +363,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target wall time of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--coarse", default="auto", choices=["auto", "exact", "screen"],
+                    help="coarse selection strategy of the IVF indexes (same probes)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one plain 1 GiB device-to-device copy (a known-size "
                          "reference for the FETCH_SIZE / WRITE_SIZE counters)")

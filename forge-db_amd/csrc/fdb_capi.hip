@@ -189,6 +189,13 @@ uint32_t fdb_ivfpq_lut_mode(const fdb_ivfpq* h) {
   return (h && h->impl) ? (uint32_t)h->impl->lut_mode() : 0;
 }
 
+fdb_status fdb_ivfpq_set_coarse_mode(fdb_ivfpq* h, uint32_t mode) {
+  return guarded([&] {
+    if (mode > 2) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown coarse mode");
+    H(h)->set_coarse_mode((int)mode);
+  });
+}
+
 fdb_status fdb_ivfpq_describe(const fdb_ivfpq* h, fdb_ivfpq_desc* out) {
   return guarded([&] {
     if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
@@ -507,6 +514,12 @@ void fdb_ivf_destroy(fdb_ivf* h) {
 
 void fdb_ivf_set_nprobe(fdb_ivf* h, uint64_t nprobe) {
   if (h && h->impl) h->impl->set_nprobe(nprobe);
+}
+fdb_status fdb_ivf_set_coarse_mode(fdb_ivf* h, uint32_t mode) {
+  return guarded([&] {
+    if (mode > 2) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown coarse mode");
+    impl_of(h)->set_coarse_mode((int)mode);
+  });
 }
 uint64_t fdb_ivf_nprobe(const fdb_ivf* h) { return (h && h->impl) ? h->impl->nprobe() : 0; }
 uint64_t fdb_ivf_len(const fdb_ivf* h) { return (h && h->impl) ? h->impl->size() : 0; }

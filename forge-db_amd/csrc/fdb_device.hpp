@@ -270,7 +270,14 @@ struct WaveTopK {
     drain(mask, dist, key);
   }
 
+  // Lanes in mask bring a pair that may enter the list.  A few are inserted
+  // one at a time; many (an empty list filling up) are merged in bulk.
   __device__ __forceinline__ void drain(uint64_t mask, float dist, uint32_t key) {
+    if (__popcll(mask) > kBulkThreshold) {
+      const bool in = (mask >> lane_id()) & 1;
+      merge64(in ? dist : f_inf(), in ? key : kNoPos);
+      return;
+    }
     while (mask) {
       const int l = __ffsll((unsigned long long)mask) - 1;
       mask &= mask - 1;
@@ -278,6 +285,68 @@ struct WaveTopK {
       const uint32_t pn = readlane_u(key, l);
       if (pair_lt(dn, pn, tau, tau_p)) insert(dn, pn);
     }
+  }
+
+  static constexpr int kBulkThreshold = 6;
+
+  // One compare-exchange of a bitonic network: keep the smaller pair when
+  // keep_min, else the larger.
+  static __device__ __forceinline__ void cx(float& d0, uint32_t& p0, float d1, uint32_t p1,
+                                            bool keep_min) {
+    const bool other_first = pair_lt(d1, p1, d0, p0);
+    if (other_first == keep_min) {
+      d0 = d1;
+      p0 = p1;
+    }
+  }
+
+  // Merge one pair per lane (sentinel (+inf, kNoPos) for none) into the
+  // list: sort the 64 new pairs (bitonic network over the lanes), reverse
+  // them against the list's last register so list-then-reversed is bitonic,
+  // keep the smaller of each position (the 64*R smallest of both, still
+  // bitonic), then sort that bitonic sequence.
+  __device__ __forceinline__ void merge64(float nd, uint32_t np) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int kk = 2; kk <= 64; kk <<= 1) {
+#pragma unroll
+      for (int j = kk >> 1; j > 0; j >>= 1) {
+        const float od = __shfl_xor(nd, j);
+        const uint32_t op = __shfl_xor(np, j);
+        const bool lower = (lane & j) == 0;
+        const bool up = (lane & kk) == 0;
+        cx(nd, np, od, op, lower == up);
+      }
+    }
+    const float rd = __shfl(nd, 63 - lane);
+    const uint32_t rp = __shfl(np, 63 - lane);
+    cx(d[R - 1], p[R - 1], rd, rp, true);
+#pragma unroll
+    for (int dist = 32 * R; dist >= 64; dist >>= 1) {
+      const int rs = dist / 64;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if ((r & rs) == 0) {
+          float lo_d = d[r], hi_d = d[r + rs];
+          uint32_t lo_p = p[r], hi_p = p[r + rs];
+          const bool swap = pair_lt(hi_d, hi_p, lo_d, lo_p);
+          d[r] = swap ? hi_d : lo_d;
+          p[r] = swap ? hi_p : lo_p;
+          d[r + rs] = swap ? lo_d : hi_d;
+          p[r + rs] = swap ? lo_p : hi_p;
+        }
+    }
+#pragma unroll
+    for (int j = 32; j > 0; j >>= 1) {
+      const bool lower = (lane & j) == 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float od = __shfl_xor(d[r], j);
+        const uint32_t op = __shfl_xor(p[r], j);
+        cx(d[r], p[r], od, op, lower);
+      }
+    }
+    read_tau();
   }
 };
 

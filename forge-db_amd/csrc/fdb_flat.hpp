@@ -116,6 +116,75 @@ struct IvfFlatScanArgs {
 };
 hipError_t launch_ivf_flat_scan(const IvfFlatScanArgs& a, hipStream_t s);
 
+// ---- exact and screened top-k over a row set ------------------------------
+
+// A row set resident on the device, as the flat searches read it.
+struct FlatRows {
+  const float* dataT;     // [dim][ld] dimension rows permuted (launch_transpose_rows)
+  uint64_t ld, n;
+  int dim;
+  const float* rows;      // [n][dim] row-major (rescoring of screened candidates)
+  const float* row_norm;  // [n] reference-order squared norms
+  float rnmax;            // the largest of them
+  const uint64_t* ids;    // nullable: results carry row indices
+};
+
+// The k smallest (distance, row) per query over a FlatRows, by the exact VALU
+// scan or by MFMA screening + exact rescoring (same results).  Owns its
+// scratch; one user at a time.
+class FlatSearcher {
+ public:
+  // whether screening serves (metric, dim, k)
+  static bool screenable(int metric, int dim, uint32_t k);
+  // q_norm: [nq] reference-order query norms (cosine and screening)
+  void exact(const FlatRows& x, int metric, const float* d_qs, const float* q_norm, uint64_t nq,
+             uint32_t k, uint64_t* ids, float* d, uint32_t* c, hipStream_t s, const int* flags = nullptr);
+  void screen(const FlatRows& x, int metric, const float* d_qs, const float* q_norm, uint64_t nq,
+              uint32_t k, uint64_t* ids, float* d, uint32_t* c, hipStream_t s);
+  // device counter: queries of the last screen() rescanned exactly
+  const uint32_t* fallbacks() const { return fallbacks_.p; }
+
+ private:
+  DevBuf<float> part_d_, cand_d_;
+  DevBuf<uint32_t> part_k_, cand_c_, fallbacks_;
+  DevBuf<uint64_t> cand_k_;
+  DevBuf<int> flags_;
+};
+
+// Keys [n] as written by FlatSearcher with ids == nullptr (~0 = none) -> int32
+// list ids (-1 = none).
+hipError_t launch_keys_to_lists(const uint64_t* keys, uint64_t n, int32_t* out, hipStream_t s);
+
+// ---- coarse quantizer ---------------------------------------------------------
+
+// Selection of the nprobe nearest of nlist centroids (squared L2 in the
+// reference's order, ascending by (distance, list id)): the exact VALU kernel
+// (launch_coarse_select) or MFMA screening + exact rescoring, which returns
+// the same lists and distances.
+class CoarseQuantizer {
+ public:
+  // centroids [nlist][dim] and their transposed copy (launch_transpose_centroids),
+  // both device-resident and owned by the caller; computes the norms
+  void init(const float* centroids, const float* centT, uint32_t nlist, uint32_t dim, hipStream_t s);
+  // 0 = automatic, 1 = exact kernel only, 2 = screening where it applies
+  void set_mode(int m) { mode_ = m; }
+  // probes [nq][np] (np <= nlist, <= 1024); dists [nq][np] nullable; a NaN
+  // distance ORs 1 into *err
+  void select(const float* d_qs, uint64_t nq, uint32_t np, int32_t* probes, float* dists, int* err,
+              hipStream_t s);
+
+ private:
+  const float* cent_ = nullptr;
+  const float* centT_ = nullptr;
+  uint32_t nlist_ = 0, dim_ = 0;
+  int mode_ = 0;
+  float rnmax_ = 0.0f;
+  FlatSearcher srch_;
+  DevBuf<float> cnorm_, qn_, dtmp_;
+  DevBuf<uint64_t> keys_;
+  DevBuf<uint32_t> cnt_;
+};
+
 // ---- BruteForceIndex ------------------------------------------------------
 
 class BruteForceIndex {
@@ -157,11 +226,8 @@ class BruteForceIndex {
   void sync_device();  // re-uploads the rows after add/remove (caller holds mu_)
   void run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids, float* d_dists,
            uint32_t* d_counts, hipStream_t s);
-  void run_exact(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids, float* d_dists,
-                 uint32_t* d_counts, hipStream_t s, const int* flags);
-  void run_screen(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids, float* d_dists,
-                  uint32_t* d_counts, hipStream_t s);
   bool screen_applies(uint64_t nq, uint32_t k) const;
+  FlatRows flat_rows() const;
 
   uint32_t dim_ = 0, metric_;
   std::vector<float> h_rows_;
@@ -175,12 +241,12 @@ class BruteForceIndex {
   uint64_t ld_ = 0;
   float rnmax_ = 0.0f;
   int screen_mode_ = 0;
+  bool searched_ = false;
   // scratch
-  DevBuf<float> q_, qn_, part_d_, out_d_, cand_d_;
-  DevBuf<uint32_t> part_k_, out_c_, cand_c_;
-  DevBuf<uint64_t> out_i_, cand_k_;
-  DevBuf<int> flags_;
-  DevBuf<uint32_t> fallbacks_;
+  FlatSearcher srch_;
+  DevBuf<float> q_, qn_, out_d_;
+  DevBuf<uint32_t> out_c_;
+  DevBuf<uint64_t> out_i_;
   hipEvent_t ev_[2] = {nullptr, nullptr};
 };
 
@@ -198,6 +264,11 @@ class IvfFlatIndex {
 
   uint32_t nlist() const { return nlist_; }
   uint32_t metric() const { return metric_; }
+  // coarse selection strategy (CoarseQuantizer::set_mode)
+  void set_coarse_mode(int m) {
+    std::lock_guard<std::mutex> g(mu_);
+    coarse_.set_mode(m);
+  }
   uint32_t dim() const { return dim_; }
   uint64_t size() const { return h_ids_.size(); }
   void set_nprobe(uint64_t np) { nprobe_.store(np < nlist_ ? np : nlist_, std::memory_order_relaxed); }
@@ -227,7 +298,8 @@ class IvfFlatIndex {
   std::vector<uint64_t> h_offsets_, h_ids_;
   hipStream_t stream_ = nullptr;
   std::mutex mu_;
-  DevBuf<float> centT_, data_, row_norm_;
+  DevBuf<float> centT_, cent_, data_, row_norm_;
+  CoarseQuantizer coarse_;
   DevBuf<uint64_t> boff_, ids_;
   DevBuf<uint32_t> row_off_;
   DevBuf<float> q_, qn_, out_d_;

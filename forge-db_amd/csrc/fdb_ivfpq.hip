@@ -237,6 +237,7 @@ IvfPqIndex::IvfPqIndex(IvfPqArtifacts&& art) : host_(std::move(art)) {
   centroids_.upload(host_.centroids.data(), host_.centroids.size(), stream_);
   centT_.reserve((size_t)centT_ld(host_.nlist) * host_.dim);
   FDB_HIP(launch_transpose_centroids(centroids_.p, host_.nlist, host_.dim, centT_.p, stream_));
+  coarse_.init(centroids_.p, centT_.p, host_.nlist, host_.dim, stream_);
   codebooks_.upload(host_.codebooks.data(), host_.codebooks.size(), stream_);
   cbnorm_.reserve((size_t)host_.M * 256);
   FDB_HIP(launch_codebook_norms(codebooks_.p, host_.M, host_.dsub, cbnorm_.p, stream_));
@@ -476,8 +477,7 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
                        d_qs, nq * host_.dim, err_.p);
     FDB_HIP(hipGetLastError());
   } else {
-    FDB_HIP(launch_coarse_select(d_qs, nq, host_.dim, centT_.p, host_.nlist, (int)np, probes_.p,
-                                 nullptr, err_.p, s));
+    coarse_.select(d_qs, nq, np, probes_.p, nullptr, err_.p, s);
   }
   if (timed) FDB_HIP(hipEventRecord(ev_[1], s));
   IvfPqScanArgs a{};
@@ -614,8 +614,7 @@ void IvfPqIndex::probe(const float* qs, uint64_t nq, uint32_t nprobe, int32_t* l
   q_.upload(qs, nq * host_.dim, stream_);
   probes_.reserve(nq * nprobe);
   probe_d_.reserve(nq * nprobe);
-  FDB_HIP(launch_coarse_select(q_.p, nq, host_.dim, centT_.p, host_.nlist, (int)nprobe, probes_.p,
-                               probe_d_.p, err_.p, stream_));
+  coarse_.select(q_.p, nq, nprobe, probes_.p, probe_d_.p, err_.p, stream_);
   FDB_HIP(hipMemcpyAsync(lists, probes_.p, 4 * nq * nprobe, hipMemcpyDeviceToHost, stream_));
   if (dists)
     FDB_HIP(hipMemcpyAsync(dists, probe_d_.p, 4 * nq * nprobe, hipMemcpyDeviceToHost, stream_));

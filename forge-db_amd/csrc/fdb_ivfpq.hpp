@@ -7,6 +7,7 @@
 #include <unordered_set>
 #include <vector>
 
+#include "fdb_flat.hpp"
 #include "fdb_format.hpp"
 #include "fdb_host.hpp"
 
@@ -34,6 +35,11 @@ class IvfPqIndex {
   // when the index shape has no fast kernel
   bool set_lut_mode(int mode);
   int lut_mode() const { return lut_mode_.load(std::memory_order_relaxed); }
+  // coarse selection strategy (CoarseQuantizer::set_mode)
+  void set_coarse_mode(int m) {
+    std::lock_guard<std::mutex> g(mu_);
+    coarse_.set_mode(m);
+  }
 
   void enable_reranking(const float* vectors_list_order, uint64_t factor);
 
@@ -92,6 +98,7 @@ class IvfPqIndex {
   std::mutex mu_;
 
   DevBuf<float> centroids_, centT_, codebooks_, cbnorm_, originals_;
+  CoarseQuantizer coarse_;
   DevBuf<uint32_t> off_;
   DevBuf<uint8_t> codes_;
   DevBuf<uint64_t> ids_;

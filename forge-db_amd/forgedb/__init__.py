@@ -44,7 +44,7 @@ EXPORTED_SYMBOLS = (
     "fdb_ivfpq_sync", "fdb_ivfpq_probe", "fdb_ivfpq_encode",
     "fdb_ivfpq_batch_search_device_timed", "fdb_ivfpq_set_lut_mode", "fdb_ivfpq_lut_mode",
     "fdb_ivfpq_search_filtered", "fdb_ivfpq_delete", "fdb_ivfpq_insert", "fdb_ivfpq_compact",
-    "fdb_ivfpq_len", "fdb_ivfpq_num_tombstones",
+    "fdb_ivfpq_len", "fdb_ivfpq_num_tombstones", "fdb_ivfpq_set_coarse_mode", "fdb_ivf_set_coarse_mode",
     "fdb_bf_create", "fdb_bf_add", "fdb_bf_remove", "fdb_bf_len", "fdb_bf_dimension",
     "fdb_bf_metric", "fdb_bf_load", "fdb_bf_save", "fdb_bf_destroy", "fdb_bf_export",
     "fdb_bf_search", "fdb_bf_batch_search", "fdb_bf_batch_search_device",
@@ -57,6 +57,7 @@ EXPORTED_SYMBOLS = (
 
 LUT_EXACT, LUT_FAST = 0, 1
 BF_AUTO, BF_EXACT, BF_SCREEN = 0, 1, 2
+COARSE_AUTO, COARSE_EXACT, COARSE_SCREEN = 0, 1, 2
 
 
 class DistanceMetric(enum.IntEnum):
@@ -131,6 +132,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fdb_ivfpq_delete": [_P, C.c_uint64, _P],
         "fdb_ivfpq_insert": [_P, _P, _P, C.c_uint64, C.c_uint32],
         "fdb_ivfpq_compact": [_P],
+        "fdb_ivfpq_set_coarse_mode": [_P, C.c_uint32],
+        "fdb_ivf_set_coarse_mode": [_P, C.c_uint32],
         "fdb_bf_create": [C.c_uint32, _P],
         "fdb_bf_add": [_P, _P, _P, C.c_uint64, C.c_uint32],
         "fdb_bf_remove": [_P, C.c_uint64, _P],
@@ -280,6 +283,10 @@ class IVFPQIndex:
 
     def lut_mode(self) -> int:
         return int(self._lib.fdb_ivfpq_lut_mode(self._h))
+
+    def set_coarse_mode(self, mode: int) -> None:
+        """COARSE_AUTO, COARSE_EXACT or COARSE_SCREEN; same probes in every mode."""
+        _check(self._lib, self._lib.fdb_ivfpq_set_coarse_mode(self._h, int(mode)))
 
     def dim(self) -> int:
         return self._dim
@@ -634,6 +641,10 @@ class IVFIndex:
 
     def nprobe(self) -> int:
         return int(self._lib.fdb_ivf_nprobe(self._h))
+
+    def set_coarse_mode(self, mode: int) -> None:
+        """COARSE_AUTO, COARSE_EXACT or COARSE_SCREEN; same probes in every mode."""
+        _check(self._lib, self._lib.fdb_ivf_set_coarse_mode(self._h, int(mode)))
 
     def __len__(self) -> int:
         return int(self._lib.fdb_ivf_len(self._h))

@@ -124,6 +124,19 @@ enum { FDB_LUT_EXACT = 0, FDB_LUT_FAST = 1 };
 FDB_API fdb_status fdb_ivfpq_set_lut_mode(fdb_ivfpq* index, uint32_t mode);
 FDB_API uint32_t fdb_ivfpq_lut_mode(const fdb_ivfpq* index);
 
+/* Coarse selection strategy (no counterpart in the reference):
+ *   FDB_COARSE_AUTO (default) and FDB_COARSE_EXACT: the exact-order VALU
+ *     kernel (faster at nlist <= 4096);
+ *   FDB_COARSE_SCREEN: MFMA screening when nprobe + 16 <= 128 and dim is a
+ *     multiple of 4 (<= 512).
+ * Screening computes approximate distances on the matrix cores, recomputes
+ * the best nprobe + 16..128 in the reference's order and proves from a
+ * rounding-error bound that no other list belongs to the nprobe nearest;
+ * queries where that fails go through the exact kernel.  The probed lists
+ * and their distances are the same in every mode. */
+enum { FDB_COARSE_AUTO = 0, FDB_COARSE_EXACT = 1, FDB_COARSE_SCREEN = 2 };
+FDB_API fdb_status fdb_ivfpq_set_coarse_mode(fdb_ivfpq* index, uint32_t mode);
+
 /* Copies the resident artifacts back (any pointer may be NULL). */
 FDB_API fdb_status fdb_ivfpq_export(const fdb_ivfpq* index, float* centroids, float* codebooks,
                                     uint64_t* list_offsets, uint64_t* ids, uint8_t* codes);
@@ -295,6 +308,8 @@ FDB_API fdb_status fdb_ivf_build(const float* vectors, const uint64_t* ids, uint
 FDB_API void fdb_ivf_destroy(fdb_ivf* index);
 /* set_nprobe (ivf.rs:125-127): min(nprobe, nlist); nprobe() (:130-132) */
 FDB_API void fdb_ivf_set_nprobe(fdb_ivf* index, uint64_t nprobe);
+/* Coarse selection strategy, as fdb_ivfpq_set_coarse_mode. */
+FDB_API fdb_status fdb_ivf_set_coarse_mode(fdb_ivf* index, uint32_t mode);
 FDB_API uint64_t fdb_ivf_nprobe(const fdb_ivf* index);
 /* len (:135), num_partitions (:145), dimension (:150) */
 FDB_API uint64_t fdb_ivf_len(const fdb_ivf* index);

@@ -16,8 +16,8 @@ import pytest
 
 import refcpu
 
-from forgedb import (BF_EXACT, BF_SCREEN, BruteForceIndex, DistanceMetric, ForgeDbError, IVFIndex,
-                     datagen)
+from forgedb import (BF_EXACT, BF_SCREEN, COARSE_SCREEN, BruteForceIndex, DistanceMetric, ForgeDbError,
+                     IVFIndex, datagen)
 
 pytestmark = pytest.mark.gpu
 
@@ -210,9 +210,11 @@ def ivf_small():
                 rows=base[order])
 
 
-def ivf_pair(s, metric, nprobe, k, queries=None):
+def ivf_pair(s, metric, nprobe, k, queries=None, coarse=None):
     q = s["queries"] if queries is None else queries
     g = IVFIndex.from_artifacts(s["cen"], s["off"], s["ids"], s["rows"], metric)
+    if coarse is not None:
+        g.set_coarse_mode(coarse)
     g.set_nprobe(nprobe)
     out = g.batch_search_arrays(q, k)
     ref = refcpu.ivf_batch_search(s["cen"], s["off"], s["ids"], s["rows"], int(metric), g.nprobe(),
@@ -226,6 +228,14 @@ def test_ivf_parity(ivf_small, metric, nprobe, k):
     print(f"ivf 24k x 96, nlist 128, nprobe {nprobe}, k {k}, {metric.name}", flush=True)
     _, (gi, gd, gc), (oi, od, oc) = ivf_pair(ivf_small, metric, nprobe, k)
     check_rows(gi, gd, gc, oi, od, oc, f"{metric.name} nprobe {nprobe}")
+
+
+@pytest.mark.parametrize("metric", [DistanceMetric.Euclidean, DistanceMetric.Manhattan])
+def test_ivf_parity_screened_coarse(ivf_small, metric):
+    print(f"ivf with screened coarse selection, {metric.name}", flush=True)
+    for nprobe, k in ((1, 10), (32, 100), (100, 5)):
+        _, (gi, gd, gc), (oi, od, oc) = ivf_pair(ivf_small, metric, nprobe, k, coarse=COARSE_SCREEN)
+        check_rows(gi, gd, gc, oi, od, oc, f"screened coarse {metric.name} nprobe {nprobe}")
 
 
 def test_ivf_single_search_nprobe_rules(ivf_small):

@@ -15,7 +15,7 @@ import pytest
 
 import refcpu
 
-from forgedb import DistanceMetric, ForgeDbError, IVFPQIndex, datagen
+from forgedb import COARSE_EXACT, COARSE_SCREEN, DistanceMetric, ForgeDbError, IVFPQIndex, datagen
 
 pytestmark = pytest.mark.gpu
 
@@ -38,11 +38,13 @@ def check_batch(gx, ox, queries, k, label):
         assert np.all(np.isinf(gd[q, c:]))
 
 
-def test_probe_parity_bit_exact(small_ivfpq):
-    print("probe parity: 64 queries, nlist 64, nprobe 1/16/64", flush=True)
+@pytest.mark.parametrize("mode", [COARSE_EXACT, COARSE_SCREEN], ids=["exact", "screen"])
+def test_probe_parity_bit_exact(small_ivfpq, mode):
+    print(f"probe parity: 64 queries, nlist 64, nprobe 1/16/48/64, coarse mode {mode}", flush=True)
     gx = gpu_index(small_ivfpq["art"])
+    gx.set_coarse_mode(mode)
     ox = small_ivfpq["oracle"]
-    for nprobe in (1, 16, 64):
+    for nprobe in (1, 16, 48, 64):
         lists, d = gx.probe(small_ivfpq["queries"], nprobe)
         for q, qv in enumerate(small_ivfpq["queries"]):
             ol, odist = ox.probes(qv, nprobe)
@@ -341,3 +343,32 @@ def test_search_filtered_parity(small_ivfpq, rerank):
             assert np.array_equal(gd[j, :len(oi)], od), label
         assert gx.search_filtered(q[0], k, allowed) == [(int(i), float(d)) for i, d in
                                                          zip(*ox.search_filtered(q[0], k, allowed))]
+
+
+@pytest.mark.parametrize("nprobe,k", [(1, 10), (16, 100), (48, 10)])
+def test_batch_search_screened_coarse(small_ivfpq, nprobe, k):
+    print(f"batch parity with screened coarse selection nprobe={nprobe} k={k}", flush=True)
+    gx = gpu_index(small_ivfpq["art"])
+    gx.set_coarse_mode(COARSE_SCREEN)
+    ox = small_ivfpq["oracle"]
+    gx.set_nprobe(nprobe)
+    ox.set_nprobe(nprobe)
+    check_batch(gx, ox, small_ivfpq["queries"], k, f"screened coarse np{nprobe} k{k}")
+    check_single(gx, ox, small_ivfpq["queries"][:8], k, f"screened coarse single np{nprobe}")
+
+
+def test_screened_coarse_duplicate_centroids(small_ivfpq):
+    print("screened coarse selection with duplicated centroids (exact ties)", flush=True)
+    art = dict(small_ivfpq["art"])
+    cen = art["centroids"].copy()
+    cen[32:] = cen[:32]  # every centroid has a twin: ties resolve to the lower list id
+    art["centroids"] = cen
+    ox = refcpu.IvfPq.create(cen, art["codebooks"], art["list_offsets"], art["ids"], art["codes"])
+    for mode in (COARSE_EXACT, COARSE_SCREEN):
+        gx = gpu_index(art)
+        gx.set_coarse_mode(mode)
+        for nprobe in (3, 16, 40):
+            lists, d = gx.probe(small_ivfpq["queries"], nprobe)
+            for q, qv in enumerate(small_ivfpq["queries"]):
+                ol, od = ox.probes(qv, nprobe)
+                assert np.array_equal(lists[q], ol) and np.array_equal(d[q], od), (mode, nprobe, q)
