@@ -150,14 +150,36 @@ def agreement(a, b, k):
 
 def cpu_sample(run, nq, seconds, probe_n):
     """Times run(m) on a probe of probe_n queries, then on a sample sized for
-    about `seconds` of CPU work; returns (sample, seconds, result)."""
+    about `seconds` of CPU work. When every query fits in less than that, the
+    whole set is searched in repeated passes (at most 30). Returns (queries
+    searched, seconds, result of the first pass, passes)."""
     t = time.perf_counter()
     run(probe_n)
     per_q = (time.perf_counter() - t) / probe_n
     sample = int(min(nq, max(probe_n, seconds / max(per_q, 1e-9))))
+    passes = 1
+    if sample == nq:
+        passes = int(min(30, max(1, seconds // max(per_q * nq, 1e-9))))
     t = time.perf_counter()
     out = run(sample)
-    return sample, time.perf_counter() - t, out
+    for _ in range(passes - 1):
+        run(sample)
+    return sample * passes, time.perf_counter() - t, out, passes
+
+
+def cpu_leg(run, nq, args, probe_n, gpu_ids, k, threads, how):
+    """The cpu_baseline object: run(m) searches the first m queries on the
+    host; its ids are compared with the GPU's on the same queries."""
+    searched, cpu_s, (oi, _, _), passes = cpu_sample(run, nq, args.cpu_seconds, probe_n)
+    sample = searched // passes
+    agree = agreement(gpu_ids[:sample], oi, k)
+    what = (f"all {nq} queries x {passes} passes" if passes > 1 else
+            f"first {sample} of the {nq} queries")
+    log(f"[bench] CPU baseline {searched / cpu_s:,.1f} QPS on {threads} threads "
+        f"({what} in {cpu_s:.1f}s); id agreement {agree:.6f}")
+    return {"value": round(searched / cpu_s, 1), "unit": "queries/s", "cores": threads,
+            "kind": "port", "sample": f"{what}, {how}, {cpu_s:.1f} s on {cpu_model()}",
+            "gpu_id_agreement": round(agree, 6)}
 
 
 def bench_ivfpq(args, w, base, queries):
@@ -230,17 +252,9 @@ def bench_ivfpq(args, w, base, queries):
                                      art["ids"], art["codes"])
         oracle.set_nprobe(nprobe)
         threads = min(16, os.cpu_count() or 1)
-        sample, cpu_s, (oi, _, _) = cpu_sample(
+        cpu = cpu_leg(
             lambda m: oracle.batch_search(queries[:m], k, parallel=True, nthreads=threads),
-            nq, args.cpu_seconds, min(nq, 200))
-        agree = agreement(exact_ids[:sample], oi, k)
-        cpu = {"value": round(sample / cpu_s, 1), "unit": "queries/s", "cores": threads,
-               "kind": "port",
-               "sample": f"first {sample} of the {nq} queries, batch_search_parallel "
-                         f"(chunks of 4), {cpu_s:.1f} s on {cpu_model()}",
-               "gpu_id_agreement": round(agree, 6)}
-        log(f"[bench] CPU baseline {sample / cpu_s:,.0f} QPS on {threads} threads "
-            f"({sample} queries in {cpu_s:.1f}s); id agreement {agree:.6f}")
+            nq, args, min(nq, 200), exact_ids, k, threads, "batch_search_parallel (chunks of 4)")
     cfg = {"n": base.shape[0], "nq": nq, "nlist": nlist, "M": M, "nprobe": nprobe, "k": k}
     return ms_per_step, roof, cpu, cfg, extra
 
@@ -278,17 +292,9 @@ def bench_bf(args, w, base, queries):
         import refcpu  # CPU baseline leg only
         threads = min(16, os.cpu_count() or 1)
         ids = np.arange(base.shape[0], dtype=np.uint64)
-        sample, cpu_s, (oi, _, _) = cpu_sample(
+        cpu = cpu_leg(
             lambda m: refcpu.bf_batch_search(base, ids, int(metric), queries[:m], k, threads),
-            nq, args.cpu_seconds, min(nq, 16))
-        agree = agreement(gpu_ids[:sample], oi, k)
-        cpu = {"value": round(sample / cpu_s, 1), "unit": "queries/s", "cores": threads,
-               "kind": "port",
-               "sample": f"first {sample} of the {nq} queries, batch_search (queries in "
-                         f"parallel), {cpu_s:.1f} s on {cpu_model()}",
-               "gpu_id_agreement": round(agree, 6)}
-        log(f"[bench] CPU baseline {sample / cpu_s:,.1f} QPS on {threads} threads "
-            f"({sample} queries in {cpu_s:.1f}s); id agreement {agree:.6f}")
+            nq, args, min(nq, 16), gpu_ids, k, threads, "batch_search (queries in parallel)")
     cfg = {"n": base.shape[0], "nq": nq, "k": k, "metric": metric.name}
     return ms_per_step, roof, cpu, cfg, {}
 
@@ -331,19 +337,11 @@ def bench_ivf(args, w, base, queries):
         import refcpu  # CPU baseline leg only
         art = index.export()
         threads = min(16, os.cpu_count() or 1)
-        sample, cpu_s, (oi, _, _) = cpu_sample(
+        cpu = cpu_leg(
             lambda m: refcpu.ivf_batch_search(art["centroids"], art["list_offsets"], art["ids"],
                                               art["rows"], int(metric), nprobe, queries[:m], k,
                                               threads),
-            nq, args.cpu_seconds, min(nq, 200))
-        agree = agreement(gpu_ids[:sample], oi, k)
-        cpu = {"value": round(sample / cpu_s, 1), "unit": "queries/s", "cores": threads,
-               "kind": "port",
-               "sample": f"first {sample} of the {nq} queries, batch_search (queries in "
-                         f"parallel), {cpu_s:.1f} s on {cpu_model()}",
-               "gpu_id_agreement": round(agree, 6)}
-        log(f"[bench] CPU baseline {sample / cpu_s:,.0f} QPS on {threads} threads "
-            f"({sample} queries in {cpu_s:.1f}s); id agreement {agree:.6f}")
+            nq, args, min(nq, 200), gpu_ids, k, threads, "batch_search (queries in parallel)")
     cfg = {"n": base.shape[0], "nq": nq, "nlist": nlist, "nprobe": nprobe, "k": k,
            "metric": metric.name}
     return ms_per_step, roof, cpu, cfg, {}

@@ -289,6 +289,40 @@ struct WaveTopK {
 
   static constexpr int kBulkThreshold = 6;
 
+  // Queued form of offer_valid for long scans.  Lanes that pass the
+  // threshold append their pair to a wave-private LDS queue q of 64 slots
+  // (qn pairs held, wave-uniform); a queue that would overflow is merged
+  // into the list in one merge64.  The threshold only moves at a merge, so a
+  // queued pair may turn out not to belong: the merge keeps the 64*R
+  // smallest of list and queue whatever was let in.  Call flush() before
+  // reading the list.
+  __device__ __forceinline__ void offer_queued(float dist, uint32_t key, bool valid, uint2* q, int& qn) {
+    uint64_t mask = __ballot(valid && dist <= tau);
+    if (mask == 0) return;
+    if (qn + __popcll(mask) > 64) {
+      flush(q, qn);
+      mask = __ballot(valid && dist <= tau);
+    }
+    const uint32_t before = __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+    if ((mask >> lane_id()) & 1) q[qn + (int)before] = make_uint2(__float_as_uint(dist), key);
+    qn += __popcll(mask);
+  }
+
+  // Merges the queue (qn pairs) into the list and empties it.  Queue slots
+  // are written and read by different lanes of the one wave; LDS operations
+  // of a wave complete in issue order, and the wave barriers keep the
+  // compiler from moving them across each other.
+  __device__ __forceinline__ void flush(uint2* q, int& qn) {
+    if (qn == 0) return;
+    __builtin_amdgcn_wave_barrier();
+    const int lane = lane_id();
+    const uint2 e = lane < qn ? q[lane] : make_uint2(__float_as_uint(f_inf()), kNoPos);
+    __builtin_amdgcn_wave_barrier();
+    merge64(__uint_as_float(e.x), e.y);
+    qn = 0;
+  }
+
   // One compare-exchange of a bitonic network: keep the smaller pair when
   // keep_min, else the larger.
   static __device__ __forceinline__ void cx(float& d0, uint32_t& p0, float d1, uint32_t p1,

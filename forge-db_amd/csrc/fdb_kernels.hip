@@ -239,10 +239,33 @@ template <int MT, int ORDER, int R, int NW, int U, int J, int FAST>
 __device__ __forceinline__ void scan_list(const float* __restrict__ lut, uint32_t start, uint32_t len,
                                           float base, uint32_t w0, int lane,
                                           const uint8_t* __restrict__ codes,
-                                          const uint32_t* __restrict__ live, WaveTopK<R>& tk) {
+                                          const uint32_t* __restrict__ live, WaveTopK<R>& tk,
+                                          uint2* queue, int& qn) {
   const uint32_t nb = (len + 63) / 64;
   const uint32_t last = start + len - 1;
-  for (uint32_t b0 = w0; b0 < nb; b0 += (uint32_t)(NW * U)) {
+  uint32_t b0 = w0;
+  // Steps whose U batches hold 64 codes each need no bounds or validity
+  // tests when no bitmap is given.
+  if (live == nullptr) {
+    const uint32_t nfull = len / 64;
+    for (; b0 + (uint32_t)((U - 1) * NW) < nfull; b0 += (uint32_t)(NW * U)) {
+      uint32_t w[U][(MT + 3) / 4];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        load_code<MT>(codes, start + (b0 + (uint32_t)(u * NW)) * 64 + (uint32_t)lane, w[u]);
+      float dist[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        dist[u] = adc_sum<MT, ORDER>(lut + J * (MT * 256), w[u]);
+        if constexpr (FAST) dist[u] = base + dist[u];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        tk.offer_queued(dist[u], start + (b0 + (uint32_t)(u * NW)) * 64 + (uint32_t)lane, true, queue,
+                        qn);
+    }
+  }
+  for (; b0 < nb; b0 += (uint32_t)(NW * U)) {
     uint32_t w[U][(MT + 3) / 4];
     uint32_t key[U];
 #pragma unroll
@@ -261,7 +284,7 @@ __device__ __forceinline__ void scan_list(const float* __restrict__ lut, uint32_
       if constexpr (FAST) dist[u] = base + dist[u];
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) tk.offer_valid(dist[u], key[u], key[u] != kNoPos);
+    for (int u = 0; u < U; ++u) tk.offer_queued(dist[u], key[u], key[u] != kNoPos, queue, qn);
   }
 }
 
@@ -269,12 +292,14 @@ template <int MT, int ORDER, int R, int NW, int U, int GMAX, int J, int FAST>
 __device__ __forceinline__ void scan_group(const float* __restrict__ lut, const float* __restrict__ rr,
                                            const GroupLists<GMAX>& gl, uint32_t w0, int lane,
                                            const uint8_t* __restrict__ codes,
-                                           const uint32_t* __restrict__ live, WaveTopK<R>& tk) {
+                                           const uint32_t* __restrict__ live, WaveTopK<R>& tk,
+                                           uint2* queue, int& qn) {
   if (J < gl.ng && gl.len[J] > 0)
     scan_list<MT, ORDER, R, NW, U, J, FAST>(lut, gl.start[J], gl.len[J], FAST ? rr[J] : 0.0f, w0,
-                                            lane, codes, live, tk);
+                                            lane, codes, live, tk, queue, qn);
   if constexpr (J + 1 < GMAX)
-    scan_group<MT, ORDER, R, NW, U, GMAX, J + 1, FAST>(lut, rr, gl, w0, lane, codes, live, tk);
+    scan_group<MT, ORDER, R, NW, U, GMAX, J + 1, FAST>(lut, rr, gl, w0, lane, codes, live, tk,
+                                                       queue, qn);
 }
 
 // One workgroup per query.  MT/DT: compile-time M and dsub (0 = runtime, then
@@ -294,6 +319,8 @@ void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
   constexpr int SLDS = (MT > 0) ? (SLUT > NW * 64 * R * 2 ? SLUT : NW * 64 * R * 2) : 1;
   __shared__ float s_static[SLDS];
   __shared__ float s_rr[GMAX];  // fast mode: |q - c_p|^2 of each list of the group
+  // per-wave candidate queues (specialised shapes)
+  __shared__ uint2 s_queue[MT > 0 ? NW * 64 : 1];
   extern __shared__ float s_dyn[];
   float* smem = (MT > 0) ? s_static : s_dyn;
   const int M = MT ? MT : a.M;
@@ -311,6 +338,8 @@ void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
 
   WaveTopK<R> tk;
   tk.init(a.k);
+  uint2* queue = s_queue + (MT > 0 ? wave * 64 : 0);
+  int qn = 0;
 
   for (int g0 = 0; g0 < a.np; g0 += G) {
     const int ng = min(G, a.np - g0);
@@ -383,7 +412,8 @@ void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
     __syncthreads();
 
     if constexpr (MT > 0) {
-      scan_group<MT, ORDER, R, NW, U, GMAX, 0, FAST>(lut, s_rr, gl, w0, lane, a.codes, a.live, tk);
+      scan_group<MT, ORDER, R, NW, U, GMAX, 0, FAST>(lut, s_rr, gl, w0, lane, a.codes, a.live, tk,
+                                                     queue, qn);
     } else {
       // generic shape: lists one after another, one code per lane
       for (int j = 0; j < ng; ++j) {
@@ -406,6 +436,7 @@ void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
     __syncthreads();
   }
 
+  tk.flush(queue, qn);
   // merge the wave lists in wave 0
   float* md = smem;
   uint32_t* mp = reinterpret_cast<uint32_t*>(smem + NW * 64 * R);
