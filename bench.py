@@ -42,6 +42,7 @@ sys.path.insert(0, os.path.join(ROOT, "forge-db_amd"))
 
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
 
 WORKLOADS = {
     "ivfpq_1m": dict(kind="ivfpq", data="ivfpq_int", n=1_000_000, nq=10_000, nlist=1024, M=16,
@@ -266,6 +267,7 @@ def bench_bf(args, w, base, queries):
     k, metric = w["k"], DistanceMetric(w["metric"])
     t = time.time()
     index = BruteForceIndex.from_arrays(base, None, metric)
+    index.set_search_mode({"auto": 0, "exact": 1, "screen": 2, "screen_f32": 3}[args.bf_mode])
     r = Runner(args, queries, k)
     nq = r.nq
 
@@ -279,13 +281,20 @@ def bench_bf(args, w, base, queries):
     log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step, {nq / ms_per_step * 1e3:,.0f} QPS")
     kms = float(np.mean([index.batch_search_device(*r.ptrs(), timed=True)
                          for _ in range(args.timing_reps)]))
+    path = index.last_search_path()
+    fallbacks = index.last_fallbacks()
     flops = 2.0 * nq * base.shape[0] * base.shape[1]
     achieved = flops / (kms / 1e3) / 1e12
-    log(f"[bench] search kernels {kms:.3f} ms -> {achieved:.1f} TFLOP/s (2*Q*N*D)")
-    roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": None,
-            "kernel": "flat_topk_kernel + merge_parts_kernel", "kernel_ms": round(kms, 4),
-            "algorithmic_flops": flops}
+    # the product each path runs on: exact-order fp32 VALU, fp32 or fp16 matrix cores
+    peak, kernel = {0: (FP32_PEAK_TFLOPS, "flat_topk_kernel + merge_parts_kernel"),
+                    1: (FP32_PEAK_TFLOPS, "mfma_screen_kernel (fp32) + rescore_kernel"),
+                    2: (FP16_PEAK_TFLOPS, "screen16_kernel (fp16) + select16_kernel + rescore_kernel")}[path]
+    log(f"[bench] search kernels {kms:.3f} ms -> {achieved:.1f} TFLOP/s (2*Q*N*D); path {path}, "
+        f"{fallbacks} of {nq} queries rescanned exactly")
+    roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
+            "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
+            "kernel": kernel, "kernel_ms": round(kms, 4), "algorithmic_flops": flops,
+            "fallbacks": fallbacks}
     gpu_ids = r.ids().copy()
     cpu = None
     if not args.no_cpu:
@@ -361,6 +370,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target wall time of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--bf-mode", default="auto", choices=["auto", "exact", "screen", "screen_f32"],
+                    help="brute-force search strategy (BruteForceIndex.set_search_mode)")
     ap.add_argument("--coarse", default="auto", choices=["auto", "exact", "screen"],
                     help="coarse selection strategy of the IVF indexes (same probes)")
     ap.add_argument("--calibrate-copy", action="store_true",

@@ -470,8 +470,15 @@ fdb_status fdb_bf_batch_search_device(fdb_bf* h, const float* d_queries, uint64_
 
 fdb_status fdb_bf_set_search_mode(fdb_bf* h, uint32_t mode) {
   return guarded([&] {
-    if (mode > 2) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown search mode");
+    if (mode > 3) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown search mode");
     impl_of(h)->set_screen_mode((int)mode);
+  });
+}
+
+fdb_status fdb_bf_last_search_path(fdb_bf* h, uint32_t* out) {
+  return guarded([&] {
+    if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    *out = (uint32_t)impl_of(h)->last_path();
   });
 }
 

@@ -416,6 +416,37 @@ __device__ __forceinline__ float screen_eps(int met, int dim, float qn, float rn
   return (4.4f * g + 12.0f * u) * (qn + rnmax) + 1e-30f;
 }
 
+// The same bound for screening values from the fp16 product
+// (v_mfma_f32_32x32x16_f16).  Rows and queries (for cosine: divided by
+// their norms first) are scaled by powers of two so that their largest
+// component lies in [2^13, 2^14) and rounded to fp16: each component is
+// then off by at most uh = 2^-11 relative plus 2^-27 of the vector's
+// largest component (values below the smallest fp16 normal, even if
+// flushed).  The products of fp16 values are exact in fp32 and their sum is
+// within g2 = dim*2u/(1 - dim*2u) of the exact sum in any order, rounded or
+// truncated.  With h = 2uh + uh^2 + eta + 1.002*g2*(1 + eta), eta =
+// 2.002*2^-27*sqrt(dim) + dim*2^-54:
+//   dot:     (h + g) |q||x|, g for the reference's own sum
+//   cosine:  h + g + 7u for the division by the norms, then the fp32
+//            screen's 2.2g + 16u (both roundings of 1 - x and the
+//            reference's cosine)
+//   L2^2:    (h + 4g + 9u) (qn + rnmax): the product as for dot, the norms,
+//            the three roundings of qn + rn - 2s and the reference's sum of
+//            squares
+// with 10% slack and a floor for products and sums near the fp32 underflow.
+__device__ __forceinline__ float screen16_eps(int met, int dim, float qn, float rnmax) {
+  const float u = 5.9604645e-8f;
+  const float uh = 4.8828125e-4f;
+  const float g = dim * u / (1.0f - dim * u);
+  const float g2 = dim * 2.0f * u / (1.0f - dim * 2.0f * u);
+  const float eta = 2.002f * 7.4505806e-9f * __builtin_sqrtf((float)dim) + dim * 5.551115e-17f;
+  const float h = 2.0f * uh + uh * uh + eta + 1.002f * g2 * (1.0f + eta);
+  if (met == FDB_METRIC_DOT_PRODUCT)
+    return 1.1f * (h + g) * __builtin_sqrtf(qn) * __builtin_sqrtf(rnmax) + 1e-30f;
+  if (met == FDB_METRIC_COSINE) return 1.1f * (h + 3.2f * g + 23.0f * u) + 1e-30f;
+  return 1.1f * (h + 4.0f * g + 9.0f * u) * (qn + rnmax) + 1e-30f;
+}
+
 template <int MET, int RS>
 __global__ __launch_bounds__(kT) void mfma_screen_kernel(ScreenArgs a) {
   extern __shared__ float sm[];
@@ -513,7 +544,9 @@ __global__ __launch_bounds__(64) void rescore_kernel(RescoreArgs a) {
   for (int d = lane; d < dim; d += 64) qv[d] = a.queries[q * dim + d];
   __syncthreads();
   const int kp = 64 * RS;
-  const uint32_t cnt = a.cand_counts[q];
+  const uint32_t cnt0 = a.cand_counts[q];
+  const bool forced = cnt0 == kForceExact;
+  const uint32_t cnt = forced ? 0u : cnt0;
   const float qn = a.q_norm[q];
   constexpr int EM = (MET == FDB_METRIC_EUCLIDEAN) ? FDB_METRIC_EUCLIDEAN_SQUARED : MET;
   WaveTopK<RK> tk;
@@ -528,9 +561,11 @@ __global__ __launch_bounds__(64) void rescore_kernel(RescoreArgs a) {
     tk.offer(e, key);
   }
   const uint32_t kk = (uint32_t)a.k < cnt ? (uint32_t)a.k : cnt;
-  bool ok = true;
-  if (cnt >= (uint32_t)kp && kk > 0) {
-    const float aK = a.cand_d[q * kp + kp - 1];
+  bool ok = !forced;
+  // with a threshold bound, fewer candidates than the top k needs is a miss
+  if (a.abound && (uint64_t)kk < ((uint64_t)a.k < a.n ? (uint64_t)a.k : a.n)) ok = false;
+  if (ok && kk > 0 && (a.abound || cnt >= (uint32_t)kp)) {
+    const float aK = a.abound ? a.abound[q] : a.cand_d[q * kp + kp - 1];
     const int s = (int)kk - 1;
     // the k-th exact pair, in the screening domain
     float v = tk.d[0];
@@ -549,7 +584,8 @@ __global__ __launch_bounds__(64) void rescore_kernel(RescoreArgs a) {
     } else {
       v = readlane_f(v, s & 63);
     }
-    ok = aK - screen_eps(MET, dim, qn, a.rnmax) > v;
+    const float eps = a.h16 ? screen16_eps(MET, dim, qn, a.rnmax) : screen_eps(MET, dim, qn, a.rnmax);
+    ok = aK - eps > v;
   }
   uint32_t count = 0;
 #pragma unroll
@@ -812,6 +848,9 @@ void BruteForceIndex::sync_device() {
     FDB_HIP(hipStreamSynchronize(stream_));
     rnmax_ = 0.0f;
     for (float v : rn) rnmax_ = std::max(rnmax_, v);  // NaN rows leave it unchanged
+    h16_.build(rows_.p, row_norm_.p, n, (int)dim_, (int)metric_, stream_);
+  } else {
+    h16_.ok = false;
   }
   n_dev_ = n;
   dirty_ = false;
@@ -995,7 +1034,7 @@ void CoarseQuantizer::select(const float* d_qs, uint64_t nq, uint32_t np, int32_
 bool BruteForceIndex::screen_applies(uint64_t nq, uint32_t k) const {
   if (!FlatSearcher::screenable((int)metric_, (int)dim_, k) || n_dev_ <= 64 || screen_mode_ == 1)
     return false;
-  return screen_mode_ == 2 || nq * n_dev_ >= (1ull << 26);
+  return screen_mode_ >= 2 || nq * n_dev_ >= (1ull << 26);
 }
 
 FlatRows BruteForceIndex::flat_rows() const {
@@ -1005,7 +1044,7 @@ FlatRows BruteForceIndex::flat_rows() const {
 void BruteForceIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids,
                           float* d_dists, uint32_t* d_counts, hipStream_t s) {
   if (nq == 0) return;
-  searched_ = false;
+  path_ = 0;
   if (k == 0 || n_dev_ == 0) {
     hipLaunchKernelGGL(fill_empty, dim3(nblocks(nq * std::max<uint32_t>(k, 1), 256)), dim3(256), 0, s,
                        nq, k, d_ids, d_dists, d_counts);
@@ -1019,8 +1058,13 @@ void BruteForceIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* 
     FDB_HIP(launch_row_norms(d_qs, nq, dim_, qn_.p, s));
   }
   if (screen) {
-    srch_.screen(flat_rows(), (int)metric_, d_qs, qn_.p, nq, k, d_ids, d_dists, d_counts, s);
-    searched_ = true;
+    if (screen_mode_ != 3 && FlatSearcher::screenable16(h16_, (int)metric_, k)) {
+      srch_.screen16(flat_rows(), h16_, (int)metric_, d_qs, qn_.p, nq, k, d_ids, d_dists, d_counts, s);
+      path_ = 2;
+    } else {
+      srch_.screen(flat_rows(), (int)metric_, d_qs, qn_.p, nq, k, d_ids, d_dists, d_counts, s);
+      path_ = 1;
+    }
   } else {
     srch_.exact(flat_rows(), (int)metric_, d_qs, qn_.p, nq, k, d_ids, d_dists, d_counts, s);
   }
@@ -1028,7 +1072,7 @@ void BruteForceIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* 
 
 uint64_t BruteForceIndex::last_fallbacks(hipStream_t s) {
   std::lock_guard<std::mutex> g(mu_);
-  if (!searched_ || !srch_.fallbacks()) return 0;  // the last search did not screen
+  if (path_ == 0 || !srch_.fallbacks()) return 0;  // the last search did not screen
   FDB_HIP(hipStreamSynchronize(s ? s : stream_));
   uint32_t v = 0;
   FDB_HIP(hipMemcpy(&v, srch_.fallbacks(), 4, hipMemcpyDeviceToHost));

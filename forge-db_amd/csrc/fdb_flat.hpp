@@ -71,6 +71,11 @@ hipError_t launch_mfma_screen(const ScreenArgs& a, hipStream_t s);
 // Exact rescoring of screened candidates ([nq][kp], ascending, as merged):
 // writes the k smallest exact results, flags [nq] (1 = the candidates may
 // miss a top-k row) and adds the number of flagged queries to *fallbacks.
+// abound (nullable): per query, a value that every row outside the
+// candidates screens above (threshold screening); then a query with fewer
+// than min(k, n) candidates, or with cand_counts = kForceExact, is flagged.
+// h16: the screening values came from the fp16 product (screen16_eps).
+constexpr uint32_t kForceExact = 0xFFFFFFFFu;
 struct RescoreArgs {
   const float* queries;
   int dim;
@@ -90,6 +95,9 @@ struct RescoreArgs {
   uint32_t* out_counts;
   int* flags;
   uint32_t* fallbacks;
+  const float* abound;
+  int h16;
+  uint64_t n;
 };
 hipError_t launch_rescore(const RescoreArgs& a, uint64_t nq, hipStream_t s);
 
@@ -129,6 +137,28 @@ struct FlatRows {
   const uint64_t* ids;    // nullable: results carry row indices
 };
 
+// The rows of a FlatRows as the fp16 screening reads them: 32-row blocks of
+// MFMA A operands (kb k-steps of 16 dimensions, zero-padded), scaled by
+// 2^xexp (cosine: each row divided by its norm first), and for Euclidean the
+// squared norms zero-padded to whole blocks.  ok = false when the rows do
+// not fit fp16 (non-finite values, zero-norm rows for cosine, a dimension
+// above 512 or not a multiple of 4, Manhattan).
+int h16_ksteps(int dim);
+struct H16Rows {
+  bool ok = false;
+  uint64_t n_ = 0, nblk = 0;
+  int dim_ = 0, kb = 0, xexp = 0;
+  float rnmin = 0.0f;  // cosine: the smallest squared row norm
+  void build(const float* rows, const float* row_norm, uint64_t n, int dim, int metric, hipStream_t s);
+  const uint16_t* x16() const { return x16_.p; }
+  const float* rn16() const { return rn16_.p; }
+
+ private:
+  DevBuf<uint16_t> x16_;
+  DevBuf<float> rn16_;
+  DevBuf<uint32_t> stats_;
+};
+
 // The k smallest (distance, row) per query over a FlatRows, by the exact VALU
 // scan or by MFMA screening + exact rescoring (same results).  Owns its
 // scratch; one user at a time.
@@ -136,19 +166,25 @@ class FlatSearcher {
  public:
   // whether screening serves (metric, dim, k)
   static bool screenable(int metric, int dim, uint32_t k);
+  static bool screenable16(const H16Rows& h, int metric, uint32_t k);
   // q_norm: [nq] reference-order query norms (cosine and screening)
   void exact(const FlatRows& x, int metric, const float* d_qs, const float* q_norm, uint64_t nq,
              uint32_t k, uint64_t* ids, float* d, uint32_t* c, hipStream_t s, const int* flags = nullptr);
   void screen(const FlatRows& x, int metric, const float* d_qs, const float* q_norm, uint64_t nq,
               uint32_t k, uint64_t* ids, float* d, uint32_t* c, hipStream_t s);
+  // fp16 screening (fdb_screen16.hip) over the same rows prepared as h
+  void screen16(const FlatRows& x, const H16Rows& h, int metric, const float* d_qs, const float* q_norm,
+                uint64_t nq, uint32_t k, uint64_t* ids, float* d, uint32_t* c, hipStream_t s);
   // device counter: queries of the last screen() rescanned exactly
   const uint32_t* fallbacks() const { return fallbacks_.p; }
 
  private:
-  DevBuf<float> part_d_, cand_d_;
-  DevBuf<uint32_t> part_k_, cand_c_, fallbacks_;
+  DevBuf<float> part_d_, cand_d_, tau_, abound_;
+  DevBuf<uint32_t> part_k_, cand_c_, fallbacks_, count_;
   DevBuf<uint64_t> cand_k_;
-  DevBuf<int> flags_;
+  DevBuf<int> flags_, qexp_, force_;
+  DevBuf<uint16_t> q16_;
+  DevBuf<uint2> buf_;
 };
 
 // Keys [n] as written by FlatSearcher with ids == nullptr (~0 = none) -> int32
@@ -215,12 +251,18 @@ class BruteForceIndex {
                            float* d_dists, uint32_t* d_counts, hipStream_t s, float* ms = nullptr);
 
   // 0 = automatic (MFMA screening where it applies), 1 = exact VALU scan
-  // only, 2 = screening where it applies
+  // only, 2 = screening where it applies, 3 = screening with the fp32
+  // product only (modes 0 and 2 take the fp16 product where the rows fit it)
   void set_screen_mode(int m) { screen_mode_ = m; }
   int screen_mode() const { return screen_mode_; }
   // queries of the last search that the screening check sent to the exact
   // scan (waits for the stream s, null: own stream)
   uint64_t last_fallbacks(hipStream_t s);
+  // how the last search ran: 0 exact scan, 1 fp32 screening, 2 fp16 screening
+  int last_path() {
+    std::lock_guard<std::mutex> g(mu_);
+    return path_;
+  }
 
  private:
   void sync_device();  // re-uploads the rows after add/remove (caller holds mu_)
@@ -240,8 +282,9 @@ class BruteForceIndex {
   DevBuf<uint64_t> ids_;
   uint64_t ld_ = 0;
   float rnmax_ = 0.0f;
+  H16Rows h16_;
   int screen_mode_ = 0;
-  bool searched_ = false;
+  int path_ = 0;  // the last search: 0 exact scan, 1 fp32 screening, 2 fp16 screening
   // scratch
   FlatSearcher srch_;
   DevBuf<float> q_, qn_, out_d_;

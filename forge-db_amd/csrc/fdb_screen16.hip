@@ -1,0 +1,555 @@
+// Brute-force screening on the fp16 matrix cores (v_mfma_f32_32x32x16_f16)
+// with a ladder of thresholds, followed by the exact rescoring of
+// fdb_flat.hip.  The reference computes every distance exactly
+// (brute_force.rs:141-146 / :162-225); here the fp16 product only decides
+// which rows are rescored, and screen16_eps bounds how far its value can be
+// from the reference's, so the results are the reference's (queries the
+// bound cannot settle are rescanned exactly).
+//
+// Stages.  Every stage runs the same kernel over a set of 32-row blocks: a
+// row whose screening value is at most the query's threshold tau is
+// appended to the query's buffer.  The first stage takes 32 evenly spaced
+// blocks with tau = +inf; after each stage tau becomes the m-th smallest
+// value appended (m ~ 32, so about 1024 rows of the next, 32x larger, sample
+// pass it).  The last stage covers every block; the K' smallest of its
+// buffer are rescored, and every other row screens above
+// min(K'-th value, tau).  The thresholds only steer the amount of work:
+// correctness rests on the last stage and the bound.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "fdb_device.hpp"
+#include "fdb_flat.hpp"
+
+namespace fdb {
+
+namespace {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int kT16 = 256;        // threads per screening workgroup (4 waves)
+constexpr int kStageKiB = 32;    // LDS per workgroup: one stage of row blocks
+constexpr uint32_t kCap = 4096;  // buffer entries per query
+constexpr uint64_t kSlice = 8192;  // queries per pass (buffers: 256 MB)
+
+// Exponent e with maxabs * 2^e in [2^13, 2^14); 0 for 0 or non-finite.
+__device__ __forceinline__ int scale_exp(float maxabs) {
+  if (!(maxabs > 0.0f) || !(maxabs < __builtin_huge_valf())) return 0;
+  int e;
+  (void)frexpf(maxabs, &e);  // maxabs in [2^(e-1), 2^e)
+  return 14 - e;
+}
+
+__device__ __forceinline__ uint32_t f2u_abs(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
+
+// ---- rows (at index sync) ------------------------------------------------
+
+__global__ void init_stats(uint32_t* s) {
+  s[0] = 0;
+  s[1] = 0;
+  s[2] = 0x7F7FFFFFu;  // FLT_MAX
+}
+
+// stats[0]: bits of max |x| (of x / |x| for cosine; NaN/inf compare above
+// every finite value); cosine only: stats[1] rows whose squared norm is not
+// a finite normal float (zero rows included), stats[2] bits of the smallest
+// squared norm.
+__global__ __launch_bounds__(256) void rows_absmax_kernel(const float* __restrict__ rows, uint64_t n, int dim,
+                                                          const float* __restrict__ rn, int cosine,
+                                                          uint32_t* __restrict__ stats) {
+  const uint64_t r = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= n) return;
+  float scale = 1.0f;
+  if (cosine) {
+    const float nr = rn[r];
+    const float inv = 1.0f / __builtin_sqrtf(nr);
+    if (!(nr >= 1.17549435e-38f) || !(nr <= 3.40282347e38f) || !(inv < __builtin_huge_valf())) {
+      if (lane == 0) atomicAdd(&stats[1], 1u);
+      return;
+    }
+    if (lane == 0) atomicMin(&stats[2], __float_as_uint(nr));
+    scale = inv;
+  }
+  uint32_t m = 0;
+  for (int d = lane; d < dim; d += 64) m = std::max(m, f2u_abs(rows[r * dim + d] * scale));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = std::max(m, (uint32_t)__shfl_xor((int)m, off));
+  if (lane == 0) atomicMax(&stats[0], m);
+}
+
+// Blocked fp16 rows: block b (rows 32b..32b+31), k-step kb, lane l holds the
+// 8 halves of row 32b + l%32, dims 16kb + 8(l/32) + 0..7 (zero beyond n or
+// dim): the A operand of one v_mfma_f32_32x32x16_f16, 1 KiB contiguous.
+__global__ __launch_bounds__(256) void rows_to_h16_kernel(const float* __restrict__ rows, uint64_t n, int dim,
+                                                          int kb, const float* __restrict__ rn, int cosine,
+                                                          int ex, v8h* __restrict__ out, uint64_t units) {
+  const uint64_t u = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= units) return;
+  const int l = (int)(u & 63);
+  const uint64_t bk = u >> 6;  // b * kb + kstep
+  const uint64_t b = bk / (uint64_t)kb;
+  const int ks = (int)(bk - b * (uint64_t)kb);
+  const uint64_t r = b * 32 + (uint64_t)(l & 31);
+  const int d0 = 16 * ks + 8 * (l >> 5);
+  v8h h;
+  float scale = 1.0f;
+  if (r < n && cosine) scale = 1.0f / __builtin_sqrtf(rn[r]);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int d = d0 + t;
+    const float v = (r < n && d < dim) ? ldexpf(rows[r * dim + d] * scale, ex) : 0.0f;
+    h[t] = (_Float16)v;
+  }
+  out[u] = h;
+}
+
+__global__ void pad_norms_kernel(const float* __restrict__ rn, uint64_t n, uint64_t npad, float* __restrict__ out) {
+  const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < npad) out[i] = i < n ? rn[i] : 0.0f;
+}
+
+// ---- queries (per pass) -------------------------------------------------------
+
+// One wave per query slot of the padded tiles: blocked fp16 operand (the B
+// operand: lane l holds query 32t + l%32, dims 16kb + 8(l/32) + 0..7), its
+// exponent, tau = +inf (-inf and forced for a query the fp16 path cannot
+// take), count = 0.  Cosine: the reference divides by sqrt(qn * rn), which
+// must stay clear of underflow and overflow for every row (rn in [rnmin,
+// rnmax]) for the normalised product to stand for it.
+__global__ __launch_bounds__(64) void queries_to_h16_kernel(const float* __restrict__ qs, uint64_t nq, int dim,
+                                                            int kb, const float* __restrict__ qn, int cosine,
+                                                            float rnmin, float rnmax, int ex,
+                                                            v8h* __restrict__ q16, int* __restrict__ qexp,
+                                                            float* __restrict__ tau, uint32_t* __restrict__ count,
+                                                            int* __restrict__ force) {
+  const uint64_t q = blockIdx.x;
+  const int lane = threadIdx.x;
+  const bool real = q < nq;
+  float scale = 1.0f;
+  bool bad = false;
+  if (real && cosine) {
+    const float n2 = qn[q];
+    scale = 1.0f / __builtin_sqrtf(n2);
+    bad = !(n2 >= 1.17549435e-38f) || !(scale < __builtin_huge_valf()) ||
+          !(n2 * rnmin >= 7.8886091e-31f) || !(n2 * rnmax <= 1.2676506e30f);  // 2^-100, 2^100
+  }
+  uint32_t m = 0;
+  if (real && !bad)
+    for (int d = lane; d < dim; d += 64) m = std::max(m, f2u_abs(qs[q * dim + d] * scale));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = std::max(m, (uint32_t)__shfl_xor((int)m, off));
+  const float maxabs = __uint_as_float(m);
+  bad = bad || !(maxabs < __builtin_huge_valf());
+  const int e = scale_exp(maxabs);
+  // the unscaling factor 2^-(e + ex) must stay a normal float
+  bad = bad || e + ex > 120 || e + ex < -120;
+  const uint64_t tile = q >> 5;
+  const int ql = (int)(q & 31);
+  for (int d = lane; d < 16 * kb; d += 64) {
+    const float v = (real && !bad && d < dim) ? ldexpf(qs[q * dim + d] * scale, e) : 0.0f;
+    const int ks = d >> 4, half = (d >> 3) & 1, t = d & 7;
+    reinterpret_cast<_Float16*>(q16)[(((tile * kb + ks) * 64) + ql + 32 * half) * 8 + t] = (_Float16)v;
+  }
+  if (lane == 0 && real) {
+    qexp[q] = e;
+    tau[q] = bad ? -__builtin_huge_valf() : __builtin_huge_valf();
+    count[q] = 0;
+    force[q] = bad ? 1 : 0;
+  }
+}
+
+// ---- the screening kernel ---------------------------------------------------------
+
+struct Screen16Args {
+  const v8h* x16;
+  uint64_t n, nblk;
+  const float* rn16;  // [nblk*32] squared norms, zero-padded (L2 only)
+  const v8h* q16;     // [qtiles][kb][64]
+  uint64_t nq;
+  const float* qn;    // [nq] (L2 only)
+  const int* qexp;    // [nq]
+  int xexp;
+  const float* tau;   // [nq]
+  uint32_t* count;    // [nq]
+  uint2* buf;         // [nq][kCap] (screening value bits, row)
+  uint64_t bstride, nsel, chunk_blocks;
+};
+
+enum { kScrDot = 0, kScrCos = 1, kScrL2 = 2 };
+
+// Workgroup: 4 waves x T query tiles of 32 (128T queries) over a chunk of
+// the selected blocks.  The queries' operands stay in registers; each stage
+// of SB = 32/KB row blocks goes through LDS once and feeds every wave.  Per
+// block and tile a lane holds 16 products of its query (32t + lane%32) with
+// rows 8(r/4) + 4(lane/32) + r%4 and tests them against its threshold.
+template <int MET, int KB, int T>
+__global__ __launch_bounds__(kT16) void screen16_kernel(Screen16Args a) {
+  constexpr int SB = (kStageKiB / KB) > 0 ? kStageKiB / KB : 1;
+  __shared__ v8h stage[SB * KB * 64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int h = lane >> 5;
+  const uint64_t tile0 = (uint64_t)blockIdx.x * (4 * T) + (uint64_t)wave * T;
+
+  v8h bq[T][KB];
+  float thr[T], fac[T], qnv[T];
+  uint64_t qidx[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const uint64_t tile = tile0 + t;
+    const uint64_t q = tile * 32 + (uint64_t)(lane & 31);
+    qidx[t] = q;
+    const bool real = q < a.nq;
+#pragma unroll
+    for (int ks = 0; ks < KB; ++ks) bq[t][ks] = a.q16[(tile * KB + ks) * 64 + lane];
+    const float tq = real ? a.tau[q] : -__builtin_huge_valf();
+    const int e = (real ? a.qexp[q] : 0) + a.xexp;
+    if constexpr (MET == kScrDot) {
+      thr[t] = ldexpf(-tq, e);   // -acc * 2^-e <= tau  <=>  acc >= -tau * 2^e
+      fac[t] = -ldexpf(1.0f, -e);
+    } else if constexpr (MET == kScrCos) {
+      thr[t] = tq;
+      fac[t] = -ldexpf(1.0f, -e);  // v = 1 - acc * 2^-e, one rounding
+    } else {
+      thr[t] = tq;
+      fac[t] = -ldexpf(2.0f, -e);  // v = (qn + rn) - 2 * acc * 2^-e
+      qnv[t] = real ? a.qn[q] : 0.0f;
+    }
+  }
+
+  const uint64_t j0 = (uint64_t)blockIdx.y * a.chunk_blocks;
+  const uint64_t j1 = std::min<uint64_t>(a.nsel, j0 + a.chunk_blocks);
+  constexpr int kUnits = SB * KB * 64;
+  for (uint64_t js = j0; js < j1; js += SB) {
+    __syncthreads();  // the previous stage is consumed
+    for (int u = tid; u < kUnits; u += kT16) {
+      const int bs = u / (KB * 64);
+      const uint64_t j = js + (uint64_t)bs;
+      if (j < j1) stage[u] = a.x16[(j * a.bstride * KB) * 64 + (uint64_t)(u - bs * KB * 64)];
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int bs = 0; bs < SB; ++bs) {
+      const uint64_t j = js + (uint64_t)bs;
+      if (j >= j1) break;
+      const uint64_t gb = j * a.bstride;
+      v16f acc[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) acc[t] = v16f{};
+#pragma unroll
+      for (int ks = 0; ks < KB; ++ks) {
+        const v8h av = stage[(bs * KB + ks) * 64 + lane];
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bq[t][ks], acc[t], 0, 0, 0);
+      }
+      const uint64_t rbase = gb * 32 + (uint64_t)(4 * h);
+      float rnv[16];
+      if constexpr (MET == kScrL2) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 v4 = *reinterpret_cast<const float4*>(a.rn16 + rbase + 8 * g);
+          rnv[4 * g] = v4.x;
+          rnv[4 * g + 1] = v4.y;
+          rnv[4 * g + 2] = v4.z;
+          rnv[4 * g + 3] = v4.w;
+        }
+      }
+      // rows past n (the last block only) never pass
+      const uint32_t valid_rows = (gb * 32 + 32 <= a.n) ? 0xFFFFFFFFu
+                                                         : (uint32_t)((1ull << (a.n - gb * 32)) - 1);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        uint32_t pass = 0;
+        float vv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          bool p;
+          if constexpr (MET == kScrDot) {
+            vv[r] = acc[t][r];
+            p = acc[t][r] >= thr[t];
+          } else if constexpr (MET == kScrCos) {
+            vv[r] = __builtin_fmaf(acc[t][r], fac[t], 1.0f);
+            p = vv[r] <= thr[t];
+          } else {
+            vv[r] = __builtin_fmaf(acc[t][r], fac[t], qnv[t] + rnv[r]);
+            p = vv[r] <= thr[t];
+          }
+          pass |= (p ? 1u : 0u) << r;
+        }
+        // row of value r: 8(r/4) + 4h + r%4 within the block
+        uint32_t rows_ok = 0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) rows_ok |= ((valid_rows >> (8 * (r >> 2) + 4 * h + (r & 3))) & 1u) << r;
+        pass &= rows_ok;
+        if (__ballot(pass != 0) == 0) continue;
+        if (pass) {
+          const uint64_t q = qidx[t];
+          const uint32_t np = (uint32_t)__popc(pass);
+          const uint32_t base = atomicAdd(&a.count[q], np);
+          uint32_t i = base;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            if ((pass >> r) & 1u) {
+              if (i < kCap) {
+                const float v = (MET == kScrDot) ? vv[r] * fac[t] : vv[r];
+                const uint32_t row = (uint32_t)(rbase + 8 * (r >> 2) + (r & 3));
+                a.buf[q * kCap + i] = make_uint2(__float_as_uint(v), row);
+              }
+              ++i;
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---- per-stage selection --------------------------------------------------------
+
+// One wave per query.  Middle stage: tau = the m-th smallest value of the
+// buffer (kept when fewer arrived; entries past the capacity were dropped,
+// and the m-th of the rest still has m rows at or below it).  Last stage:
+// the kp smallest (value, row) pairs as candidates, abound = the kp-th value
+// (every row outside screens at or above it) or tau when fewer arrived; an
+// overflowing or forced query gets cand count kForceExact.  Resets count.
+template <int R>
+__global__ __launch_bounds__(64) void select16_kernel(uint32_t* __restrict__ count, const uint2* __restrict__ buf,
+                                                      float* __restrict__ tau, int m, int final_stage, int kp,
+                                                      const int* __restrict__ force, float* __restrict__ cand_d,
+                                                      uint64_t* __restrict__ cand_k, uint32_t* __restrict__ cand_c,
+                                                      float* __restrict__ abound) {
+  const uint64_t q = blockIdx.x;
+  const int lane = threadIdx.x;
+  const uint32_t c = count[q];
+  const uint32_t ce = std::min(c, kCap);
+  WaveTopK<R> tk;
+  tk.init(final_stage ? kp : m);
+  for (uint32_t i0 = 0; i0 < ce; i0 += 64) {
+    const uint32_t i = i0 + (uint32_t)lane;
+    const bool in = i < ce;
+    const uint2 e = in ? buf[q * kCap + i] : make_uint2(0u, 0u);
+    tk.offer(in ? __uint_as_float(e.x) : f_inf(), in ? e.y : kNoPos);
+  }
+  const float t_old = tau[q];
+  if (!final_stage) {
+    if (ce >= (uint32_t)m && lane == 0) tau[q] = tk.tau;
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int s = r * 64 + lane;
+      if (s < kp) {
+        cand_d[q * kp + s] = tk.d[r];
+        cand_k[q * kp + s] = tk.p[r] == kNoPos ? ~0ull : (uint64_t)tk.p[r];
+      }
+    }
+    if (lane == 0) {
+      const bool forced = force[q] != 0 || c > kCap;
+      cand_c[q] = forced ? kForceExact : std::min<uint32_t>(ce, (uint32_t)kp);
+      abound[q] = ce >= (uint32_t)kp ? tk.tau : t_old;
+    }
+  }
+  if (lane == 0) count[q] = 0;
+}
+
+template <int MET, int KB>
+void* pick16_t() {
+  if constexpr (KB <= 8) return (void*)screen16_kernel<MET, KB, 2>;
+  else return (void*)screen16_kernel<MET, KB, 1>;
+}
+
+template <int MET>
+void* pick16(int kb) {
+  switch (kb) {
+    case 4: return pick16_t<MET, 4>();
+    case 6: return pick16_t<MET, 6>();
+    case 8: return pick16_t<MET, 8>();
+    case 12: return pick16_t<MET, 12>();
+    case 16: return pick16_t<MET, 16>();
+    case 24: return pick16_t<MET, 24>();
+    case 32: return pick16_t<MET, 32>();
+  }
+  return nullptr;
+}
+
+int tiles_per_wave(int kb) { return kb <= 8 ? 2 : 1; }
+
+unsigned cdiv(uint64_t a, uint64_t b) { return (unsigned)((a + b - 1) / b); }
+
+__global__ void zero_counter(uint32_t* p) { *p = 0; }
+
+}  // namespace
+
+// k-steps of 16 dimensions: the next supported count at or above dim/16.
+int h16_ksteps(int dim) {
+  const int need = (dim + 15) / 16;
+  for (int kb : {4, 6, 8, 12, 16, 24, 32})
+    if (need <= kb) return kb;
+  return 0;
+}
+
+void H16Rows::build(const float* rows, const float* row_norm, uint64_t n, int dim, int metric,
+                    hipStream_t s) {
+  ok = false;
+  n_ = n;
+  dim_ = dim;
+  kb = h16_ksteps(dim);
+  if (n == 0 || kb == 0 || dim % 4 != 0) return;
+  if (metric == FDB_METRIC_MANHATTAN) return;
+  const int cosine = metric == FDB_METRIC_COSINE ? 1 : 0;
+  stats_.reserve(3);
+  hipLaunchKernelGGL(init_stats, dim3(1), dim3(1), 0, s, stats_.p);
+  FDB_HIP(hipGetLastError());
+  hipLaunchKernelGGL(rows_absmax_kernel, dim3(cdiv(n, 4)), dim3(256), 0, s, rows, n, dim, row_norm, cosine,
+                     stats_.p);
+  FDB_HIP(hipGetLastError());
+  uint32_t st[3];
+  FDB_HIP(hipMemcpyAsync(st, stats_.p, sizeof(st), hipMemcpyDeviceToHost, s));
+  FDB_HIP(hipStreamSynchronize(s));
+  float maxabs;
+  std::memcpy(&maxabs, &st[0], 4);
+  std::memcpy(&rnmin, &st[2], 4);
+  // zero, denormal or non-finite norms (cosine), non-finite values
+  if (st[1] != 0 || !std::isfinite(maxabs)) return;
+  int e = 0;
+  if (maxabs > 0.0f) {
+    int ee;
+    (void)std::frexp(maxabs, &ee);
+    e = 14 - ee;
+  }
+  if (e > 100 || e < -100) return;
+  xexp = e;
+  nblk = (n + 31) / 32;
+  const uint64_t units = nblk * (uint64_t)kb * 64;
+  x16_.reserve(units * 8);
+  hipLaunchKernelGGL(rows_to_h16_kernel, dim3(cdiv(units, 256)), dim3(256), 0, s, rows, n, dim, kb, row_norm,
+                     cosine, e, reinterpret_cast<v8h*>(x16_.p), units);
+  FDB_HIP(hipGetLastError());
+  if (metric == FDB_METRIC_EUCLIDEAN || metric == FDB_METRIC_EUCLIDEAN_SQUARED) {
+    rn16_.reserve(nblk * 32);
+    hipLaunchKernelGGL(pad_norms_kernel, dim3(cdiv(nblk * 32, 256)), dim3(256), 0, s, row_norm, n, nblk * 32,
+                       rn16_.p);
+    FDB_HIP(hipGetLastError());
+  }
+  ok = true;
+}
+
+bool FlatSearcher::screenable16(const H16Rows& h, int metric, uint32_t k) {
+  return h.ok && screenable(metric, h.dim_, k) && metric != FDB_METRIC_MANHATTAN;
+}
+
+void FlatSearcher::screen16(const FlatRows& x, const H16Rows& h, int metric, const float* d_qs,
+                            const float* q_norm, uint64_t nq, uint32_t k, uint64_t* d_ids, float* d_dists,
+                            uint32_t* d_counts, hipStream_t s) {
+  if (!screenable16(h, metric, k)) throw Error(FDB_ERR_UNSUPPORTED, "fp16 screening does not apply");
+  const int kp = (k + 16 <= 64) ? 64 : 128;
+  const int kb = h.kb;
+  const int T = tiles_per_wave(kb);
+  const int met = metric == FDB_METRIC_DOT_PRODUCT ? kScrDot : (metric == FDB_METRIC_COSINE ? kScrCos : kScrL2);
+  void* fn = met == kScrDot ? pick16<kScrDot>(kb) : (met == kScrCos ? pick16<kScrCos>(kb) : pick16<kScrL2>(kb));
+  if (!fn) throw Error(FDB_ERR_UNSUPPORTED, "no fp16 screening kernel for this dimension");
+  const int sb = std::max(1, kStageKiB / kb);
+
+  // the ladder of block counts, last = all blocks
+  std::vector<uint64_t> ladder{h.nblk};
+  while (ladder.front() > 32) ladder.insert(ladder.begin(), (ladder.front() + 31) / 32);
+
+  const uint64_t slice = std::min<uint64_t>(kSlice, nq);
+  const uint64_t qtiles_max = (slice + 31) / 32;
+  q16_.reserve((qtiles_max + 4 * (uint64_t)T) * (uint64_t)kb * 64 * 8);
+  qexp_.reserve(slice);
+  tau_.reserve(slice);
+  count_.reserve(slice);
+  force_.reserve(slice);
+  buf_.reserve(slice * kCap);
+  cand_d_.reserve(slice * kp);
+  cand_k_.reserve(slice * kp);
+  cand_c_.reserve(slice);
+  abound_.reserve(slice);
+  flags_.reserve(nq);
+  fallbacks_.reserve(1);
+  hipLaunchKernelGGL(zero_counter, dim3(1), dim3(1), 0, s, fallbacks_.p);
+  FDB_HIP(hipGetLastError());
+
+  for (uint64_t q0 = 0; q0 < nq; q0 += slice) {
+    const uint64_t m = std::min(slice, nq - q0);
+    const uint64_t qtiles = (m + 31) / 32;
+    // tiles past the last one that a workgroup reads are zero queries
+    const uint64_t groups = (qtiles + 4 * T - 1) / (4 * T);
+    const uint64_t slots = groups * 4 * T * 32;
+    hipLaunchKernelGGL(queries_to_h16_kernel, dim3((unsigned)slots), dim3(64), 0, s, d_qs + q0 * h.dim_, m,
+                       h.dim_, kb, q_norm + q0, met == kScrCos ? 1 : 0, h.rnmin, x.rnmax, h.xexp,
+                       reinterpret_cast<v8h*>(q16_.p), qexp_.p, tau_.p, count_.p, force_.p);
+    FDB_HIP(hipGetLastError());
+    for (size_t st = 0; st < ladder.size(); ++st) {
+      const bool last = st + 1 == ladder.size();
+      const uint64_t nsel = ladder[st];
+      Screen16Args a{};
+      a.x16 = reinterpret_cast<const v8h*>(h.x16());
+      a.n = h.n_;
+      a.nblk = h.nblk;
+      a.rn16 = h.rn16();
+      a.q16 = reinterpret_cast<const v8h*>(q16_.p);
+      a.nq = m;
+      a.qn = q_norm + q0;
+      a.qexp = qexp_.p;
+      a.xexp = h.xexp;
+      a.tau = tau_.p;
+      a.count = count_.p;
+      a.buf = buf_.p;
+      a.bstride = last ? 1 : h.nblk / nsel;
+      a.nsel = nsel;
+      // chunks: about 2048 workgroups, whole stages each
+      const uint64_t want = std::max<uint64_t>(1, 2048 / groups);
+      uint64_t cb = (nsel + want - 1) / want;
+      cb = std::max<uint64_t>(sb, (cb + sb - 1) / sb * sb);
+      a.chunk_blocks = cb;
+      const unsigned nchunks = cdiv(nsel, cb);
+      void* args[] = {(void*)&a};
+      FDB_HIP(hipLaunchKernel(fn, dim3((unsigned)groups, nchunks), dim3(kT16), args, 0, s));
+      if (!last) {
+        // rank for the next threshold: about 1024 rows of the next stage pass it
+        const uint64_t ratio = std::max<uint64_t>(1, ladder[st + 1] / nsel);
+        const int rank = (int)std::clamp<uint64_t>(1024 / ratio, 32, 64);
+        hipLaunchKernelGGL(select16_kernel<1>, dim3((unsigned)m), dim3(64), 0, s, count_.p, buf_.p, tau_.p, rank,
+                           0, kp, force_.p, cand_d_.p, cand_k_.p, cand_c_.p, abound_.p);
+      } else if (kp == 64) {
+        hipLaunchKernelGGL(select16_kernel<1>, dim3((unsigned)m), dim3(64), 0, s, count_.p, buf_.p, tau_.p, 0, 1,
+                           kp, force_.p, cand_d_.p, cand_k_.p, cand_c_.p, abound_.p);
+      } else {
+        hipLaunchKernelGGL(select16_kernel<2>, dim3((unsigned)m), dim3(64), 0, s, count_.p, buf_.p, tau_.p, 0, 1,
+                           kp, force_.p, cand_d_.p, cand_k_.p, cand_c_.p, abound_.p);
+      }
+      FDB_HIP(hipGetLastError());
+    }
+    RescoreArgs r{};
+    r.queries = d_qs + q0 * x.dim;
+    r.dim = x.dim;
+    r.rows = x.rows;
+    r.row_norm = x.row_norm;
+    r.q_norm = q_norm + q0;
+    r.rnmax = x.rnmax;
+    r.cand_keys = cand_k_.p;
+    r.cand_d = cand_d_.p;
+    r.cand_counts = cand_c_.p;
+    r.kp = kp;
+    r.metric = metric;
+    r.k = (int)k;
+    r.ids = x.ids;
+    r.out_ids = d_ids + q0 * k;
+    r.out_d = d_dists + q0 * k;
+    r.out_counts = d_counts + q0;
+    r.flags = flags_.p + q0;
+    r.fallbacks = fallbacks_.p;
+    r.abound = abound_.p;
+    r.h16 = 1;
+    r.n = x.n;
+    FDB_HIP(launch_rescore(r, m, s));
+  }
+  exact(x, metric, d_qs, q_norm, nq, k, d_ids, d_dists, d_counts, s, flags_.p);
+}
+
+}  // namespace fdb

@@ -48,7 +48,7 @@ EXPORTED_SYMBOLS = (
     "fdb_bf_create", "fdb_bf_add", "fdb_bf_remove", "fdb_bf_len", "fdb_bf_dimension",
     "fdb_bf_metric", "fdb_bf_load", "fdb_bf_save", "fdb_bf_destroy", "fdb_bf_export",
     "fdb_bf_search", "fdb_bf_batch_search", "fdb_bf_batch_search_device",
-    "fdb_bf_set_search_mode", "fdb_bf_last_fallbacks",
+    "fdb_bf_set_search_mode", "fdb_bf_last_fallbacks", "fdb_bf_last_search_path",
     "fdb_ivf_create", "fdb_ivf_build", "fdb_ivf_destroy", "fdb_ivf_set_nprobe", "fdb_ivf_nprobe",
     "fdb_ivf_len", "fdb_ivf_num_partitions", "fdb_ivf_dimension", "fdb_ivf_export",
     "fdb_ivf_search", "fdb_ivf_batch_search", "fdb_ivf_batch_search_device", "fdb_ivf_sync",
@@ -56,7 +56,7 @@ EXPORTED_SYMBOLS = (
 )
 
 LUT_EXACT, LUT_FAST = 0, 1
-BF_AUTO, BF_EXACT, BF_SCREEN = 0, 1, 2
+BF_AUTO, BF_EXACT, BF_SCREEN, BF_SCREEN_F32 = 0, 1, 2, 3
 COARSE_AUTO, COARSE_EXACT, COARSE_SCREEN = 0, 1, 2
 
 
@@ -145,6 +145,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fdb_bf_batch_search_device": [_P, _P, C.c_uint64, C.c_uint32, _P, _P, _P, _P, _P],
         "fdb_bf_set_search_mode": [_P, C.c_uint32],
         "fdb_bf_last_fallbacks": [_P, _P, _P],
+        "fdb_bf_last_search_path": [_P, _P],
         "fdb_ivf_create": [_P, C.c_uint32, C.c_uint32, _P, _P, _P, C.c_uint32, _P],
         "fdb_ivf_build": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint64, _P],
         "fdb_ivf_export": [_P, _P, _P, _P, _P],
@@ -502,9 +503,18 @@ class BruteForceIndex:
         _check(self._lib, self._lib.fdb_bf_add(self._h, _ptr(r), _ptr(idv), r.shape[0], r.shape[1]))
 
     def set_search_mode(self, mode: int) -> None:
-        """BF_AUTO (default), BF_EXACT (exact-order scan only) or BF_SCREEN
-        (MFMA screening + exact rescoring where it applies); same results."""
+        """BF_AUTO (default), BF_EXACT (exact-order scan only), BF_SCREEN
+        (matrix-core screening + exact rescoring where it applies; fp16
+        products when the rows fit) or BF_SCREEN_F32 (screening with fp32
+        products); same results."""
         _check(self._lib, self._lib.fdb_bf_set_search_mode(self._h, int(mode)))
+
+    def last_search_path(self) -> int:
+        """How the last search ran: 0 exact scan, 1 fp32 screening, 2 fp16
+        screening."""
+        out = C.c_uint32()
+        _check(self._lib, self._lib.fdb_bf_last_search_path(self._h, C.byref(out)))
+        return int(out.value)
 
     def last_fallbacks(self, stream: int = 0) -> int:
         """Queries of the last search that were rescanned exactly."""

@@ -270,17 +270,22 @@ FDB_API fdb_status fdb_bf_batch_search_device(fdb_bf* index, const float* d_quer
  * loop):
  *   FDB_BF_AUTO (default) and FDB_BF_SCREEN: for dot product, cosine and
  *     (squared) Euclidean with dim a multiple of 4 (<= 512) and k <= 112,
- *     an MFMA fp32 pass screens K' = 64 or 128 candidates per query, their
+ *     a matrix-core pass screens K' = 64 or 128 candidates per query, their
  *     distances are recomputed exactly in the reference's order, and a
  *     rounding-error bound proves that no other row can enter the top k;
  *     queries where it cannot be proved are rescanned exactly.  Results are
- *     identical to FDB_BF_EXACT.
+ *     identical to FDB_BF_EXACT.  The pass uses fp16 products when the rows
+ *     fit (finite, no zero-norm rows for cosine), else fp32 products.
  *   FDB_BF_EXACT: the exact-order VALU scan for every query.
+ *   FDB_BF_SCREEN_F32: screening with the fp32 products only.
  * fdb_bf_last_fallbacks reports how many queries of the last search were
  * rescanned (it waits for hip_stream; NULL = the handle's own stream). */
-enum { FDB_BF_AUTO = 0, FDB_BF_EXACT = 1, FDB_BF_SCREEN = 2 };
+enum { FDB_BF_AUTO = 0, FDB_BF_EXACT = 1, FDB_BF_SCREEN = 2, FDB_BF_SCREEN_F32 = 3 };
 FDB_API fdb_status fdb_bf_set_search_mode(fdb_bf* index, uint32_t mode);
 FDB_API fdb_status fdb_bf_last_fallbacks(fdb_bf* index, void* hip_stream, uint64_t* out);
+/* How the last search ran (diagnostics; no counterpart in the reference):
+ * 0 exact scan, 1 fp32 screening, 2 fp16 screening. */
+FDB_API fdb_status fdb_bf_last_search_path(fdb_bf* index, uint32_t* out);
 
 /* ------------------------------------------------------------------------ */
 /* IVF (full vectors): src/index/ivf.rs                                     */

@@ -16,8 +16,8 @@ import pytest
 
 import refcpu
 
-from forgedb import (BF_EXACT, BF_SCREEN, COARSE_SCREEN, BruteForceIndex, DistanceMetric, ForgeDbError,
-                     IVFIndex, datagen)
+from forgedb import (BF_EXACT, BF_SCREEN, BF_SCREEN_F32, COARSE_SCREEN, BruteForceIndex, DistanceMetric,
+                     ForgeDbError, IVFIndex, datagen)
 
 pytestmark = pytest.mark.gpu
 
@@ -34,8 +34,8 @@ def check_rows(gi, gd, gc, oi, od, oc, label):
         assert np.all(gi[q, c:] == NO_ID) and np.all(np.isinf(gd[q, c:]))
 
 
-MODES = [BF_EXACT, BF_SCREEN]
-MODE_IDS = ["exact", "screen"]
+MODES = [BF_EXACT, BF_SCREEN, BF_SCREEN_F32]
+MODE_IDS = ["exact", "screen", "screen_f32"]
 
 
 def bf_pair(rows, ids, metric, queries, k, mode=BF_EXACT, index=None):
@@ -71,10 +71,11 @@ def test_bf_normalised_parity(metric, mode):
     g = BruteForceIndex.from_arrays(base, ids, metric)
     (gi, gd, gc), (oi, od, oc) = bf_pair(base, ids, metric, queries, 100, mode, index=g)
     check_rows(gi, gd, gc, oi, od, oc, metric.name)
-    if mode == BF_SCREEN:
+    if mode != BF_EXACT:
         fb = g.last_fallbacks()
         print(f"  screening fallbacks: {fb} of 200", flush=True)
         assert fb < 20  # the screen decides nearly every query by itself
+        assert g.last_search_path() == (2 if mode == BF_SCREEN else 1)
 
 
 def test_bf_screen_fallback_on_near_ties():
@@ -94,9 +95,10 @@ def test_bf_screen_fallback_on_near_ties():
         rows[rng.choice(4000, 300, replace=False)] = near
         queries = np.stack([q, rows[5]])
         g = BruteForceIndex.from_arrays(rows, ids, metric)
-        (gi, gd, gc), (oi, od, oc) = bf_pair(rows, ids, metric, queries, 20, BF_SCREEN, index=g)
-        check_rows(gi, gd, gc, oi, od, oc, f"near ties {metric.name}")
-        assert g.last_fallbacks() >= 1, metric.name
+        for mode in (BF_SCREEN, BF_SCREEN_F32):
+            (gi, gd, gc), (oi, od, oc) = bf_pair(rows, ids, metric, queries, 20, mode, index=g)
+            check_rows(gi, gd, gc, oi, od, oc, f"near ties {metric.name} mode {mode}")
+            assert g.last_fallbacks() >= 1, (metric.name, mode)
 
 
 @pytest.mark.parametrize("dim,n,nq,k", [(1, 300, 5, 4), (7, 1000, 17, 64), (8, 513, 3, 65),
@@ -114,6 +116,75 @@ def test_bf_shapes(dim, n, nq, k):
         for mode in MODES:
             (gi, gd, gc), (oi, od, oc) = bf_pair(rows, ids, metric, queries, k, mode, index=g)
             check_rows(gi, gd, gc, oi, od, oc, f"dim{dim} {metric.name} mode {mode}")
+
+
+@pytest.mark.parametrize("n,dim,nq,k", [(100, 32, 40, 10), (1025, 64, 70, 48), (40_000, 32, 300, 100),
+                                        (3000, 96, 8200, 1), (2047, 200, 33, 112)])
+def test_bf_fp16_screen_sizes(n, dim, nq, k):
+    """Row counts for one, two and three threshold stages, a query batch
+    over two passes, the largest k, a dimension padded to whole k-steps."""
+    print(f"bf fp16 screening n={n} dim={dim} nq={nq} k={k}", flush=True)
+    rng = np.random.default_rng(n + dim)
+    rows = rng.standard_normal((n, dim)).astype(np.float32)
+    queries = rng.standard_normal((nq, dim)).astype(np.float32)
+    ids = rng.permutation(n).astype(np.uint64)
+    for metric in (DistanceMetric.Cosine, DistanceMetric.DotProduct, DistanceMetric.Euclidean,
+                   DistanceMetric.EuclideanSquared):
+        g = BruteForceIndex.from_arrays(rows, ids, metric)
+        (gi, gd, gc), (oi, od, oc) = bf_pair(rows, ids, metric, queries, k, BF_SCREEN, index=g)
+        check_rows(gi, gd, gc, oi, od, oc, f"fp16 n{n} {metric.name}")
+        assert g.last_search_path() == 2, metric.name
+        assert g.last_fallbacks() <= max(2, nq // 20), metric.name
+
+
+def test_bf_fp16_screen_edges():
+    """Rows or queries that fp16 cannot carry: the search still matches the
+    oracle, through the fp32 screen (rows) or the exact rescan (queries)."""
+    print("bf fp16 screening edge cases", flush=True)
+    rng = np.random.default_rng(5)
+    n, dim = 3000, 64
+    base = rng.standard_normal((n, dim)).astype(np.float32)
+    ids = np.arange(n, dtype=np.uint64)
+    queries = rng.standard_normal((40, dim)).astype(np.float32)
+
+    def run(rows, qs, metric, k=10):
+        g = BruteForceIndex.from_arrays(rows, ids, metric)
+        (gi, gd, gc), (oi, od, oc) = bf_pair(rows, ids, metric, qs, k, BF_SCREEN, index=g)
+        check_rows(gi, gd, gc, oi, od, oc, f"edge {metric.name}")
+        return g
+
+    # a zero row: cosine distance 0 to every query (the reference's zero
+    # denominator), so fp16 screening is off for the index
+    rows = base.copy()
+    rows[17] = 0.0
+    assert run(rows, queries, DistanceMetric.Cosine).last_search_path() == 1
+    # a zero query under cosine: rescanned exactly, the others screened
+    qs = queries.copy()
+    qs[3] = 0.0
+    g = run(base, qs, DistanceMetric.Cosine)
+    assert g.last_search_path() == 2 and g.last_fallbacks() >= 1
+    # components beyond the fp16 range are scaled into it (rows as a whole,
+    # each query on its own)
+    rows = base.copy()
+    rows[100, 5] = 1e6
+    assert run(rows, queries, DistanceMetric.DotProduct).last_search_path() == 2
+    qs = queries.copy()
+    qs[7, 0] = 3e5
+    assert run(base, qs, DistanceMetric.DotProduct).last_search_path() == 2
+    # a row scale the power-of-two scaling does not cover: fp32 screening
+    rows = base.copy()
+    rows[100, 5] = 1e35
+    assert run(rows, queries, DistanceMetric.DotProduct).last_search_path() == 1
+    # small and large scales are carried by the power-of-two scaling
+    for scale in (1e-6, 1e3):
+        for metric in (DistanceMetric.EuclideanSquared, DistanceMetric.DotProduct, DistanceMetric.Cosine):
+            g = run(base * np.float32(scale), queries * np.float32(scale), metric)
+            assert g.last_search_path() == 2, (scale, metric.name)
+            assert g.last_fallbacks() <= 2, (scale, metric.name)
+    # near the float underflow the bound's floor sends queries to the exact
+    # scan, and cosine rows with denormal norms keep the index off fp16
+    for metric in (DistanceMetric.EuclideanSquared, DistanceMetric.DotProduct, DistanceMetric.Cosine):
+        run(base * np.float32(1e-20), queries * np.float32(1e-20), metric)
 
 
 def test_bf_ties_keep_the_earlier_row():
