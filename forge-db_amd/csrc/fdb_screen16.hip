@@ -29,10 +29,11 @@ namespace {
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int kT16 = 256;        // threads per screening workgroup (4 waves)
-constexpr int kStageKiB = 32;    // LDS per workgroup: one stage of row blocks
-constexpr uint32_t kCap = 4096;  // buffer entries per query
-constexpr uint64_t kSlice = 8192;  // queries per pass (buffers: 256 MB)
+constexpr int kT16 = 256;          // threads per screening workgroup (4 waves)
+constexpr int kStageKiB = 32;      // LDS per workgroup: one stage of row blocks
+constexpr uint32_t kSub = 64;      // entries of one append buffer
+constexpr uint64_t kSlice = 8192;  // queries per pass
+constexpr uint64_t kSubBudget = 1ull << 25;  // append entries per pass (256 MB)
 
 // Exponent e with maxabs * 2^e in [2^13, 2^14); 0 for 0 or non-finite.
 __device__ __forceinline__ int scale_exp(float maxabs) {
@@ -56,28 +57,47 @@ __global__ void init_stats(uint32_t* s) {
 // every finite value); cosine only: stats[1] rows whose squared norm is not
 // a finite normal float (zero rows included), stats[2] bits of the smallest
 // squared norm.
+// Grid-stride over rows, one wave per row at a time; one set of atomics per
+// workgroup.
 __global__ __launch_bounds__(256) void rows_absmax_kernel(const float* __restrict__ rows, uint64_t n, int dim,
                                                           const float* __restrict__ rn, int cosine,
                                                           uint32_t* __restrict__ stats) {
-  const uint64_t r = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  __shared__ uint32_t red[3][4];
   const int lane = threadIdx.x & 63;
-  if (r >= n) return;
-  float scale = 1.0f;
-  if (cosine) {
-    const float nr = rn[r];
-    const float inv = 1.0f / __builtin_sqrtf(nr);
-    if (!(nr >= 1.17549435e-38f) || !(nr <= 3.40282347e38f) || !(inv < __builtin_huge_valf())) {
-      if (lane == 0) atomicAdd(&stats[1], 1u);
-      return;
+  const int wave = threadIdx.x >> 6;
+  uint32_t m = 0, bad = 0, mn = 0x7F7FFFFFu;
+  for (uint64_t r = (uint64_t)blockIdx.x * 4 + wave; r < n; r += (uint64_t)gridDim.x * 4) {
+    float scale = 1.0f;
+    if (cosine) {
+      const float nr = rn[r];
+      const float inv = 1.0f / __builtin_sqrtf(nr);
+      if (!(nr >= 1.17549435e-38f) || !(nr <= 3.40282347e38f) || !(inv < __builtin_huge_valf())) {
+        ++bad;
+        continue;
+      }
+      mn = std::min(mn, __float_as_uint(nr));
+      scale = inv;
     }
-    if (lane == 0) atomicMin(&stats[2], __float_as_uint(nr));
-    scale = inv;
+    for (int d = lane; d < dim; d += 64) m = std::max(m, f2u_abs(rows[r * dim + d] * scale));
   }
-  uint32_t m = 0;
-  for (int d = lane; d < dim; d += 64) m = std::max(m, f2u_abs(rows[r * dim + d] * scale));
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) m = std::max(m, (uint32_t)__shfl_xor((int)m, off));
-  if (lane == 0) atomicMax(&stats[0], m);
+  if (lane == 0) {
+    red[0][wave] = m;
+    red[1][wave] = bad;
+    red[2][wave] = mn;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w) {
+      red[0][0] = std::max(red[0][0], red[0][w]);
+      red[1][0] += red[1][w];
+      red[2][0] = std::min(red[2][0], red[2][w]);
+    }
+    atomicMax(&stats[0], red[0][0]);
+    if (red[1][0]) atomicAdd(&stats[1], red[1][0]);
+    atomicMin(&stats[2], red[2][0]);
+  }
 }
 
 // Blocked fp16 rows: block b (rows 32b..32b+31), k-step kb, lane l holds the
@@ -116,15 +136,14 @@ __global__ void pad_norms_kernel(const float* __restrict__ rn, uint64_t n, uint6
 // One wave per query slot of the padded tiles: blocked fp16 operand (the B
 // operand: lane l holds query 32t + l%32, dims 16kb + 8(l/32) + 0..7), its
 // exponent, tau = +inf (-inf and forced for a query the fp16 path cannot
-// take), count = 0.  Cosine: the reference divides by sqrt(qn * rn), which
+// take).  Cosine: the reference divides by sqrt(qn * rn), which
 // must stay clear of underflow and overflow for every row (rn in [rnmin,
 // rnmax]) for the normalised product to stand for it.
 __global__ __launch_bounds__(64) void queries_to_h16_kernel(const float* __restrict__ qs, uint64_t nq, int dim,
                                                             int kb, const float* __restrict__ qn, int cosine,
                                                             float rnmin, float rnmax, int ex,
                                                             v8h* __restrict__ q16, int* __restrict__ qexp,
-                                                            float* __restrict__ tau, uint32_t* __restrict__ count,
-                                                            int* __restrict__ force) {
+                                                            float* __restrict__ tau, int* __restrict__ force) {
   const uint64_t q = blockIdx.x;
   const int lane = threadIdx.x;
   const bool real = q < nq;
@@ -156,7 +175,6 @@ __global__ __launch_bounds__(64) void queries_to_h16_kernel(const float* __restr
   if (lane == 0 && real) {
     qexp[q] = e;
     tau[q] = bad ? -__builtin_huge_valf() : __builtin_huge_valf();
-    count[q] = 0;
     force[q] = bad ? 1 : 0;
   }
 }
@@ -173,8 +191,12 @@ struct Screen16Args {
   const int* qexp;    // [nq]
   int xexp;
   const float* tau;   // [nq]
-  uint32_t* count;    // [nq]
-  uint2* buf;         // [nq][kCap] (screening value bits, row)
+  // append buffers, one per (query, chunk, half wave): sb = (q*nchunks +
+  // chunk)*2 + half holds scnt[sb] entries (the first kSub of them stored)
+  // at sbuf[sb*kSub ..]: (screening value bits, row)
+  uint32_t* scnt;
+  uint2* sbuf;
+  uint32_t nchunks;
   uint64_t bstride, nsel, chunk_blocks;
 };
 
@@ -186,7 +208,9 @@ enum { kScrDot = 0, kScrCos = 1, kScrL2 = 2 };
 // block and tile a lane holds 16 products of its query (32t + lane%32) with
 // rows 8(r/4) + 4(lane/32) + r%4 and tests them against its threshold.
 template <int MET, int KB, int T>
-__global__ __launch_bounds__(kT16) void screen16_kernel(Screen16Args a) {
+// Dot and cosine up to 256 dimensions fit three waves per SIMD (168 VGPRs).
+__global__ __launch_bounds__(kT16)
+__attribute__((amdgpu_waves_per_eu((MET != kScrL2 && KB <= 16) ? 3 : 1, 8))) void screen16_kernel(Screen16Args a) {
   constexpr int SB = (kStageKiB / KB) > 0 ? kStageKiB / KB : 1;
   __shared__ v8h stage[SB * KB * 64];
   const int tid = threadIdx.x;
@@ -197,12 +221,15 @@ __global__ __launch_bounds__(kT16) void screen16_kernel(Screen16Args a) {
 
   v8h bq[T][KB];
   float thr[T], fac[T], qnv[T];
-  uint64_t qidx[T];
+  uint64_t qidx[T], sbase[T];
+  uint32_t cnt[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
     const uint64_t tile = tile0 + t;
     const uint64_t q = tile * 32 + (uint64_t)(lane & 31);
     qidx[t] = q;
+    sbase[t] = ((q * a.nchunks + blockIdx.y) * 2 + (uint64_t)h) * kSub;
+    cnt[t] = 0;
     const bool real = q < a.nq;
 #pragma unroll
     for (int ks = 0; ks < KB; ++ks) bq[t][ks] = a.q16[(tile * KB + ks) * 64 + lane];
@@ -222,16 +249,33 @@ __global__ __launch_bounds__(kT16) void screen16_kernel(Screen16Args a) {
   }
 
   const uint64_t j0 = (uint64_t)blockIdx.y * a.chunk_blocks;
-  const uint64_t j1 = std::min<uint64_t>(a.nsel, j0 + a.chunk_blocks);
+  const uint64_t j1 = std::min<uint64_t>(a.nsel, j0 + a.chunk_blocks);  // > j0: no empty chunks
   constexpr int kUnits = SB * KB * 64;
+  constexpr int kPer = (kUnits + kT16 - 1) / kT16;
+  // The next stage's loads are issued before the current stage is computed.
+  // Blocks past the chunk's end re-read its last block (never computed).
+  v8h pre[kPer];
+  auto fetch = [&](uint64_t js) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int u = tid + i * kT16;
+      if (kUnits % kT16 == 0 || u < kUnits) {
+        const int bs = u / (KB * 64);
+        const uint64_t j = std::min<uint64_t>(js + (uint64_t)bs, j1 - 1);
+        pre[i] = a.x16[(j * a.bstride * KB) * 64 + (uint64_t)(u - bs * KB * 64)];
+      }
+    }
+  };
+  fetch(j0);
   for (uint64_t js = j0; js < j1; js += SB) {
     __syncthreads();  // the previous stage is consumed
-    for (int u = tid; u < kUnits; u += kT16) {
-      const int bs = u / (KB * 64);
-      const uint64_t j = js + (uint64_t)bs;
-      if (j < j1) stage[u] = a.x16[(j * a.bstride * KB) * 64 + (uint64_t)(u - bs * KB * 64)];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int u = tid + i * kT16;
+      if (kUnits % kT16 == 0 || u < kUnits) stage[u] = pre[i];
     }
     __syncthreads();
+    if (js + SB < j1) fetch(js + SB);
 #pragma unroll 1
     for (int bs = 0; bs < SB; ++bs) {
       const uint64_t j = js + (uint64_t)bs;
@@ -258,101 +302,106 @@ __global__ __launch_bounds__(kT16) void screen16_kernel(Screen16Args a) {
           rnv[4 * g + 3] = v4.w;
         }
       }
-      // rows past n (the last block only) never pass
-      const uint32_t valid_rows = (gb * 32 + 32 <= a.n) ? 0xFFFFFFFFu
-                                                         : (uint32_t)((1ull << (a.n - gb * 32)) - 1);
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        uint32_t pass = 0;
-        float vv[16];
+        // hot test: one compare (a ballot) per value; appends only for the
+        // values some lane passes (the screening value is recomputed there,
+        // not kept in registers)
+        auto value = [&](int r) {
+          if constexpr (MET == kScrDot) return acc[t][r];
+          else if constexpr (MET == kScrCos) return __builtin_fmaf(acc[t][r], fac[t], 1.0f);
+          else return __builtin_fmaf(acc[t][r], fac[t], qnv[t] + rnv[r]);
+        };
+        uint64_t mk[16];
+        uint64_t any = 0;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          bool p;
-          if constexpr (MET == kScrDot) {
-            vv[r] = acc[t][r];
-            p = acc[t][r] >= thr[t];
-          } else if constexpr (MET == kScrCos) {
-            vv[r] = __builtin_fmaf(acc[t][r], fac[t], 1.0f);
-            p = vv[r] <= thr[t];
-          } else {
-            vv[r] = __builtin_fmaf(acc[t][r], fac[t], qnv[t] + rnv[r]);
-            p = vv[r] <= thr[t];
-          }
-          pass |= (p ? 1u : 0u) << r;
+          const float v = value(r);
+          mk[r] = __ballot((MET == kScrDot) ? v >= thr[t] : v <= thr[t]);
+          any |= mk[r];
         }
-        // row of value r: 8(r/4) + 4h + r%4 within the block
-        uint32_t rows_ok = 0;
+        if (any == 0) continue;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) rows_ok |= ((valid_rows >> (8 * (r >> 2) + 4 * h + (r & 3))) & 1u) << r;
-        pass &= rows_ok;
-        if (__ballot(pass != 0) == 0) continue;
-        if (pass) {
-          const uint64_t q = qidx[t];
-          const uint32_t np = (uint32_t)__popc(pass);
-          const uint32_t base = atomicAdd(&a.count[q], np);
-          uint32_t i = base;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            if ((pass >> r) & 1u) {
-              if (i < kCap) {
-                const float v = (MET == kScrDot) ? vv[r] * fac[t] : vv[r];
-                const uint32_t row = (uint32_t)(rbase + 8 * (r >> 2) + (r & 3));
-                a.buf[q * kCap + i] = make_uint2(__float_as_uint(v), row);
-              }
-              ++i;
+        for (int r = 0; r < 16; ++r) {
+          if (mk[r] == 0) continue;
+          // row of value r: 8(r/4) + 4h + r%4 within the block; rows past n
+          // (the last block only) never pass
+          const uint32_t row = (uint32_t)(rbase + 8 * (r >> 2) + (r & 3));
+          if (((mk[r] >> lane) & 1u) && row < a.n) {
+            if (cnt[t] < kSub) {
+              const float v = (MET == kScrDot) ? value(r) * fac[t] : value(r);
+              a.sbuf[sbase[t] + cnt[t]] = make_uint2(__float_as_uint(v), row);
             }
+            ++cnt[t];
           }
         }
       }
     }
   }
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+    if (qidx[t] < a.nq) a.scnt[sbase[t] / kSub] = cnt[t];
 }
 
 // ---- per-stage selection --------------------------------------------------------
 
-// One wave per query.  Middle stage: tau = the m-th smallest value of the
-// buffer (kept when fewer arrived; entries past the capacity were dropped,
-// and the m-th of the rest still has m rows at or below it).  Last stage:
-// the kp smallest (value, row) pairs as candidates, abound = the kp-th value
-// (every row outside screens at or above it) or tau when fewer arrived; an
-// overflowing or forced query gets cand count kForceExact.  Resets count.
+// One wave per query over its nsub append buffers.  Middle stage: tau = the
+// m-th smallest value stored (kept when fewer arrived; a buffer that
+// overflowed dropped entries, and the m-th of the rest still has m rows at
+// or below it).  Last stage: the kp smallest (value, row) pairs as
+// candidates, abound = the kp-th value (every row outside screens at or above
+// it) or tau when fewer arrived; an overflowing or forced query gets cand
+// count kForceExact.
 template <int R>
-__global__ __launch_bounds__(64) void select16_kernel(uint32_t* __restrict__ count, const uint2* __restrict__ buf,
+__global__ __launch_bounds__(64) void select16_kernel(const uint32_t* __restrict__ scnt,
+                                                      const uint2* __restrict__ sbuf, uint32_t nsub,
                                                       float* __restrict__ tau, int m, int final_stage, int kp,
                                                       const int* __restrict__ force, float* __restrict__ cand_d,
                                                       uint64_t* __restrict__ cand_k, uint32_t* __restrict__ cand_c,
                                                       float* __restrict__ abound) {
   const uint64_t q = blockIdx.x;
   const int lane = threadIdx.x;
-  const uint32_t c = count[q];
-  const uint32_t ce = std::min(c, kCap);
   WaveTopK<R> tk;
   tk.init(final_stage ? kp : m);
-  for (uint32_t i0 = 0; i0 < ce; i0 += 64) {
-    const uint32_t i = i0 + (uint32_t)lane;
-    const bool in = i < ce;
-    const uint2 e = in ? buf[q * kCap + i] : make_uint2(0u, 0u);
-    tk.offer(in ? __uint_as_float(e.x) : f_inf(), in ? e.y : kNoPos);
+  uint32_t stored = 0;
+  bool over = false;
+  for (uint32_t s0 = 0; s0 < nsub; s0 += 64) {
+    const uint32_t s = s0 + (uint32_t)lane;
+    const uint32_t c = s < nsub ? scnt[q * nsub + s] : 0u;
+    over = over || __ballot(c > kSub) != 0;
+    const uint32_t ce = std::min(c, kSub);
+    uint32_t cmax = ce;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) cmax = std::max(cmax, (uint32_t)__shfl_xor((int)cmax, off));
+    const uint2* __restrict__ b = sbuf + (q * nsub + s) * kSub;
+    for (uint32_t i = 0; i < cmax; ++i) {
+      const bool in = i < ce;
+      const uint2 e = in ? b[i] : make_uint2(0u, 0u);
+      tk.offer(in ? __uint_as_float(e.x) : f_inf(), in ? e.y : kNoPos);
+    }
+    uint32_t sum = ce;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += (uint32_t)__shfl_xor((int)sum, off);
+    stored += sum;
   }
   const float t_old = tau[q];
   if (!final_stage) {
-    if (ce >= (uint32_t)m && lane == 0) tau[q] = tk.tau;
-  } else {
+    if (stored >= (uint32_t)m && lane == 0) tau[q] = tk.tau;
+    return;
+  }
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int s = r * 64 + lane;
-      if (s < kp) {
-        cand_d[q * kp + s] = tk.d[r];
-        cand_k[q * kp + s] = tk.p[r] == kNoPos ? ~0ull : (uint64_t)tk.p[r];
-      }
-    }
-    if (lane == 0) {
-      const bool forced = force[q] != 0 || c > kCap;
-      cand_c[q] = forced ? kForceExact : std::min<uint32_t>(ce, (uint32_t)kp);
-      abound[q] = ce >= (uint32_t)kp ? tk.tau : t_old;
+  for (int r = 0; r < R; ++r) {
+    const int s = r * 64 + lane;
+    if (s < kp) {
+      cand_d[q * kp + s] = tk.d[r];
+      cand_k[q * kp + s] = tk.p[r] == kNoPos ? ~0ull : (uint64_t)tk.p[r];
     }
   }
-  if (lane == 0) count[q] = 0;
+  if (lane == 0) {
+    const bool forced = force[q] != 0 || over;
+    cand_c[q] = forced ? kForceExact : std::min<uint32_t>(stored, (uint32_t)kp);
+    abound[q] = stored >= (uint32_t)kp ? tk.tau : t_old;
+  }
 }
 
 template <int MET, int KB>
@@ -403,8 +452,8 @@ void H16Rows::build(const float* rows, const float* row_norm, uint64_t n, int di
   stats_.reserve(3);
   hipLaunchKernelGGL(init_stats, dim3(1), dim3(1), 0, s, stats_.p);
   FDB_HIP(hipGetLastError());
-  hipLaunchKernelGGL(rows_absmax_kernel, dim3(cdiv(n, 4)), dim3(256), 0, s, rows, n, dim, row_norm, cosine,
-                     stats_.p);
+  hipLaunchKernelGGL(rows_absmax_kernel, dim3(std::min<unsigned>(2048, cdiv(n, 4))), dim3(256), 0, s, rows, n,
+                     dim, row_norm, cosine, stats_.p);
   FDB_HIP(hipGetLastError());
   uint32_t st[3];
   FDB_HIP(hipMemcpyAsync(st, stats_.p, sizeof(st), hipMemcpyDeviceToHost, s));
@@ -451,20 +500,42 @@ void FlatSearcher::screen16(const FlatRows& x, const H16Rows& h, int metric, con
   const int met = metric == FDB_METRIC_DOT_PRODUCT ? kScrDot : (metric == FDB_METRIC_COSINE ? kScrCos : kScrL2);
   void* fn = met == kScrDot ? pick16<kScrDot>(kb) : (met == kScrCos ? pick16<kScrCos>(kb) : pick16<kScrL2>(kb));
   if (!fn) throw Error(FDB_ERR_UNSUPPORTED, "no fp16 screening kernel for this dimension");
-  const int sb = std::max(1, kStageKiB / kb);
 
   // the ladder of block counts, last = all blocks
   std::vector<uint64_t> ladder{h.nblk};
   while (ladder.front() > 32) ladder.insert(ladder.begin(), (ladder.front() + 31) / 32);
 
-  const uint64_t slice = std::min<uint64_t>(kSlice, nq);
+  // balanced passes of at most kSlice queries
+  const uint64_t passes = (nq + kSlice - 1) / kSlice;
+  const uint64_t slice = (nq + passes - 1) / passes;
   const uint64_t qtiles_max = (slice + 31) / 32;
-  q16_.reserve((qtiles_max + 4 * (uint64_t)T) * (uint64_t)kb * 64 * 8);
+  const uint64_t groups_max = (qtiles_max + 4 * T - 1) / (4 * T);
+  // Chunks per stage: about 2048 workgroups, within the append budget; a
+  // small stage (the first, or any of at most 64 blocks, where tau may still
+  // be +inf) takes at most 4 blocks per chunk so that every row of a half
+  // wave's 64 fits its buffer.
+  auto chunks = [&](uint64_t nsel, uint64_t groups, uint64_t m, bool small) {
+    const uint64_t want = std::max<uint64_t>(1, 2048 / groups);
+    const uint64_t room = std::max<uint64_t>(1, kSubBudget / (m * 2 * kSub));
+    uint64_t cb = (nsel + std::min(want, room) - 1) / std::min(want, room);
+    if (small) cb = std::min<uint64_t>(cb, 4);
+    return std::make_pair(std::max<uint64_t>(cb, 1), (nsel + std::max<uint64_t>(cb, 1) - 1) / std::max<uint64_t>(cb, 1));
+  };
+  // buffer sizes: the largest over every pass and stage (a shorter pass has
+  // fewer query groups and may take more chunks)
+  uint64_t max_subs = 1;
+  for (uint64_t q0 = 0; q0 < nq; q0 += slice) {
+    const uint64_t m = std::min(slice, nq - q0);
+    const uint64_t groups = ((m + 31) / 32 + 4 * T - 1) / (4 * T);
+    for (size_t st = 0; st < ladder.size(); ++st)
+      max_subs = std::max(max_subs, m * 2 * chunks(ladder[st], groups, m, st == 0 || ladder[st] <= 64).second);
+  }
+  q16_.reserve((groups_max * 4 * (uint64_t)T) * (uint64_t)kb * 64 * 8);
   qexp_.reserve(slice);
   tau_.reserve(slice);
-  count_.reserve(slice);
   force_.reserve(slice);
-  buf_.reserve(slice * kCap);
+  count_.reserve(max_subs);
+  buf_.reserve(max_subs * kSub);
   cand_d_.reserve(slice * kp);
   cand_k_.reserve(slice * kp);
   cand_c_.reserve(slice);
@@ -482,11 +553,12 @@ void FlatSearcher::screen16(const FlatRows& x, const H16Rows& h, int metric, con
     const uint64_t slots = groups * 4 * T * 32;
     hipLaunchKernelGGL(queries_to_h16_kernel, dim3((unsigned)slots), dim3(64), 0, s, d_qs + q0 * h.dim_, m,
                        h.dim_, kb, q_norm + q0, met == kScrCos ? 1 : 0, h.rnmin, x.rnmax, h.xexp,
-                       reinterpret_cast<v8h*>(q16_.p), qexp_.p, tau_.p, count_.p, force_.p);
+                       reinterpret_cast<v8h*>(q16_.p), qexp_.p, tau_.p, force_.p);
     FDB_HIP(hipGetLastError());
     for (size_t st = 0; st < ladder.size(); ++st) {
       const bool last = st + 1 == ladder.size();
       const uint64_t nsel = ladder[st];
+      const auto [cb, nch] = chunks(nsel, groups, m, st == 0 || nsel <= 64);
       Screen16Args a{};
       a.x16 = reinterpret_cast<const v8h*>(h.x16());
       a.n = h.n_;
@@ -498,30 +570,27 @@ void FlatSearcher::screen16(const FlatRows& x, const H16Rows& h, int metric, con
       a.qexp = qexp_.p;
       a.xexp = h.xexp;
       a.tau = tau_.p;
-      a.count = count_.p;
-      a.buf = buf_.p;
+      a.scnt = count_.p;
+      a.sbuf = buf_.p;
+      a.nchunks = (uint32_t)nch;
       a.bstride = last ? 1 : h.nblk / nsel;
       a.nsel = nsel;
-      // chunks: about 2048 workgroups, whole stages each
-      const uint64_t want = std::max<uint64_t>(1, 2048 / groups);
-      uint64_t cb = (nsel + want - 1) / want;
-      cb = std::max<uint64_t>(sb, (cb + sb - 1) / sb * sb);
       a.chunk_blocks = cb;
-      const unsigned nchunks = cdiv(nsel, cb);
       void* args[] = {(void*)&a};
-      FDB_HIP(hipLaunchKernel(fn, dim3((unsigned)groups, nchunks), dim3(kT16), args, 0, s));
+      FDB_HIP(hipLaunchKernel(fn, dim3((unsigned)groups, (unsigned)nch), dim3(kT16), args, 0, s));
+      const uint32_t nsub = (uint32_t)(2 * nch);
       if (!last) {
         // rank for the next threshold: about 1024 rows of the next stage pass it
         const uint64_t ratio = std::max<uint64_t>(1, ladder[st + 1] / nsel);
         const int rank = (int)std::clamp<uint64_t>(1024 / ratio, 32, 64);
-        hipLaunchKernelGGL(select16_kernel<1>, dim3((unsigned)m), dim3(64), 0, s, count_.p, buf_.p, tau_.p, rank,
-                           0, kp, force_.p, cand_d_.p, cand_k_.p, cand_c_.p, abound_.p);
+        hipLaunchKernelGGL(select16_kernel<1>, dim3((unsigned)m), dim3(64), 0, s, count_.p, buf_.p, nsub, tau_.p,
+                           rank, 0, kp, force_.p, cand_d_.p, cand_k_.p, cand_c_.p, abound_.p);
       } else if (kp == 64) {
-        hipLaunchKernelGGL(select16_kernel<1>, dim3((unsigned)m), dim3(64), 0, s, count_.p, buf_.p, tau_.p, 0, 1,
-                           kp, force_.p, cand_d_.p, cand_k_.p, cand_c_.p, abound_.p);
+        hipLaunchKernelGGL(select16_kernel<1>, dim3((unsigned)m), dim3(64), 0, s, count_.p, buf_.p, nsub, tau_.p, 0,
+                           1, kp, force_.p, cand_d_.p, cand_k_.p, cand_c_.p, abound_.p);
       } else {
-        hipLaunchKernelGGL(select16_kernel<2>, dim3((unsigned)m), dim3(64), 0, s, count_.p, buf_.p, tau_.p, 0, 1,
-                           kp, force_.p, cand_d_.p, cand_k_.p, cand_c_.p, abound_.p);
+        hipLaunchKernelGGL(select16_kernel<2>, dim3((unsigned)m), dim3(64), 0, s, count_.p, buf_.p, nsub, tau_.p, 0,
+                           1, kp, force_.p, cand_d_.p, cand_k_.p, cand_c_.p, abound_.p);
       }
       FDB_HIP(hipGetLastError());
     }
