@@ -152,7 +152,7 @@ def agreement(a, b, k):
 def cpu_sample(run, nq, seconds, probe_n):
     """Times run(m) on a probe of probe_n queries, then on a sample sized for
     about `seconds` of CPU work. When every query fits in less than that, the
-    whole set is searched in repeated passes (at most 30). Returns (queries
+    whole set is searched in repeated passes. Returns (queries
     searched, seconds, result of the first pass, passes)."""
     t = time.perf_counter()
     run(probe_n)
@@ -160,7 +160,7 @@ def cpu_sample(run, nq, seconds, probe_n):
     sample = int(min(nq, max(probe_n, seconds / max(per_q, 1e-9))))
     passes = 1
     if sample == nq:
-        passes = int(min(30, max(1, seconds // max(per_q * nq, 1e-9))))
+        passes = int(min(100_000, max(1, seconds // max(per_q * nq, 1e-9))))
     t = time.perf_counter()
     out = run(sample)
     for _ in range(passes - 1):

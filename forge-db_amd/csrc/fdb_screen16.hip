@@ -8,13 +8,13 @@
 //
 // Stages.  Every stage runs the same kernel over a set of 32-row blocks: a
 // row whose screening value is at most the query's threshold tau is
-// appended to the query's buffer.  The first stage takes 32 evenly spaced
-// blocks with tau = +inf; after each stage tau becomes the m-th smallest
-// value appended (m ~ 32, so about 1024 rows of the next, 32x larger, sample
-// pass it).  The last stage covers every block; the K' smallest of its
-// buffer are rescored, and every other row screens above
-// min(K'-th value, tau).  The thresholds only steer the amount of work:
-// correctness rests on the last stage and the bound.
+// appended to the query's buffers.  The first stage takes at most 32 evenly
+// spaced blocks with tau = +inf; after each stage tau becomes the m-th
+// smallest value appended, m chosen so that about 256 rows of the next
+// (32x, last 8x larger) sample pass it.  The last stage covers every block;
+// the K' smallest of its appends are rescored, and every other row screens
+// above min(K'-th value, tau).  The thresholds only steer the amount of
+// work: correctness rests on the last stage and the bound.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -501,8 +501,12 @@ void FlatSearcher::screen16(const FlatRows& x, const H16Rows& h, int metric, con
   void* fn = met == kScrDot ? pick16<kScrDot>(kb) : (met == kScrCos ? pick16<kScrCos>(kb) : pick16<kScrL2>(kb));
   if (!fn) throw Error(FDB_ERR_UNSUPPORTED, "no fp16 screening kernel for this dimension");
 
-  // the ladder of block counts, last = all blocks
+  // The ladder of block counts, last = all blocks: an 8x step into the last
+  // stage (its threshold is the 32nd value of a 1/8 sample: about 256 rows
+  // of every block pass it, with a spread of about 1/sqrt(32)), 32x steps
+  // before, down to a first stage of at most 32 blocks.
   std::vector<uint64_t> ladder{h.nblk};
+  if (h.nblk > 32) ladder.insert(ladder.begin(), (h.nblk + 7) / 8);
   while (ladder.front() > 32) ladder.insert(ladder.begin(), (ladder.front() + 31) / 32);
 
   // balanced passes of at most kSlice queries
@@ -580,9 +584,12 @@ void FlatSearcher::screen16(const FlatRows& x, const H16Rows& h, int metric, con
       FDB_HIP(hipLaunchKernel(fn, dim3((unsigned)groups, (unsigned)nch), dim3(kT16), args, 0, s));
       const uint32_t nsub = (uint32_t)(2 * nch);
       if (!last) {
-        // rank for the next threshold: about 1024 rows of the next stage pass it
+        // rank for the next threshold: about 256 rows of the next stage pass
+        // it; 32 at least before the last stage, whose threshold bounds the
+        // rows it leaves out
         const uint64_t ratio = std::max<uint64_t>(1, ladder[st + 1] / nsel);
-        const int rank = (int)std::clamp<uint64_t>(1024 / ratio, 32, 64);
+        const uint64_t lo = st + 2 == ladder.size() ? 32 : 8;
+        const int rank = (int)std::clamp<uint64_t>(256 / ratio, lo, 64);
         hipLaunchKernelGGL(select16_kernel<1>, dim3((unsigned)m), dim3(64), 0, s, count_.p, buf_.p, nsub, tau_.p,
                            rank, 0, kp, force_.p, cand_d_.p, cand_k_.p, cand_c_.p, abound_.p);
       } else if (kp == 64) {
