@@ -23,7 +23,9 @@ roofline:
   bf_1m_dot     queries, k 100 (cosine / dot product); flops 2*Q*N*D
   ivf_1m_l2     IVF (full vectors) 1,000,000 x 96 Gaussian mixture, nlist
   ivf_1m_l1     4096, nprobe 32, 10,000 queries, k 100 (Euclidean /
-                Manhattan); bytes sum over queries of scanned rows * D * 4
+                Manhattan); bytes: the probed lists' rows as the scan reads
+                them (half precision when screening, plus the K'
+                candidates' f32 rows; else f32)
   ivfpq_10m     IVF-PQ 10,000,000 x 96 Gaussian mixture, nlist 4096,
                 M 32 x 3, nprobe 64, 10,000 queries, k 100
 
@@ -318,6 +320,7 @@ def bench_ivf(args, w, base, queries):
     log(f"[bench] GPU build (k-means {nlist}, 100 iterations max) in {time.time() - t:.1f}s")
     index.set_nprobe(nprobe)
     index.set_coarse_mode({"auto": 0, "exact": 1, "screen": 2}[args.coarse])
+    index.set_search_mode({"auto": 0, "exact": 1}[args.ivf_mode])
     r = Runner(args, queries, k)
     nq = r.nq
 
@@ -329,17 +332,30 @@ def bench_ivf(args, w, base, queries):
     times = [index.batch_search_device(*r.ptrs(), timed=True) for _ in range(args.timing_reps)]
     coarse_ms = float(np.mean([c for c, _ in times]))
     scan_ms = float(np.mean([s for _, s in times]))
+    path = index.last_search_path()
+    fallbacks = index.last_fallbacks()
     lists = index.probe(queries, nprobe)
     sizes = np.diff(index.export()["list_offsets"].astype(np.int64))
     scanned = int(sizes[lists].sum())
-    row_bytes = scanned * base.shape[1] * 4
+    dim = base.shape[1]
+    fp32_bytes = scanned * dim * 4
+    if path == 2:
+        # half-precision rows of the probed lists + the K' candidates' rows
+        kp = 64 if k + 16 <= 64 else 128
+        row_bytes = scanned * ((dim + 1) // 2) * 4 + nq * kp * dim * 4
+        kernel = "ivf16_screen_kernel + rescore_kernel"
+    else:
+        row_bytes = fp32_bytes
+        kernel = "ivf_flat_scan_kernel"
     achieved = row_bytes / (scan_ms / 1e3) / 1e9
     log(f"[bench] coarse {coarse_ms:.3f} ms, scan {scan_ms:.3f} ms; {scanned / nq:,.0f} rows per "
-        f"query; {row_bytes / 1e9:.2f} GB of rows -> {achieved:,.0f} GB/s")
+        f"query; path {path} ({fallbacks} of {nq} queries rescanned exactly); {row_bytes / 1e9:.2f} GB "
+        f"read -> {achieved:,.0f} GB/s ({fp32_bytes / 1e9:.2f} GB of f32 rows in the probed lists)")
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "ivf_flat_scan_kernel", "kernel_ms": round(scan_ms, 4),
-            "algorithmic_bytes": row_bytes, "coarse_ms": round(coarse_ms, 4)}
+            "kernel": kernel, "kernel_ms": round(scan_ms, 4),
+            "algorithmic_bytes": row_bytes, "f32_row_bytes": fp32_bytes, "coarse_ms": round(coarse_ms, 4),
+            "fallbacks": fallbacks}
     gpu_ids = r.ids().copy()
     cpu = None
     if not args.no_cpu:
@@ -370,6 +386,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target wall time of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--ivf-mode", default="auto", choices=["auto", "exact"],
+                    help="IVF scan strategy (IVFIndex.set_search_mode)")
     ap.add_argument("--bf-mode", default="auto", choices=["auto", "exact", "screen", "screen_f32"],
                     help="brute-force search strategy (BruteForceIndex.set_search_mode)")
     ap.add_argument("--coarse", default="auto", choices=["auto", "exact", "screen"],

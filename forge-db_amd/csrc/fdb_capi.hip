@@ -528,6 +528,27 @@ fdb_status fdb_ivf_set_coarse_mode(fdb_ivf* h, uint32_t mode) {
     impl_of(h)->set_coarse_mode((int)mode);
   });
 }
+fdb_status fdb_ivf_set_search_mode(fdb_ivf* h, uint32_t mode) {
+  return guarded([&] {
+    if (mode > 1) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown search mode");
+    impl_of(h)->set_search_mode((int)mode);
+  });
+}
+
+fdb_status fdb_ivf_last_fallbacks(fdb_ivf* h, void* stream, uint64_t* out) {
+  return guarded([&] {
+    if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    *out = impl_of(h)->last_fallbacks((hipStream_t)stream);
+  });
+}
+
+fdb_status fdb_ivf_last_search_path(fdb_ivf* h, uint32_t* out) {
+  return guarded([&] {
+    if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    *out = (uint32_t)impl_of(h)->last_path();
+  });
+}
+
 uint64_t fdb_ivf_nprobe(const fdb_ivf* h) { return (h && h->impl) ? h->impl->nprobe() : 0; }
 uint64_t fdb_ivf_len(const fdb_ivf* h) { return (h && h->impl) ? h->impl->size() : 0; }
 uint32_t fdb_ivf_num_partitions(const fdb_ivf* h) { return (h && h->impl) ? h->impl->nlist() : 0; }

@@ -286,6 +286,7 @@ __global__ __launch_bounds__(kT) void ivf_flat_scan_kernel(IvfFlatScanArgs a) {
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const uint64_t q = blockIdx.x;
+  if (a.flags && a.flags[q] == 0) return;  // settled by screening
   const int dim = a.dim;
   for (int d = tid; d < dim; d += kT) qp[perm_row(d, dim)] = a.queries[q * dim + d];
   const float qn = (MET == FDB_METRIC_COSINE) ? a.q_norm[q] : 0.0f;
@@ -447,6 +448,40 @@ __device__ __forceinline__ float screen16_eps(int met, int dim, float qn, float 
   return 1.1f * (h + 4.0f * g + 9.0f * u) * (qn + rnmax) + 1e-30f;
 }
 
+// IVF fp16 screening (fdb_ivf16.hip): rows and query scaled by the same 2^e
+// and rounded to fp16 (uh = 2^-11 relative, values below 2^-14 * 2^-e off by
+// at most eta = 2^-14 * 2^-e), differences rounded to fp16, squared (or
+// taken absolute) exactly and summed in fp32 (within g2 = D*2u/(1 - D*2u)).
+// Each component's screening difference is then within
+//   E_i = uh (1 + uh) (|q_i| + |x_i| + |d_i|) + 3.01 eta
+// of d_i = q_i - x_i.  The error grows with the row's own distance, so the
+// check is monotone: with Dk the k-th reference value, Dp = Dk / (1 - g -
+// 2.01u) bounds the exact value of every row whose reference value is at
+// most Dk, and such a row screens at most
+//   L2^2: (1 + g2) (Dp + 1.1 (2 uh (1 + uh) (A + s) s + 6.02 eta sqrt(D) s
+//                             + 3 uh^2 (A + s)^2 + 20 D eta^2)),
+//         s = sqrt(Dp), A = |q| + max|x|
+//   L1:   (1 + g2) (Lp + 1.1 (uh (1 + uh) (|q|_1 + max|x|_1 + Lp) + 3.01 D eta))
+// A screened list whose K'-th value exceeds that leaves out no such row.
+__device__ __forceinline__ float ivf16_bound(bool l1, float vk, float qmag, float xmag, int xexp, int dim) {
+  const float u = 5.9604645e-8f;
+  const float uh = 4.8828125e-4f;
+  const float g = dim * u / (1.0f - dim * u);
+  const float g2 = dim * 2.0f * u / (1.0f - dim * 2.0f * u);
+  const float eta = ldexpf(1.0f, -14 - xexp);
+  if (l1) {
+    const float lp = vk / (1.0f - g - 1.01f * u);
+    const float err = uh * (1.0f + uh) * (qmag + xmag + lp) + 3.01f * dim * eta;
+    return (1.0f + g2) * (lp + 1.1f * err) * 1.0001f + 1e-30f;
+  }
+  const float dp = vk / (1.0f - g - 2.01f * u);
+  const float s = __builtin_sqrtf(dp);
+  const float A = qmag + xmag;
+  const float err = 2.0f * uh * (1.0f + uh) * (A + s) * s + 6.02f * eta * __builtin_sqrtf((float)dim) * s +
+                    3.0f * uh * uh * (A + s) * (A + s) + 20.0f * dim * eta * eta;
+  return (1.0f + g2) * (dp + 1.1f * err) * 1.0001f + 1e-30f;
+}
+
 template <int MET, int RS>
 __global__ __launch_bounds__(kT) void mfma_screen_kernel(ScreenArgs a) {
   extern __shared__ float sm[];
@@ -557,15 +592,20 @@ __global__ __launch_bounds__(64) void rescore_kernel(RescoreArgs a) {
     const bool valid = s < cnt;
     const uint32_t key = valid ? (uint32_t)a.cand_keys[q * kp + s] : kNoPos;
     float e = f_inf();
-    if (valid) e = exact_lane<MET>(qv, a.rows + (uint64_t)key * dim, dim, qn, a.row_norm[key]);
+    if (valid)
+      e = exact_lane<MET>(qv, a.rows + (uint64_t)key * dim, dim, qn,
+                          MET == FDB_METRIC_COSINE ? a.row_norm[key] : 0.0f);
     tk.offer(e, key);
   }
   const uint32_t kk = (uint32_t)a.k < cnt ? (uint32_t)a.k : cnt;
   bool ok = !forced;
   // with a threshold bound, fewer candidates than the top k needs is a miss
-  if (a.abound && (uint64_t)kk < ((uint64_t)a.k < a.n ? (uint64_t)a.k : a.n)) ok = false;
-  if (ok && kk > 0 && (a.abound || cnt >= (uint32_t)kp)) {
-    const float aK = a.abound ? a.abound[q] : a.cand_d[q * kp + kp - 1];
+  if (a.bkind == kBoundH16 && (uint64_t)kk < ((uint64_t)a.k < a.n ? (uint64_t)a.k : a.n)) ok = false;
+  // without one (all other rows screen above the K'-th candidate), fewer
+  // than K' candidates means every row is a candidate
+  const bool check = a.bkind == kBoundH16 || (cnt >= (uint32_t)kp && (a.bkind == kBoundF32 || a.abound[q] < f_inf()));
+  if (ok && kk > 0 && check) {
+    const float aK = a.bkind == kBoundF32 ? a.cand_d[q * kp + kp - 1] : a.abound[q];
     const int s = (int)kk - 1;
     // the k-th exact pair, in the screening domain
     float v = tk.d[0];
@@ -584,8 +624,21 @@ __global__ __launch_bounds__(64) void rescore_kernel(RescoreArgs a) {
     } else {
       v = readlane_f(v, s & 63);
     }
-    const float eps = a.h16 ? screen16_eps(MET, dim, qn, a.rnmax) : screen_eps(MET, dim, qn, a.rnmax);
-    ok = aK - eps > v;
+    if (a.bkind == kBoundIvf16) {
+      float qmag = 0.0f;  // |q|_1 for Manhattan, |q|_2 otherwise
+      if constexpr (MET == FDB_METRIC_MANHATTAN) {
+        for (int d = lane; d < dim; d += 64) qmag += __builtin_fabsf(qv[d]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) qmag += __shfl_xor(qmag, off);
+        qmag *= 1.0f + (float)dim * 5.9604645e-8f;
+      } else {
+        qmag = __builtin_sqrtf(qn) * (1.0f + (float)dim * 5.9604645e-8f);
+      }
+      ok = aK > ivf16_bound(MET == FDB_METRIC_MANHATTAN, v, qmag, a.xmag, a.xexp, dim);
+    } else {
+      const float eps = a.bkind == kBoundH16 ? screen16_eps(MET, dim, qn, a.rnmax) : screen_eps(MET, dim, qn, a.rnmax);
+      ok = aK - eps > v;
+    }
   }
   uint32_t count = 0;
 #pragma unroll
@@ -773,6 +826,10 @@ hipError_t launch_rescore(const RescoreArgs& a, uint64_t nq, hipStream_t s) {
     case FDB_METRIC_EUCLIDEAN_SQUARED: fn = pick_rescore<FDB_METRIC_EUCLIDEAN_SQUARED>(RS, RK); break;
     case FDB_METRIC_COSINE: fn = pick_rescore<FDB_METRIC_COSINE>(RS, RK); break;
     case FDB_METRIC_DOT_PRODUCT: fn = pick_rescore<FDB_METRIC_DOT_PRODUCT>(RS, RK); break;
+    case FDB_METRIC_MANHATTAN:
+      if (a.bkind != kBoundIvf16) return hipErrorInvalidValue;
+      fn = pick_rescore<FDB_METRIC_MANHATTAN>(RS, RK);
+      break;
     default: return hipErrorInvalidValue;
   }
   void* args[] = {(void*)&a};
@@ -1153,23 +1210,22 @@ IvfFlatIndex::IvfFlatIndex(const float* centroids, uint32_t nlist, uint32_t dim,
     tot += (h_offsets_[l + 1] - h_offsets_[l] + 3) / 4 * 4 * (uint64_t)dim;
   }
   data_.reserve(std::max<uint64_t>(tot, 4));
-  {
-    DevBuf<float> d_rows;
-    d_rows.upload(h_rows_.data(), std::max<uint64_t>(n * dim, 1), stream_);
-    for (uint32_t l = 0; l < nlist; ++l) {
-      const uint64_t s = h_offsets_[l], len = h_offsets_[l + 1] - s;
-      if (len == 0) continue;
-      FDB_HIP(launch_transpose_rows(d_rows.p + s * dim, len, dim, (len + 3) / 4 * 4, data_.p + boff[l], stream_));
-    }
-    if (metric == FDB_METRIC_COSINE) {
-      row_norm_.reserve(std::max<uint64_t>(n, 1));
-      FDB_HIP(launch_row_norms(d_rows.p, n, dim, row_norm_.p, stream_));
-    }
-    FDB_HIP(hipStreamSynchronize(stream_));
+  rowsl_.upload(h_rows_.data(), std::max<uint64_t>(n * dim, 1), stream_);
+  for (uint32_t l = 0; l < nlist; ++l) {
+    const uint64_t s = h_offsets_[l], len = h_offsets_[l + 1] - s;
+    if (len == 0) continue;
+    FDB_HIP(launch_transpose_rows(rowsl_.p + s * dim, len, dim, (len + 3) / 4 * 4, data_.p + boff[l], stream_));
   }
+  if (metric == FDB_METRIC_COSINE) {
+    row_norm_.reserve(std::max<uint64_t>(n, 1));
+    FDB_HIP(launch_row_norms(rowsl_.p, n, dim, row_norm_.p, stream_));
+  }
+  FDB_HIP(hipStreamSynchronize(stream_));
   boff_.upload(boff.data(), nlist, stream_);
   std::vector<uint32_t> ro(h_offsets_.begin(), h_offsets_.end());
   row_off_.upload(ro.data(), ro.size(), stream_);
+  if (metric == FDB_METRIC_EUCLIDEAN || metric == FDB_METRIC_EUCLIDEAN_SQUARED || metric == FDB_METRIC_MANHATTAN)
+    l16_.build(rowsl_.p, h_offsets_, nlist, (int)dim, row_off_.p, stream_);
   ids_.upload(h_ids_.data(), std::max<uint64_t>(n, 1), stream_);
   err_.reserve(1);
   hipLaunchKernelGGL(clear_flag, dim3(1), dim3(1), 0, stream_, err_.p);
@@ -1264,9 +1320,54 @@ void IvfFlatIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_i
     coarse_.select(d_qs, nq, np, probes_.p, nullptr, err_.p, s);
   }
   if (timed) FDB_HIP(hipEventRecord(ev_[1], s));
-  if (metric_ == FDB_METRIC_COSINE) {
+  const bool l1 = metric_ == FDB_METRIC_MANHATTAN;
+  // (the exact rescoring reads rows as float4: dim a multiple of 4, <= 512)
+  const bool screen = search_mode_ != 1 && l16_.ok && k + 16 <= 128 && dim_ % 4 == 0 && dim_ <= 512 &&
+                      (l1 || metric_ == FDB_METRIC_EUCLIDEAN || metric_ == FDB_METRIC_EUCLIDEAN_SQUARED);
+  if (metric_ == FDB_METRIC_COSINE || screen) {
     qn_.reserve(nq);
     FDB_HIP(launch_row_norms(d_qs, nq, dim_, qn_.p, s));
+  }
+  path_ = 0;
+  if (screen) {
+    // fp16 screening of the probed lists, exact rescoring of K' candidates,
+    // then the exact scan for the queries the bound does not settle
+    const int kp = (k + 16 <= 64) ? 64 : 128;
+    cand_d_.reserve(nq * kp);
+    cand_k_.reserve(nq * kp);
+    cand_c_.reserve(nq);
+    abound_.reserve(nq);
+    flags_.reserve(nq);
+    fallbacks_.reserve(1);
+    hipLaunchKernelGGL(clear_u32, dim3(1), dim3(1), 0, s, fallbacks_.p);
+    FDB_HIP(hipGetLastError());
+    FDB_HIP(l16_.screen(d_qs, nq, probes_.p, np, nlist_, row_off_.p, l1, kp, cand_d_.p, cand_k_.p, cand_c_.p,
+                        abound_.p, s));
+    RescoreArgs r{};
+    r.queries = d_qs;
+    r.dim = (int)dim_;
+    r.rows = rowsl_.p;
+    r.row_norm = row_norm_.p;
+    r.q_norm = qn_.p;
+    r.cand_keys = cand_k_.p;
+    r.cand_d = cand_d_.p;
+    r.cand_counts = cand_c_.p;
+    r.kp = kp;
+    r.metric = (int)metric_;
+    r.k = (int)k;
+    r.ids = ids_.p;
+    r.out_ids = d_ids;
+    r.out_d = d_dists;
+    r.out_counts = d_counts;
+    r.flags = flags_.p;
+    r.fallbacks = fallbacks_.p;
+    r.abound = abound_.p;
+    r.bkind = kBoundIvf16;
+    r.n = h_ids_.size();
+    r.xmag = l1 ? l16_.xnorm1_max : l16_.xnorm2_max;
+    r.xexp = l16_.xexp;
+    FDB_HIP(launch_rescore(r, nq, s));
+    path_ = 2;
   }
   IvfFlatScanArgs a{};
   a.queries = d_qs;
@@ -1286,6 +1387,7 @@ void IvfFlatIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_i
   a.out_ids = d_ids;
   a.out_d = d_dists;
   a.out_counts = d_counts;
+  a.flags = screen ? flags_.p : nullptr;
   FDB_HIP(launch_ivf_flat_scan(a, s));
   if (timed) {
     FDB_HIP(hipEventRecord(ev_[2], s));
@@ -1293,6 +1395,15 @@ void IvfFlatIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_i
     if (coarse_ms) FDB_HIP(hipEventElapsedTime(coarse_ms, ev_[0], ev_[1]));
     if (scan_ms) FDB_HIP(hipEventElapsedTime(scan_ms, ev_[1], ev_[2]));
   }
+}
+
+uint64_t IvfFlatIndex::last_fallbacks(hipStream_t s) {
+  std::lock_guard<std::mutex> g(mu_);
+  if (path_ == 0 || !fallbacks_.p) return 0;  // the last search did not screen
+  FDB_HIP(hipStreamSynchronize(s ? s : stream_));
+  uint32_t v = 0;
+  FDB_HIP(hipMemcpy(&v, fallbacks_.p, 4, hipMemcpyDeviceToHost));
+  return v;
 }
 
 void IvfFlatIndex::probe(const float* qs, uint64_t nq, uint32_t nprobe, int32_t* lists) {

@@ -71,11 +71,18 @@ hipError_t launch_mfma_screen(const ScreenArgs& a, hipStream_t s);
 // Exact rescoring of screened candidates ([nq][kp], ascending, as merged):
 // writes the k smallest exact results, flags [nq] (1 = the candidates may
 // miss a top-k row) and adds the number of flagged queries to *fallbacks.
-// abound (nullable): per query, a value that every row outside the
-// candidates screens above (threshold screening); then a query with fewer
-// than min(k, n) candidates, or with cand_counts = kForceExact, is flagged.
-// h16: the screening values came from the fp16 product (screen16_eps).
+// bkind selects the check:
+//   kBoundF32:   fp32 screening, the K'-th candidate value minus screen_eps
+//                bounds every other row;
+//   kBoundH16:   fp16 brute-force screening (screen16_eps); abound[q] bounds
+//                the rows outside, and fewer than min(k, n) candidates is a
+//                miss;
+//   kBoundIvf16: fp16 IVF screening (ivf16_bound; xmag, xexp); abound[q]
+//                (+inf: every scanned row is a candidate) against the bound
+//                of the k-th value.
+// A query with cand_counts = kForceExact is flagged.
 constexpr uint32_t kForceExact = 0xFFFFFFFFu;
+enum { kBoundF32 = 0, kBoundH16 = 1, kBoundIvf16 = 2 };
 struct RescoreArgs {
   const float* queries;
   int dim;
@@ -96,8 +103,10 @@ struct RescoreArgs {
   int* flags;
   uint32_t* fallbacks;
   const float* abound;
-  int h16;
+  int bkind;
   uint64_t n;
+  float xmag;  // kBoundIvf16: max |x|_2 (max |x|_1 for Manhattan) over the rows
+  int xexp;    // kBoundIvf16: the rows' fp16 scale exponent
 };
 hipError_t launch_rescore(const RescoreArgs& a, uint64_t nq, hipStream_t s);
 
@@ -121,8 +130,35 @@ struct IvfFlatScanArgs {
   uint64_t* out_ids;
   float* out_d;
   uint32_t* out_counts;
+  const int* flags;  // nullable: [nq]; queries with a zero flag return at once
 };
 hipError_t launch_ivf_flat_scan(const IvfFlatScanArgs& a, hipStream_t s);
+
+// The lists of an IVF index in half precision for screening (fdb_ivf16.hip):
+// per list a block [dim2][lld] of 32-bit words, word (j, r) the pair
+// (x_2j, x_2j+1) * 2^xexp of row r as two halves (lld = |L_p| rounded up to
+// 4; an odd dim is padded with a zero), and the rows' largest L2 and L1
+// norms.  ok = false when the rows are not finite or their scale is out of
+// reach.
+struct Ivf16Lists {
+  bool ok = false;
+  int dim_ = 0, dim2 = 0, xexp = 0;
+  float xnorm2_max = 0.0f, xnorm1_max = 0.0f;
+  // d_rows [N][dim] row-major in list order; offsets [nlist+1]
+  void build(const float* d_rows, const std::vector<uint64_t>& offsets, uint32_t nlist, int dim,
+             const uint32_t* d_row_off, hipStream_t s);
+  // the kp (64 or 128) smallest screening values per query over its probed
+  // lists: cand_d/cand_k [nq][kp] (list positions), cand_c [nq] (kForceExact
+  // when the query does not fit fp16), abound [nq] (the kp-th value, +inf when
+  // every scanned row is a candidate); l1: Manhattan, else squared L2
+  hipError_t screen(const float* d_qs, uint64_t nq, const int32_t* probes, uint32_t np, uint32_t nlist,
+                    const uint32_t* d_row_off, bool l1, int kp, float* cand_d, uint64_t* cand_k, uint32_t* cand_c,
+                    float* abound, hipStream_t s) const;
+
+ private:
+  DevBuf<uint32_t> data_, stats_;
+  DevBuf<uint64_t> boff_;
+};
 
 // ---- exact and screened top-k over a row set ------------------------------
 
@@ -312,6 +348,20 @@ class IvfFlatIndex {
     std::lock_guard<std::mutex> g(mu_);
     coarse_.set_mode(m);
   }
+  // scan strategy: 0 = automatic (fp16 screening + exact rescoring for
+  // Euclidean, squared Euclidean and Manhattan when k <= 112 and dim is a
+  // multiple of 4, <= 512), 1 = exact scan only; same results
+  void set_search_mode(int m) {
+    std::lock_guard<std::mutex> g(mu_);
+    search_mode_ = m;
+  }
+  // queries of the last search rescanned exactly after screening (waits for s)
+  uint64_t last_fallbacks(hipStream_t s);
+  // how the last search ran: 0 exact scan, 2 fp16 screening
+  int last_path() {
+    std::lock_guard<std::mutex> g(mu_);
+    return path_;
+  }
   uint32_t dim() const { return dim_; }
   uint64_t size() const { return h_ids_.size(); }
   void set_nprobe(uint64_t np) { nprobe_.store(np < nlist_ ? np : nlist_, std::memory_order_relaxed); }
@@ -342,6 +392,13 @@ class IvfFlatIndex {
   hipStream_t stream_ = nullptr;
   std::mutex mu_;
   DevBuf<float> centT_, cent_, data_, row_norm_;
+  DevBuf<float> rowsl_;  // [N][dim] row-major, list order (rescoring)
+  Ivf16Lists l16_;
+  int search_mode_ = 0, path_ = 0;
+  DevBuf<float> cand_d_, abound_;
+  DevBuf<uint64_t> cand_k_;
+  DevBuf<uint32_t> cand_c_, fallbacks_;
+  DevBuf<int> flags_;
   CoarseQuantizer coarse_;
   DevBuf<uint64_t> boff_, ids_;
   DevBuf<uint32_t> row_off_;

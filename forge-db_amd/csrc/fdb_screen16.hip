@@ -621,7 +621,7 @@ void FlatSearcher::screen16(const FlatRows& x, const H16Rows& h, int metric, con
     r.flags = flags_.p + q0;
     r.fallbacks = fallbacks_.p;
     r.abound = abound_.p;
-    r.h16 = 1;
+    r.bkind = kBoundH16;
     r.n = x.n;
     FDB_HIP(launch_rescore(r, m, s));
   }

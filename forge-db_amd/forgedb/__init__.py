@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "fdb_ivfpq_batch_search_device_timed", "fdb_ivfpq_set_lut_mode", "fdb_ivfpq_lut_mode",
     "fdb_ivfpq_search_filtered", "fdb_ivfpq_delete", "fdb_ivfpq_insert", "fdb_ivfpq_compact",
     "fdb_ivfpq_len", "fdb_ivfpq_num_tombstones", "fdb_ivfpq_set_coarse_mode", "fdb_ivf_set_coarse_mode",
+    "fdb_ivf_set_search_mode", "fdb_ivf_last_fallbacks", "fdb_ivf_last_search_path",
     "fdb_bf_create", "fdb_bf_add", "fdb_bf_remove", "fdb_bf_len", "fdb_bf_dimension",
     "fdb_bf_metric", "fdb_bf_load", "fdb_bf_save", "fdb_bf_destroy", "fdb_bf_export",
     "fdb_bf_search", "fdb_bf_batch_search", "fdb_bf_batch_search_device",
@@ -57,6 +58,7 @@ EXPORTED_SYMBOLS = (
 
 LUT_EXACT, LUT_FAST = 0, 1
 BF_AUTO, BF_EXACT, BF_SCREEN, BF_SCREEN_F32 = 0, 1, 2, 3
+IVF_AUTO, IVF_EXACT = 0, 1
 COARSE_AUTO, COARSE_EXACT, COARSE_SCREEN = 0, 1, 2
 
 
@@ -134,6 +136,9 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fdb_ivfpq_compact": [_P],
         "fdb_ivfpq_set_coarse_mode": [_P, C.c_uint32],
         "fdb_ivf_set_coarse_mode": [_P, C.c_uint32],
+        "fdb_ivf_set_search_mode": [_P, C.c_uint32],
+        "fdb_ivf_last_fallbacks": [_P, _P, _P],
+        "fdb_ivf_last_search_path": [_P, _P],
         "fdb_bf_create": [C.c_uint32, _P],
         "fdb_bf_add": [_P, _P, _P, C.c_uint64, C.c_uint32],
         "fdb_bf_remove": [_P, C.c_uint64, _P],
@@ -655,6 +660,24 @@ class IVFIndex:
     def set_coarse_mode(self, mode: int) -> None:
         """COARSE_AUTO, COARSE_EXACT or COARSE_SCREEN; same probes in every mode."""
         _check(self._lib, self._lib.fdb_ivf_set_coarse_mode(self._h, int(mode)))
+
+    def set_search_mode(self, mode: int) -> None:
+        """IVF_AUTO (default: half-precision screening + exact rescoring for
+        Euclidean, squared Euclidean and Manhattan) or IVF_EXACT (exact-order
+        scan only); same results."""
+        _check(self._lib, self._lib.fdb_ivf_set_search_mode(self._h, int(mode)))
+
+    def last_fallbacks(self, stream: int = 0) -> int:
+        """Queries of the last search that were rescanned exactly."""
+        out = C.c_uint64()
+        _check(self._lib, self._lib.fdb_ivf_last_fallbacks(self._h, C.c_void_p(stream), C.byref(out)))
+        return int(out.value)
+
+    def last_search_path(self) -> int:
+        """How the last search ran: 0 exact scan, 2 fp16 screening."""
+        out = C.c_uint32()
+        _check(self._lib, self._lib.fdb_ivf_last_search_path(self._h, C.byref(out)))
+        return int(out.value)
 
     def __len__(self) -> int:
         return int(self._lib.fdb_ivf_len(self._h))

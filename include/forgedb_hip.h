@@ -315,6 +315,22 @@ FDB_API void fdb_ivf_destroy(fdb_ivf* index);
 FDB_API void fdb_ivf_set_nprobe(fdb_ivf* index, uint64_t nprobe);
 /* Coarse selection strategy, as fdb_ivfpq_set_coarse_mode. */
 FDB_API fdb_status fdb_ivf_set_coarse_mode(fdb_ivf* index, uint32_t mode);
+/* Scan strategy (no counterpart in the reference, whose scan is one loop):
+ *   FDB_IVF_AUTO (default): for Euclidean, squared Euclidean and Manhattan
+ *     with k <= 112 and dim a multiple of 4 (<= 512), the probed lists are scanned in half precision to pick
+ *     K' = 64 or 128 candidates per query, their distances are recomputed
+ *     exactly in the reference's order, and a rounding-error bound proves
+ *     that no other scanned row can enter the top k; queries where it cannot
+ *     be proved are rescanned exactly.  Results are identical to
+ *     FDB_IVF_EXACT.
+ *   FDB_IVF_EXACT: the exact-order scan for every query.
+ * fdb_ivf_last_fallbacks counts the queries of the last search that were
+ * rescanned (waits for hip_stream; NULL = the handle's own stream);
+ * fdb_ivf_last_search_path reports 0 (exact scan) or 2 (fp16 screening). */
+enum { FDB_IVF_AUTO = 0, FDB_IVF_EXACT = 1 };
+FDB_API fdb_status fdb_ivf_set_search_mode(fdb_ivf* index, uint32_t mode);
+FDB_API fdb_status fdb_ivf_last_fallbacks(fdb_ivf* index, void* hip_stream, uint64_t* out);
+FDB_API fdb_status fdb_ivf_last_search_path(fdb_ivf* index, uint32_t* out);
 FDB_API uint64_t fdb_ivf_nprobe(const fdb_ivf* index);
 /* len (:135), num_partitions (:145), dimension (:150) */
 FDB_API uint64_t fdb_ivf_len(const fdb_ivf* index);

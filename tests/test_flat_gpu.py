@@ -16,8 +16,8 @@ import pytest
 
 import refcpu
 
-from forgedb import (BF_EXACT, BF_SCREEN, BF_SCREEN_F32, COARSE_SCREEN, BruteForceIndex, DistanceMetric,
-                     ForgeDbError, IVFIndex, datagen)
+from forgedb import (BF_EXACT, BF_SCREEN, BF_SCREEN_F32, COARSE_SCREEN, IVF_AUTO, IVF_EXACT, BruteForceIndex,
+                     DistanceMetric, ForgeDbError, IVFIndex, datagen)
 
 pytestmark = pytest.mark.gpu
 
@@ -281,9 +281,13 @@ def ivf_small():
                 rows=base[order])
 
 
-def ivf_pair(s, metric, nprobe, k, queries=None, coarse=None):
+IVF_SCREENED = (DistanceMetric.Euclidean, DistanceMetric.EuclideanSquared, DistanceMetric.Manhattan)
+
+
+def ivf_pair(s, metric, nprobe, k, queries=None, coarse=None, mode=IVF_AUTO):
     q = s["queries"] if queries is None else queries
     g = IVFIndex.from_artifacts(s["cen"], s["off"], s["ids"], s["rows"], metric)
+    g.set_search_mode(mode)
     if coarse is not None:
         g.set_coarse_mode(coarse)
     g.set_nprobe(nprobe)
@@ -293,12 +297,55 @@ def ivf_pair(s, metric, nprobe, k, queries=None, coarse=None):
     return g, out, ref
 
 
+@pytest.mark.parametrize("mode", [IVF_AUTO, IVF_EXACT], ids=["auto", "exact"])
 @pytest.mark.parametrize("metric", METRICS, ids=[m.name for m in METRICS])
 @pytest.mark.parametrize("nprobe,k", [(1, 10), (8, 100), (32, 100), (128, 7)])
-def test_ivf_parity(ivf_small, metric, nprobe, k):
-    print(f"ivf 24k x 96, nlist 128, nprobe {nprobe}, k {k}, {metric.name}", flush=True)
-    _, (gi, gd, gc), (oi, od, oc) = ivf_pair(ivf_small, metric, nprobe, k)
+def test_ivf_parity(ivf_small, metric, nprobe, k, mode):
+    print(f"ivf 24k x 96, nlist 128, nprobe {nprobe}, k {k}, {metric.name}, mode {mode}", flush=True)
+    g, (gi, gd, gc), (oi, od, oc) = ivf_pair(ivf_small, metric, nprobe, k, mode=mode)
     check_rows(gi, gd, gc, oi, od, oc, f"{metric.name} nprobe {nprobe}")
+    screened = mode == IVF_AUTO and metric in IVF_SCREENED
+    assert g.last_search_path() == (2 if screened else 0)
+    if screened:
+        fb = g.last_fallbacks()
+        print(f"  fp16 screening: {fb} of 64 queries rescanned", flush=True)
+        assert fb <= 6
+
+
+def test_ivf_fp16_screen_edges(ivf_small):
+    """Near-equal rows, a query beyond the rows' scale, an odd dimension and
+    lists shorter than the candidate count: results match the oracle, and
+    the queries the bound cannot settle are rescanned."""
+    print("ivf fp16 screening edge cases", flush=True)
+    rng = np.random.default_rng(21)
+    s = dict(ivf_small)
+    # 200 copies (within 1e-4) of each of 3 rows of the first list
+    rows = s["rows"].copy()
+    n0 = int(s["off"][1])
+    for t in range(3):
+        src = rows[t].copy()
+        pos = rng.choice(np.arange(3, n0), min(200, n0 - 3) // 3, replace=False)
+        rows[pos] = src + rng.uniform(-1e-4, 1e-4, (len(pos), rows.shape[1])).astype(np.float32)
+    s["rows"] = rows
+    q = np.concatenate([rows[:3] + 1e-3, s["queries"][:5]]).astype(np.float32)
+    q[4, 7] = 1e6  # far beyond the rows' scale: rescanned exactly
+    for metric in IVF_SCREENED:
+        g, (gi, gd, gc), (oi, od, oc) = ivf_pair(s, metric, 4, 100, queries=q)
+        check_rows(gi, gd, gc, oi, od, oc, f"near ties {metric.name}")
+        assert g.last_search_path() == 2 and g.last_fallbacks() >= 1, metric.name
+    # an odd number of dimension pairs, short lists (every scanned row a
+    # candidate); a dimension the exact rescoring does not take (37) scans
+    # exactly
+    for dim, path in ((44, 2), (37, 0)):
+        base = rng.standard_normal((3000, dim)).astype(np.float32)
+        cen, off, order = refcpu.ivf_build(base, 64, seed=2)
+        s2 = dict(cen=cen, off=off, ids=order.astype(np.uint64), rows=base[order],
+                  queries=rng.standard_normal((50, dim)).astype(np.float32))
+        for metric in IVF_SCREENED:
+            for nprobe, k in ((1, 100), (6, 30), (64, 112)):
+                g, (gi, gd, gc), (oi, od, oc) = ivf_pair(s2, metric, nprobe, k)
+                check_rows(gi, gd, gc, oi, od, oc, f"dim {dim} {metric.name} nprobe {nprobe}")
+                assert g.last_search_path() == path
 
 
 @pytest.mark.parametrize("metric", [DistanceMetric.Euclidean, DistanceMetric.Manhattan])
