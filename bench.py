@@ -293,8 +293,10 @@ def bench_bf(args, w, base, queries):
                     2: (FP16_PEAK_TFLOPS, "screen16_kernel (fp16) + select16_kernel + rescore_kernel")}[path]
     log(f"[bench] search kernels {kms:.3f} ms -> {achieved:.1f} TFLOP/s (2*Q*N*D); path {path}, "
         f"{fallbacks} of {nq} queries rescanned exactly")
+    traffic = read_traffic("bf_screen16_1Mx128_dot_traffic.txt") if (path == 2 and w is WORKLOADS["bf_1m_dot"]) \
+        else None
     roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
-            "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None,
+            "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": traffic,
             "kernel": kernel, "kernel_ms": round(kms, 4), "algorithmic_flops": flops,
             "fallbacks": fallbacks}
     gpu_ids = r.ids().copy()
@@ -351,8 +353,10 @@ def bench_ivf(args, w, base, queries):
     log(f"[bench] coarse {coarse_ms:.3f} ms, scan {scan_ms:.3f} ms; {scanned / nq:,.0f} rows per "
         f"query; path {path} ({fallbacks} of {nq} queries rescanned exactly); {row_bytes / 1e9:.2f} GB "
         f"read -> {achieved:,.0f} GB/s ({fp32_bytes / 1e9:.2f} GB of f32 rows in the probed lists)")
+    traffic = read_traffic("ivf16_screen_1Mx96_l2_traffic.txt") if (path == 2 and w is WORKLOADS["ivf_1m_l2"]) \
+        else None
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "kernel": kernel, "kernel_ms": round(scan_ms, 4),
             "algorithmic_bytes": row_bytes, "f32_row_bytes": fp32_bytes, "coarse_ms": round(coarse_ms, 4),
             "fallbacks": fallbacks}
