@@ -32,7 +32,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int kT16 = 256;          // threads per screening workgroup (4 waves)
 constexpr int kStageKiB = 32;      // LDS per workgroup: one stage of row blocks
 constexpr uint32_t kSub = 64;      // entries of one append buffer
-constexpr uint64_t kSlice = 8192;  // queries per pass
+constexpr uint64_t kSlice = 16384;  // queries per pass
 constexpr uint64_t kSubBudget = 1ull << 26;  // append entries per pass (512 MB)
 
 // Exponent e with maxabs * 2^e in [2^13, 2^14); 0 for 0 or non-finite.

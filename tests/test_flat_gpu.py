@@ -119,7 +119,7 @@ def test_bf_shapes(dim, n, nq, k):
 
 
 @pytest.mark.parametrize("n,dim,nq,k", [(100, 32, 40, 10), (1025, 64, 70, 48), (40_000, 32, 300, 100),
-                                        (3000, 96, 8200, 1), (2047, 200, 33, 112)])
+                                        (3000, 96, 16500, 1), (2047, 200, 33, 112)])
 def test_bf_fp16_screen_sizes(n, dim, nq, k):
     """Row counts for one, two and three threshold stages, a query batch
     over two passes, the largest k, a dimension padded to whole k-steps."""
