@@ -1066,7 +1066,14 @@ void CoarseQuantizer::select(const float* d_qs, uint64_t nq, uint32_t np, int32_
   const bool screen =
       mode_ == 2 && FlatSearcher::screenable(FDB_METRIC_EUCLIDEAN_SQUARED, (int)dim_, np) && nlist_ > 64;
   if (!screen) {
-    FDB_HIP(launch_coarse_select(d_qs, nq, (int)dim_, centT_, (int)nlist_, (int)np, probes, dists, err, s));
+    const uint64_t parts = (uint64_t)coarse_parts(nq, (int)nlist_, (int)np);
+    const uint64_t cap = parts > 1 ? nq * parts * np : 0;
+    if (cap) {
+      part_d_.reserve(cap);
+      part_k_.reserve(cap);
+    }
+    FDB_HIP(launch_coarse_select(d_qs, nq, (int)dim_, centT_, (int)nlist_, (int)np, probes, dists, err, s,
+                                 part_d_.p, part_k_.p, cap));
     return;
   }
   // the exact kernel reports NaN distances; here a NaN query is looked for

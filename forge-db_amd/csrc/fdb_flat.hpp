@@ -252,9 +252,9 @@ class CoarseQuantizer {
   int mode_ = 0;
   float rnmax_ = 0.0f;
   FlatSearcher srch_;
-  DevBuf<float> cnorm_, qn_, dtmp_;
+  DevBuf<float> cnorm_, qn_, dtmp_, part_d_;
   DevBuf<uint64_t> keys_;
-  DevBuf<uint32_t> cnt_;
+  DevBuf<uint32_t> cnt_, part_k_;
 };
 
 // ---- BruteForceIndex ------------------------------------------------------

@@ -22,18 +22,31 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kCoarseTQ = 4;                 // queries per wave
 constexpr int kCoarseQB = 4 * kCoarseTQ;     // queries per workgroup (4 waves)
+// below this many query tiles (two per CU) the centroids are split into
+// parts: at 100 queries four parts ran 2-3.5x faster, at 10,000 queries (625
+// tiles) one part was 5-30% faster, every part paying its own list fill
+constexpr uint64_t kCoarseTargetWG = 512;
+// bound on the partial-list workspace, in (distance, centroid) entries
+constexpr uint64_t kCoarsePartEntries = 1ull << 24;
 
 // ---------------------------------------------------------------------------
 // Coarse selection.  A workgroup takes kCoarseQB queries, each wave 4 of
-// them, and sweeps all centroids 256 at a time: lane L holds centroids
+// them, and sweeps one part of the centroids (blockIdx.y: centroids
+// [y*part_len, (y+1)*part_len), part_len a multiple of 256; all of them when
+// gridDim.y = 1) 256 at a time, so the four waves read the same centroid
+// values and a small batch can still fill the GPU: lane L holds centroids
 // c..c+3 (c = base + 4L).  For lane l of the reference's 8 FMA lanes it
 // walks rows l*d8 .. l*d8+d8-1 of centT: one coalesced float4 of centroid
 // values and one wave-uniform (broadcast) float4 of the wave's 4 query values
 // per row feed 16 independent FMA chains; each finished lane chain is added
 // to the running total left to right, then the tail rows are added as
 // separate multiply and add.  The 16 distances go straight from registers
-// into the wave's 4 WaveTopK lists.  centT rows have ldc >= nlist (a
-// multiple of 256) entries; columns >= nlist are never selected.
+// into the wave's 4 WaveTopK lists through per-query LDS queues
+// (offer_queued), so a list is merged once per 64 passing candidates rather
+// than at every offer.  centT rows have ldc >= nlist (a
+// multiple of 256) entries; columns >= nlist are never selected.  With one
+// part the lists are the result; with several, each part's list goes to
+// part_d / part_k [nq][parts][nsel] and coarse_merge_kernel selects from them.
 // ---------------------------------------------------------------------------
 // D8T: compile-time floor(dim / 8) (0 = runtime), so one lane's rows can be
 // loaded before any is used.
@@ -41,8 +54,10 @@ template <int R, int D8T>
 __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
     const float* __restrict__ queries, uint64_t nq, int dim, const float* __restrict__ centT,
     int ldc, int nlist, int nsel, int32_t* __restrict__ out_lists, float* __restrict__ out_dists,
-    int* __restrict__ err_flag) {
+    int* __restrict__ err_flag, int part_len, float* __restrict__ part_d,
+    uint32_t* __restrict__ part_k) {
   extern __shared__ float qsT[];  // [dim][QB], rows permuted
+  __shared__ uint2 s_queue[kThreads / 64][kCoarseTQ][64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -56,13 +71,19 @@ __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
     qsT[row * kCoarseQB + qq] = (q0 + qq < nq) ? queries[(q0 + qq) * (uint64_t)dim + d] : 0.0f;
   }
   WaveTopK<R> tk[kCoarseTQ];
+  int qn[kCoarseTQ];
 #pragma unroll
-  for (int t = 0; t < kCoarseTQ; ++t) tk[t].init(nsel);
+  for (int t = 0; t < kCoarseTQ; ++t) {
+    tk[t].init(nsel);
+    qn[t] = 0;
+  }
   bool saw_nan = false;
   __syncthreads();
 
   const float* __restrict__ qw = qsT + wave * kCoarseTQ;
-  for (int base = 0; base < nlist; base += 256) {
+  const int c_beg = (int)blockIdx.y * part_len;
+  const int c_end = min(nlist, c_beg + part_len);
+  for (int base = c_beg; base < c_end; base += 256) {
     const int c = base + 4 * lane;
     float tot[kCoarseTQ][4];
 #pragma unroll
@@ -131,38 +152,76 @@ __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const bool in = c + u < nlist;
+      const bool in = c + u < c_end;
 #pragma unroll
       for (int t = 0; t < kCoarseTQ; ++t) {
-        const float dv = in ? tot[t][u] : f_inf();
+        const float dv = tot[t][u];
         if (in && dv != dv) saw_nan = true;
-        tk[t].offer(dv, in ? (uint32_t)(c + u) : kNoPos);
+        tk[t].offer_queued(dv, (uint32_t)(c + u), in, s_queue[wave][t], qn[t]);
       }
     }
   }
+#pragma unroll
+  for (int t = 0; t < kCoarseTQ; ++t) tk[t].flush(s_queue[wave][t], qn[t]);
 
+  const bool parts = gridDim.y > 1;
 #pragma unroll
   for (int t = 0; t < kCoarseTQ; ++t) {
     const uint64_t q = q0 + wave * kCoarseTQ + t;
     if (q >= nq) continue;
+    const uint64_t o = parts ? (q * gridDim.y + blockIdx.y) * nsel : q * nsel;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int s = r * 64 + lane;
       if (s < nsel) {
-        out_lists[q * nsel + s] = (int32_t)tk[t].p[r];
-        if (out_dists) out_dists[q * nsel + s] = tk[t].d[r];
+        if (parts) {
+          part_d[o + s] = tk[t].d[r];
+          part_k[o + s] = tk[t].p[r];
+        } else {
+          out_lists[o + s] = (int32_t)tk[t].p[r];
+          if (out_dists) out_dists[o + s] = tk[t].d[r];
+        }
       }
     }
   }
   if (saw_nan && err_flag) atomicOr(err_flag, 1);
 }
 
+// One wave per query: the nsel smallest (distance, centroid) pairs of its
+// `parts` partial lists (entries without a centroid are (+inf, kNoPos)).
+template <int R>
+__global__ __launch_bounds__(kThreads) void coarse_merge_kernel(
+    const float* __restrict__ part_d, const uint32_t* __restrict__ part_k, uint64_t nq, int parts,
+    int nsel, int32_t* __restrict__ out_lists, float* __restrict__ out_dists) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t q = (uint64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (q >= nq) return;
+  WaveTopK<R> tk;
+  tk.init(nsel);
+  const int total = parts * nsel;
+  const float* pd = part_d + q * total;
+  const uint32_t* pk = part_k + q * total;
+  for (int b = 0; b < total; b += 64) {
+    const int e = b + lane;
+    tk.offer(e < total ? pd[e] : f_inf(), e < total ? pk[e] : kNoPos);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int s = r * 64 + lane;
+    if (s < nsel) {
+      out_lists[q * nsel + s] = (int32_t)tk.p[r];
+      if (out_dists) out_dists[q * nsel + s] = tk.d[r];
+    }
+  }
+}
+
 template <int R>
 hipError_t launch_coarse_t(const float* queries, uint64_t nq, int dim, const float* centT, int ldc,
                            int nlist, int nsel, int32_t* out_lists, float* out_dists, int* err_flag,
-                           hipStream_t stream) {
+                           int parts, float* part_d, uint32_t* part_k, hipStream_t stream) {
   const size_t lds = sizeof(float) * (size_t)kCoarseQB * dim;
-  void (*fn)(const float*, uint64_t, int, const float*, int, int, int, int32_t*, float*, int*) =
+  void (*fn)(const float*, uint64_t, int, const float*, int, int, int, int32_t*, float*, int*, int,
+             float*, uint32_t*) =
       dim / 8 == 16 ? coarse_select_kernel<R, 16>
                     : (dim / 8 == 12 ? coarse_select_kernel<R, 12> : coarse_select_kernel<R, 0>);
   if (lds > 64 * 1024) {
@@ -171,8 +230,14 @@ hipError_t launch_coarse_t(const float* queries, uint64_t nq, int dim, const flo
     if (e != hipSuccess) return e;
   }
   const uint64_t blocks = (nq + kCoarseQB - 1) / kCoarseQB;
-  hipLaunchKernelGGL(fn, dim3((unsigned)blocks), dim3(kThreads), lds, stream, queries, nq, dim,
-                     centT, ldc, nlist, nsel, out_lists, out_dists, err_flag);
+  const int part_len = (ldc / 256 + parts - 1) / parts * 256;
+  hipLaunchKernelGGL(fn, dim3((unsigned)blocks, (unsigned)parts), dim3(kThreads), lds, stream,
+                     queries, nq, dim, centT, ldc, nlist, nsel, out_lists, out_dists, err_flag,
+                     part_len, part_d, part_k);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || parts == 1) return e;
+  hipLaunchKernelGGL(coarse_merge_kernel<R>, dim3((unsigned)((nq + 3) / 4)), dim3(kThreads), 0,
+                     stream, part_d, part_k, nq, parts, nsel, out_lists, out_dists);
   return hipGetLastError();
 }
 
@@ -635,18 +700,40 @@ __global__ __launch_bounds__(kThreads) void pq_encode_kernel(
 
 }  // namespace
 
+int coarse_parts(uint64_t nq, int nlist, int nsel) {
+  const uint64_t tiles = (nq + kCoarseQB - 1) / kCoarseQB;
+  const int sweeps = centT_ld(nlist) / 256;
+  if (nq == 0 || tiles >= kCoarseTargetWG || sweeps < 2) return 1;
+  int parts = (int)std::min<uint64_t>((kCoarseTargetWG + tiles - 1) / tiles, (uint64_t)sweeps);
+  // every part must still hold nsel centroids
+  parts = std::min(parts, std::max(1, nlist / std::max(nsel, 1)));
+  while (parts > 1 && nq * (uint64_t)parts * nsel > kCoarsePartEntries) --parts;
+  if (parts <= 1) return 1;
+  // equal whole sweeps per part, none empty
+  const int per = (sweeps + parts - 1) / parts;
+  return (sweeps + per - 1) / per;
+}
+
 hipError_t launch_coarse_select(const float* queries, uint64_t nq, int dim, const float* centT,
                                 int nlist, int nsel, int32_t* out_lists, float* out_dists,
-                                int* err_flag, hipStream_t stream) {
+                                int* err_flag, hipStream_t stream, float* part_d,
+                                uint32_t* part_k, uint64_t part_cap) {
   if (nq == 0) return hipSuccess;
   if (nsel <= 0 || nsel > 1024 || nlist <= 0 || dim <= 0 || dim > 2048) return hipErrorInvalidValue;
+  int parts = (part_d && part_k) ? coarse_parts(nq, nlist, nsel) : 1;
+  if (parts > 1 && nq * (uint64_t)parts * nsel > part_cap) return hipErrorInvalidValue;
+  const int ld = centT_ld(nlist);
+#define FDB_CS(R)                                                                                  \
+  return launch_coarse_t<R>(queries, nq, dim, centT, ld, nlist, nsel, out_lists, out_dists, err_flag, \
+                            parts, part_d, part_k, stream);
   switch (topk_regs(nsel)) {
-    case 1: return launch_coarse_t<1>(queries, nq, dim, centT, centT_ld(nlist), nlist, nsel, out_lists, out_dists, err_flag, stream);
-    case 2: return launch_coarse_t<2>(queries, nq, dim, centT, centT_ld(nlist), nlist, nsel, out_lists, out_dists, err_flag, stream);
-    case 4: return launch_coarse_t<4>(queries, nq, dim, centT, centT_ld(nlist), nlist, nsel, out_lists, out_dists, err_flag, stream);
-    case 8: return launch_coarse_t<8>(queries, nq, dim, centT, centT_ld(nlist), nlist, nsel, out_lists, out_dists, err_flag, stream);
-    case 16: return launch_coarse_t<16>(queries, nq, dim, centT, centT_ld(nlist), nlist, nsel, out_lists, out_dists, err_flag, stream);
+    case 1: FDB_CS(1)
+    case 2: FDB_CS(2)
+    case 4: FDB_CS(4)
+    case 8: FDB_CS(8)
+    case 16: FDB_CS(16)
   }
+#undef FDB_CS
   return hipErrorInvalidValue;
 }
 

@@ -13,9 +13,16 @@ namespace fdb {
 // matrix transposed to [dim][nlist] with dimensions permuted so that the 8
 // FMA lanes read contiguous rows (see permute_dim).  nsel <= 1024.
 // err_flag (nullable) is OR-ed with 1 when a distance is NaN.
+// With a workspace part_d / part_k of part_cap entries (>= nq *
+// coarse_parts(nq, nlist, nsel) * nsel), a batch too small to fill the GPU
+// splits the centroids into coarse_parts(...) parts, each selecting its own
+// list, and a second kernel merges them; the result is the same.
 hipError_t launch_coarse_select(const float* queries, uint64_t nq, int dim, const float* centT,
                                 int nlist, int nsel, int32_t* out_lists, float* out_dists,
-                                int* err_flag, hipStream_t stream);
+                                int* err_flag, hipStream_t stream, float* part_d = nullptr,
+                                uint32_t* part_k = nullptr, uint64_t part_cap = 0);
+// Number of centroid parts launch_coarse_select uses for this batch (1 = none).
+int coarse_parts(uint64_t nq, int nlist, int nsel);
 
 // Leading dimension of centT: rows are padded to a multiple of 256 columns
 // (the coarse kernel reads 256 centroids per sweep); padding is zero.

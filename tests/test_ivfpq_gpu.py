@@ -52,6 +52,32 @@ def test_probe_parity_bit_exact(small_ivfpq, mode):
             assert np.array_equal(lists[q], ol), (nprobe, q)
 
 
+@pytest.mark.parametrize("nlist,dim,nq", [(300, 40, 2100), (1100, 128, 33), (4096, 96, 700)])
+def test_probe_parity_centroid_parts(nlist, dim, nq):
+    """Batches too small to fill the GPU split the centroids into parts whose
+    lists are merged; twins placed in other parts make exact ties across them."""
+    print(f"probe parity with centroid parts: nlist {nlist}, dim {dim}, {nq} queries", flush=True)
+    rng = np.random.default_rng(nlist + dim)
+    M = 4
+    cen = rng.standard_normal((nlist, dim)).astype(np.float32)
+    half = nlist // 2
+    cen[half:half + nlist // 4] = cen[:nlist // 4]  # twins: ties resolve to the lower list id
+    cb = rng.standard_normal((M, 256, dim // M)).astype(np.float32)
+    offsets = np.arange(nlist + 1, dtype=np.uint64)
+    ids = np.arange(nlist, dtype=np.uint64)
+    codes = rng.integers(0, 256, (nlist, M), dtype=np.uint8)
+    gx = gpu_index(dict(centroids=cen, codebooks=cb, list_offsets=offsets, ids=ids, codes=codes))
+    ox = refcpu.IvfPq.create(cen, cb, offsets, ids, codes)
+    queries = (cen[rng.integers(0, nlist, nq)] + 0.3 * rng.standard_normal((nq, dim))).astype(np.float32)
+    queries[::7] = cen[rng.integers(0, nlist // 4, len(queries[::7]))]  # exactly on a twin
+    for nprobe in (1, 16, 100, min(nlist, 1024)):  # nprobe is limited to 1024
+        lists, d = gx.probe(queries, nprobe)
+        for q in range(nq):
+            ol, od = ox.probes(queries[q], nprobe)
+            assert np.array_equal(d[q], od), (nprobe, q)
+            assert np.array_equal(lists[q], ol), (nprobe, q)
+
+
 @pytest.mark.parametrize("nprobe,k", [(1, 10), (8, 10), (16, 1), (16, 64), (16, 65), (16, 100),
                                       (64, 10), (5, 256), (3, 1000)])
 def test_batch_search_parity(small_ivfpq, nprobe, k):
