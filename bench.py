@@ -195,6 +195,8 @@ def bench_ivfpq(args, w, base, queries):
     log(f"[bench] GPU build (k-means {nlist}, PQ {M}x256, encode) in {time.time() - t:.1f}s")
     index.set_nprobe(nprobe)
     index.set_coarse_mode({"auto": 0, "exact": 1, "screen": 2}[args.coarse])
+    mode = {"auto": 0, "exact": 1, "screen": 2}[args.ivfpq_mode]
+    index.set_search_mode(mode)
     r = Runner(args, queries, k)
     nq = r.nq
 
@@ -217,6 +219,24 @@ def bench_ivfpq(args, w, base, queries):
 
     coarse_ms, scan_ms = kernel_times()
     exact_ids = r.ids().copy()
+    path = index.last_search_path()
+    fallbacks, cands = index.last_screen_stats(r.sptr)
+    extra = {}
+    if path == 2:
+        log(f"[bench] path 2 (fp16 screening): {fallbacks} of {nq} queries rescanned exactly, "
+            f"{cands / nq:,.0f} candidates rescored per query")
+        # the table scan on the same batch, for comparison
+        index.set_search_mode(1)
+        table_ms = r.timed_loop(step, sync)
+        _, table_scan_ms = kernel_times()
+        table_same = agreement(r.ids(), exact_ids, k)
+        index.set_search_mode(mode)
+        step()
+        sync()
+        log(f"[bench] table scan: {table_ms:.3f} ms/step, {nq / table_ms * 1e3:,.0f} QPS, scan "
+            f"{table_scan_ms:.3f} ms; id agreement with the screened path {table_same:.6f}")
+        extra["table_scan"] = {"value": round(nq / table_ms * 1e3, 1), "ms_per_step": round(table_ms, 4),
+                               "scan_ms": round(table_scan_ms, 4), "id_agreement": round(table_same, 6)}
 
     # the opt-in fast LUT mode, timed the same way (distances within ~1e-6)
     index.set_lut_mode(LUT_FAST)
@@ -236,16 +256,33 @@ def bench_ivfpq(args, w, base, queries):
     achieved = code_bytes / (scan_ms / 1e3) / 1e9
     log(f"[bench] coarse {coarse_ms:.3f} ms, scan {scan_ms:.3f} ms; {scanned / nq:,.0f} codes "
         f"per query; {code_bytes / 1e9:.3f} GB of codes -> {achieved:,.0f} GB/s")
-    dsub = base.shape[1] // M
-    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": read_traffic(f"ivfpq_scan_{args.workload_tag}_traffic.txt"),
-            "kernel": f"ivfpq_scan_kernel<{M},{dsub},...>", "kernel_ms": round(scan_ms, 4),
-            "algorithmic_bytes": code_bytes, "coarse_ms": round(coarse_ms, 4)}
-    extra = {"fast_lut": {"value": round(nq / fast_ms * 1e3, 1), "ms_per_step": round(fast_ms, 4),
-                          "scan_ms": round(fast_scan_ms, 4),
-                          "achieved_gbs": round(code_bytes / (fast_scan_ms / 1e3) / 1e9, 1),
-                          "id_agreement_with_exact": round(fast_agree, 6)}}
+    dim = base.shape[1]
+    dsub = dim // M
+    if path == 2:
+        # screening: 2 * D16 flops per (query, code) of the probes after the first
+        d16 = (dim + 15) // 16 * 16
+        screened = scanned - int(sizes[lists[:, 0]].sum())
+        flops = 2 * d16 * screened
+        tflops = flops / (scan_ms / 1e3) / 1e12
+        log(f"[bench] screening {screened / nq:,.0f} codes per query x {d16} dims: "
+            f"{flops / 1e12:.1f} TFLOP in the scan stage -> {tflops:,.1f} TFLOP/s")
+        roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / FP16_PEAK_TFLOPS, 4),
+                "traffic": read_traffic(f"ivfpq_screen_{args.workload_tag}_traffic.txt"),
+                "kernel": "pq16_screen_kernel + first-list scan + rescore", "kernel_ms": round(scan_ms, 4),
+                "algorithmic_flops": flops, "adc_code_bytes_per_s": round(achieved * 1e9, 1),
+                "coarse_ms": round(coarse_ms, 4), "fallbacks": fallbacks,
+                "candidates_per_query": round(cands / nq, 1)}
+    else:
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": read_traffic(f"ivfpq_scan_{args.workload_tag}_traffic.txt"),
+                "kernel": f"ivfpq_scan_kernel<{M},{dsub},...>", "kernel_ms": round(scan_ms, 4),
+                "algorithmic_bytes": code_bytes, "coarse_ms": round(coarse_ms, 4)}
+    extra["fast_lut"] = {"value": round(nq / fast_ms * 1e3, 1), "ms_per_step": round(fast_ms, 4),
+                         "scan_ms": round(fast_scan_ms, 4),
+                         "achieved_gbs": round(code_bytes / (fast_scan_ms / 1e3) / 1e9, 1),
+                         "id_agreement_with_exact": round(fast_agree, 6)}
 
     cpu = None
     if not args.no_cpu:
@@ -394,6 +431,8 @@ def main():
                     help="IVF scan strategy (IVFIndex.set_search_mode)")
     ap.add_argument("--bf-mode", default="auto", choices=["auto", "exact", "screen", "screen_f32"],
                     help="brute-force search strategy (BruteForceIndex.set_search_mode)")
+    ap.add_argument("--ivfpq-mode", default="auto", choices=["auto", "exact", "screen"],
+                    help="IVF-PQ scan: auto (fp16 screening for large batches), table scan, or screening")
     ap.add_argument("--coarse", default="auto", choices=["auto", "exact", "screen"],
                     help="coarse selection strategy of the IVF indexes (same probes)")
     ap.add_argument("--calibrate-copy", action="store_true",

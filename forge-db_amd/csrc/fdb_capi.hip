@@ -196,6 +196,26 @@ fdb_status fdb_ivfpq_set_coarse_mode(fdb_ivfpq* h, uint32_t mode) {
   });
 }
 
+fdb_status fdb_ivfpq_set_search_mode(fdb_ivfpq* h, uint32_t mode) {
+  return guarded([&] {
+    if (!H(h)->set_search_mode((int)mode)) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown search mode");
+  });
+}
+
+fdb_status fdb_ivfpq_last_screen_stats(fdb_ivfpq* h, void* stream, uint64_t* fallbacks, uint64_t* candidates) {
+  return guarded([&] {
+    if (!fallbacks || !candidates) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    H(h)->last_screen_stats(*fallbacks, *candidates, (hipStream_t)stream);
+  });
+}
+
+fdb_status fdb_ivfpq_last_search_path(fdb_ivfpq* h, uint32_t* out) {
+  return guarded([&] {
+    if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    *out = (uint32_t)H(h)->last_search_path();
+  });
+}
+
 fdb_status fdb_ivfpq_describe(const fdb_ivfpq* h, fdb_ivfpq_desc* out) {
   return guarded([&] {
     if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");

@@ -260,6 +260,7 @@ void IvfPqIndex::upload_lists() {
   if (host_.has_originals && !host_.originals.empty())
     originals_.upload(host_.originals.data(), host_.originals.size(), stream_);
   live_dirty_ = true;
+  pq16_dirty_ = true;
   FDB_HIP(hipStreamSynchronize(stream_));
 }
 
@@ -278,6 +279,14 @@ const uint32_t* IvfPqIndex::live_bitmap() {
     live_dirty_ = false;
   }
   return live_.p;
+}
+
+void IvfPqIndex::last_screen_stats(uint64_t& fallbacks, uint64_t& candidates, hipStream_t s) {
+  std::lock_guard<std::mutex> g(mu_);
+  fallbacks = candidates = 0;
+  if (path_ != 2) return;
+  FDB_HIP(hipStreamSynchronize(s ? s : stream_));
+  pq16s_.read_stats(fallbacks, candidates, s ? s : stream_);
 }
 
 void IvfPqIndex::throw_if_nan() {
@@ -514,7 +523,54 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
     a.out_pos = nullptr;
     a.out_counts = d_counts;
   }
-  FDB_HIP(launch_ivfpq_scan(a, s));
+  // fp16 screening with exact rescoring (same results; fdb_ivfpq16.hpp):
+  // plain exact-table batches over at least two lists
+  const int smode = search_mode_.load(std::memory_order_relaxed);
+  const uint64_t scanned = host_.nlist ? host_.ids.size() * np / host_.nlist : 0;
+  bool screen = smode != 1 && !rerank && !trunc && live == nullptr && a.lut_mode == 0 && np >= 2 &&
+                host_.M * host_.dsub <= 256 && (smode == 2 || nq * scanned >= kPq16MinWork);
+  if (screen && pq16_dirty_) {
+    pq16_.build(codebooks_.p, codes_.p, off_.p, host_.offsets, host_.nlist, (int)host_.M, (int)host_.dsub, s);
+    pq16_dirty_ = false;
+  }
+  screen = screen && pq16_.ok;
+  path_ = screen ? 2 : 0;
+  if (screen) {
+    pq16s_.reset_stats(s);
+    const uint64_t sl = std::min<uint64_t>(nq, Pq16Searcher::slice((int)k));
+    const uint64_t D = host_.dim;
+    for (uint64_t q0 = 0; q0 < nq; q0 += sl) {
+      const uint64_t m = std::min<uint64_t>(sl, nq - q0);
+      Pq16SearchArgs sa{};
+      sa.queries = d_qs + q0 * D;
+      sa.nq = m;
+      sa.probes = probes_.p + q0 * np;
+      sa.np = (int)np;
+      sa.centroids = centroids_.p;
+      sa.codebooks = codebooks_.p;
+      sa.codes = codes_.p;
+      sa.ids = ids_.p;
+      sa.list_off = off_.p;
+      sa.k = (int)k;
+      sa.order = order;
+      sa.out_ids = d_ids + q0 * k;
+      sa.out_d = d_dists + q0 * k;
+      sa.out_counts = d_counts + q0;
+      pq16s_.search(pq16_, sa, s);
+      // the queries screening did not settle: the exact scan
+      IvfPqScanArgs af = a;
+      af.queries = sa.queries;
+      af.nq = m;
+      af.probes = sa.probes;
+      af.out_ids = sa.out_ids;
+      af.out_dists = sa.out_d;
+      af.out_counts = sa.out_counts;
+      af.flags = pq16s_.flags();
+      FDB_HIP(launch_ivfpq_scan(af, s));
+    }
+  } else {
+    FDB_HIP(launch_ivfpq_scan(a, s));
+  }
   if (rerank)
     FDB_HIP(launch_rerank(d_qs, nq, (int)host_.dim, originals_.p, ids_.p, cand_pos_.p, cand_cnt_.p,
                           (uint32_t)fetch, k, d_ids, d_dists, d_counts, s));

@@ -10,6 +10,7 @@
 #include "fdb_flat.hpp"
 #include "fdb_format.hpp"
 #include "fdb_host.hpp"
+#include "fdb_ivfpq16.hpp"
 
 namespace fdb {
 
@@ -42,6 +43,22 @@ class IvfPqIndex {
   }
 
   void enable_reranking(const float* vectors_list_order, uint64_t factor);
+
+  // 0 = automatic (fp16 screening with exact rescoring for large plain
+  // batches, fdb_ivfpq16.hpp), 1 = exact scan only, 2 = screening wherever
+  // it applies; the results are the same
+  bool set_search_mode(int m) {
+    if (m < 0 || m > 2) return false;
+    search_mode_.store(m, std::memory_order_relaxed);
+    return true;
+  }
+  // the last batch: 2 = screened, 0 = exact scan; queries it rescanned
+  // exactly and candidates it rescored
+  int last_search_path() {
+    std::lock_guard<std::mutex> g(mu_);
+    return path_;
+  }
+  void last_screen_stats(uint64_t& fallbacks, uint64_t& candidates, hipStream_t s);
 
   // single query with search() semantics; returns count
   uint32_t search(const float* q, uint32_t k, uint64_t* ids, float* dists);
@@ -94,6 +111,9 @@ class IvfPqIndex {
   IvfPqArtifacts host_;
   std::atomic<uint64_t> nprobe_{1};
   std::atomic<int> lut_mode_{0};
+  std::atomic<int> search_mode_{0};
+  // automatic screening from this many scanned codes per batch
+  static constexpr uint64_t kPq16MinWork = 1ull << 26;
   hipStream_t stream_ = nullptr;
   std::mutex mu_;
 
@@ -119,6 +139,13 @@ class IvfPqIndex {
   DevBuf<int> err_;
   DevBuf<uint8_t> codes_out_;
   hipEvent_t ev_[3] = {nullptr, nullptr, nullptr};
+
+  // screening: the decoded lists (rebuilt after the lists change) and its
+  // scratch
+  Pq16Lists pq16_;
+  bool pq16_dirty_ = true;
+  Pq16Searcher pq16s_;
+  int path_ = 0;
 };
 
 // Seeded k-means over n host rows [n][dim] (KMeans::fit_raw, kmeans.rs:87-193):

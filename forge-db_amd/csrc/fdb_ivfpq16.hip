@@ -1,0 +1,1203 @@
+// IVF-PQ screening on the matrix cores with exact rescoring; the method and
+// its bound are described in fdb_ivfpq16.hpp.
+//
+// pq16_decode_kernel   decoded residuals (codewords of each code, pq.rs:114-139
+//                      inverted) to fp16 MFMA blocks, per list
+// pq16_norms_kernel    |x^|^2 per code and the largest per list
+// pq16_count/offsets/scatter_kernel
+//                      the probed (query, probe) pairs grouped by list
+// pq16_screen_kernel   fp16 products of residuals and codes, threshold test,
+//                      candidate append
+// pq16_rescore_kernel  exact table distances of the candidates in the
+//                      reference's order (pq.rs:149-189 entries, :218-245 or
+//                      :318-485 sums) and the final top k
+#include "fdb_ivfpq16.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "fdb_device.hpp"
+
+namespace fdb {
+
+namespace {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // 8 halves as a native vector
+
+constexpr int kT = 256;
+constexpr int kTileQ = 128;  // (query, probe) pairs per screening workgroup: 4 waves x 32
+
+uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+// WaveTopK registers for k: ceil(k / 64) rounded up to a power of two
+int list_regs(int k) {
+  int r = (k + 63) / 64, p = 1;
+  while (p < r) p <<= 1;
+  return p;
+}
+
+__global__ void pq16_fill_u32(uint32_t* __restrict__ p, uint64_t n, uint32_t v) {
+  for (uint64_t i = (uint64_t)blockIdx.x * kT + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kT) p[i] = v;
+}
+
+// stats[0]: bits of the largest |codebook component| (non-finite values
+// compare above every finite one).  Grid-stride, one atomic per wave.
+__global__ __launch_bounds__(kT) void pq16_cb_stats_kernel(const float* __restrict__ cb, uint64_t n,
+                                                           uint32_t* __restrict__ stats) {
+  uint32_t m = 0;
+  for (uint64_t i = (uint64_t)blockIdx.x * kT + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kT)
+    m = max(m, __float_as_uint(cb[i]) & 0x7FFFFFFFu);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off));
+  if ((threadIdx.x & 63) == 0) atomicMax(&stats[0], m);
+}
+
+// The list owning block B: the largest p < nlist with bo[p] <= B (lists
+// without blocks share their successor's offset).
+__device__ __forceinline__ uint32_t owner(const uint32_t* __restrict__ off, uint32_t nlist, uint32_t B) {
+  uint32_t lo = 0, hi = nlist;  // off[lo] <= B < off[hi]
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (off[mid] <= B) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// Codewords padded to ds4 = dsub rounded up to 4 floats (zeros after).
+__global__ __launch_bounds__(kT) void pq16_pad_cb_kernel(const float* __restrict__ cb, uint64_t nword, int dsub,
+                                                         int ds4, float* __restrict__ out) {
+  const uint64_t e = (uint64_t)blockIdx.x * kT + threadIdx.x;
+  if (e >= nword * ds4) return;
+  const uint64_t w = e / ds4;
+  const int i = (int)(e - w * ds4);
+  out[e] = i < dsub ? cb[w * dsub + i] : 0.0f;
+}
+
+// One workgroup (64*KC threads) per block; thread (kc, lane) writes the 8
+// halves of its lane for k-chunk kc.
+__global__ void pq16_decode_kernel(const float* __restrict__ cb, const uint8_t* __restrict__ codes,
+                                   const uint32_t* __restrict__ list_off, const uint32_t* __restrict__ bo,
+                                   uint32_t nlist, int M, int dsub, int KC, float scale,
+                                   uint4* __restrict__ out) {
+  const uint32_t B = blockIdx.x;
+  const uint32_t p = owner(bo, nlist, B);
+  const int kc = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const uint32_t row = (B - bo[p]) * 32 + (lane & 31);
+  const uint32_t len = list_off[p + 1] - list_off[p];
+  const bool valid = row < len;
+  const uint64_t i = (uint64_t)list_off[p] + row;
+  const int D = M * dsub;
+  _Float16 h[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int d = kc * 16 + 8 * (lane >> 5) + t;
+    float v = 0.0f;
+    if (valid && d < D) {
+      const int m = d / dsub;
+      const int e = d - m * dsub;
+      v = cb[((uint64_t)m * 256 + codes[i * M + m]) * dsub + e] * scale;
+    }
+    h[t] = (_Float16)v;
+  }
+  uint4 w;
+  w.x = (uint32_t)__builtin_bit_cast(uint16_t, h[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[1]) << 16);
+  w.y = (uint32_t)__builtin_bit_cast(uint16_t, h[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[3]) << 16);
+  w.z = (uint32_t)__builtin_bit_cast(uint16_t, h[4]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[5]) << 16);
+  w.w = (uint32_t)__builtin_bit_cast(uint16_t, h[6]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[7]) << 16);
+  out[((uint64_t)B * KC + kc) * 64 + lane] = w;
+}
+
+// Thread per padded code slot: |x^|^2 in fp32 (FMA chain in dimension
+// order; any order is within the bound's gamma_D) and the list maximum.
+__global__ __launch_bounds__(kT) void pq16_norms_kernel(const float* __restrict__ cb,
+                                                        const uint8_t* __restrict__ codes,
+                                                        const uint32_t* __restrict__ list_off,
+                                                        const uint32_t* __restrict__ bo, uint32_t nlist,
+                                                        uint64_t nslots, int M, int dsub,
+                                                        float* __restrict__ xnb, uint32_t* __restrict__ xmax2) {
+  const uint64_t slot = (uint64_t)blockIdx.x * kT + threadIdx.x;
+  if (slot >= nslots) return;
+  const uint32_t B = (uint32_t)(slot >> 5);
+  const uint32_t p = owner(bo, nlist, B);
+  const uint32_t row = (B - bo[p]) * 32 + (uint32_t)(slot & 31);
+  const uint32_t len = list_off[p + 1] - list_off[p];
+  float s = 0.0f;
+  if (row < len) {
+    const uint64_t i = (uint64_t)list_off[p] + row;
+    for (int m = 0; m < M; ++m) {
+      const float* __restrict__ c = cb + ((uint64_t)m * 256 + codes[i * M + m]) * dsub;
+      for (int e = 0; e < dsub; ++e) s = __builtin_fmaf(c[e], c[e], s);
+    }
+    atomicMax(&xmax2[p], __float_as_uint(s));
+  }
+  xnb[slot] = s;
+}
+
+// ---- (query, probe) pairs by list ------------------------------------------
+//
+// A counting sort without global atomics: workgroup w takes pairs
+// [w*chunk, (w+1)*chunk) of the [nq][np] probe array, counts them per list
+// in LDS and writes its row H[w][list]; pq16_offsets_kernel turns the rows
+// into each list's range and each (w, list) base; the scatter recounts in
+// LDS and places every pair at base + its LDS slot.  A pair (q, j) takes
+// part when its list is valid and j < jlim[q] (jlim null: every probe).
+
+constexpr uint32_t kHistMax = 8192;  // lists counted in LDS (32 KiB)
+constexpr int kSortWG = 32;          // workgroups of the counting sort (at most)
+constexpr uint32_t kCB = 64;         // blocks of 32 codes per screening tile
+constexpr int kSlots = 8;            // candidate slots per lane in LDS
+
+struct PairSet {
+  const int32_t* probes;
+  uint64_t nq;
+  int np;
+  const uint32_t* jlim;
+  uint32_t nlist;
+  uint64_t chunk;  // pairs per sorting workgroup
+};
+
+// (pairs of a slice number below 2^32)
+__device__ __forceinline__ bool pair_list(const PairSet& s, uint32_t e, uint32_t& p) {
+  const uint32_t q = e / (uint32_t)s.np;
+  const uint32_t j = e - q * (uint32_t)s.np;
+  if (s.jlim && j >= s.jlim[q]) return false;
+  const int32_t v = s.probes[e];
+  if (v < 0 || (uint32_t)v >= s.nlist) return false;
+  p = (uint32_t)v;
+  return true;
+}
+
+__global__ __launch_bounds__(kT) void pq16_count_kernel(PairSet s, uint32_t* __restrict__ H) {
+  __shared__ uint32_t hist[kHistMax];
+  const uint32_t w = blockIdx.x;
+  for (uint32_t i = threadIdx.x; i < s.nlist; i += kT) hist[i] = 0;
+  __syncthreads();
+  const uint32_t n = (uint32_t)(s.nq * (uint64_t)s.np);
+  const uint32_t e1 = (uint32_t)min((uint64_t)n, (w + 1) * s.chunk);
+  for (uint32_t e = (uint32_t)(w * s.chunk) + threadIdx.x; e < e1; e += kT) {
+    uint32_t p;
+    if (pair_list(s, e, p)) atomicAdd(&hist[p], 1u);
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < s.nlist; i += kT) H[(uint64_t)w * s.nlist + i] = hist[i];
+}
+
+// One workgroup of 1024 threads.  cnt_p = sum over w of H[w][p]; qoff =
+// exclusive prefix of cnt; tiles_p = ceil(cnt_p / kTileQ) * ceil(min(nb_p,
+// blim) / kCB) (nb_p = bo[p+1] - bo[p]), toff = their exclusive prefix; both
+// totals at [nlist].  H[w][p] is replaced by the pair base of (w, p).
+__global__ __launch_bounds__(1024) void pq16_offsets_kernel(uint32_t* __restrict__ H, uint32_t G, uint32_t nlist,
+                                                            const uint32_t* __restrict__ bo, uint32_t blim,
+                                                            uint32_t* __restrict__ qoff,
+                                                            uint32_t* __restrict__ toff) {
+  __shared__ uint32_t wq[16], wt[16];
+  __shared__ uint32_t carry[2];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  if (tid == 0) carry[0] = carry[1] = 0;
+  __syncthreads();
+  for (uint32_t base = 0; base < nlist; base += 1024) {
+    const uint32_t i = base + tid;
+    uint32_t c = 0, t = 0;
+    if (i < nlist) {
+#pragma unroll 4
+      for (uint32_t w = 0; w < G; ++w) c += H[(uint64_t)w * nlist + i];
+      const uint32_t nb = min(bo[i + 1] - bo[i], blim);
+      t = (c + kTileQ - 1) / kTileQ * ((nb + kCB - 1) / kCB);
+    }
+    uint32_t sc = c, st = t;  // inclusive wave scans
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t uc = (uint32_t)__shfl_up((int)sc, off);
+      const uint32_t ut = (uint32_t)__shfl_up((int)st, off);
+      if (lane >= off) {
+        sc += uc;
+        st += ut;
+      }
+    }
+    if (lane == 63) {
+      wq[wave] = sc;
+      wt[wave] = st;
+    }
+    __syncthreads();
+    uint32_t pq = carry[0], pt = carry[1];
+    for (int w = 0; w < wave; ++w) {
+      pq += wq[w];
+      pt += wt[w];
+    }
+    if (i < nlist) {
+      uint32_t run = pq + sc - c;
+      qoff[i] = run;
+      toff[i] = pt + st - t;
+      for (uint32_t w = 0; w < G; ++w) {
+        const uint32_t h = H[(uint64_t)w * nlist + i];
+        H[(uint64_t)w * nlist + i] = run;
+        run += h;
+      }
+    }
+    __syncthreads();
+    if (tid == 1023) {
+      carry[0] = pq + sc;
+      carry[1] = pt + st;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    qoff[nlist] = carry[0];
+    toff[nlist] = carry[1];
+  }
+}
+
+__global__ __launch_bounds__(kT) void pq16_scatter_kernel(PairSet s, const uint32_t* __restrict__ base,
+                                                          uint2* __restrict__ qlist) {
+  __shared__ uint32_t hist[kHistMax];
+  const uint32_t w = blockIdx.x;
+  for (uint32_t i = threadIdx.x; i < s.nlist; i += kT) hist[i] = 0;
+  __syncthreads();
+  const uint32_t n = (uint32_t)(s.nq * (uint64_t)s.np);
+  const uint32_t e1 = (uint32_t)min((uint64_t)n, (w + 1) * s.chunk);
+  for (uint32_t e = (uint32_t)(w * s.chunk) + threadIdx.x; e < e1; e += kT) {
+    uint32_t p;
+    if (pair_list(s, e, p)) {
+      const uint32_t slot = atomicAdd(&hist[p], 1u);
+      const uint32_t q = e / (uint32_t)s.np;
+      qlist[base[(uint64_t)w * s.nlist + p] + slot] = make_uint2(q, e - q * (uint32_t)s.np);
+    }
+  }
+}
+
+// Thread per list: the list of each of its tiles (tl [tiles]).
+__global__ __launch_bounds__(kT) void pq16_tiles_kernel(const uint32_t* __restrict__ toff, uint32_t nlist,
+                                                        uint32_t* __restrict__ tl) {
+  const uint32_t p = blockIdx.x * kT + threadIdx.x;
+  if (p >= nlist) return;
+  for (uint32_t t = toff[p]; t < toff[p + 1]; ++t) tl[t] = p;
+}
+
+// Thread per query: the first probes whose lists hold at least k codes
+// (jlim), each one's 32-aligned offset into the query's buffer of screened
+// values (offA [nq][np]; nothing past capA is kept), the buffer entries
+// written (nA, padding included) and the codes among them (nreal).
+__global__ __launch_bounds__(kT) void pq16_plan_kernel(const int32_t* __restrict__ probes, uint64_t nq, int np,
+                                                       uint32_t nlist, const uint32_t* __restrict__ list_off,
+                                                       int k, uint32_t capA, uint32_t* __restrict__ jlim,
+                                                       uint32_t* __restrict__ offA, uint32_t* __restrict__ nA,
+                                                       uint32_t* __restrict__ nreal) {
+  const uint64_t q = (uint64_t)blockIdx.x * kT + threadIdx.x;
+  if (q >= nq) return;
+  uint64_t cum = 0, real = 0;
+  uint32_t J = 0;
+  for (int j = 0; j < np; ++j) {
+    if (real >= (uint64_t)k || cum >= capA) break;
+    const int32_t p = probes[q * np + j];
+    offA[q * np + j] = (uint32_t)cum;
+    J = (uint32_t)j + 1;
+    if (p >= 0 && (uint32_t)p < nlist) {
+      const uint64_t len = list_off[p + 1] - list_off[p];
+      real += std::min<uint64_t>(len, capA - cum);
+      cum += (len + 31) / 32 * 32;
+    }
+  }
+  jlim[q] = J;
+  nA[q] = (uint32_t)std::min<uint64_t>(cum, capA);
+  nreal[q] = (uint32_t)real;
+}
+
+// ---- screening --------------------------------------------------------------
+
+struct ScreenArgs {
+  const float* queries;
+  int D;
+  int vec;  // D = 16 * KC and 16-byte aligned query and centroid rows
+  const float* centroids;
+  const uint32_t* list_off;
+  const uint32_t* bo;
+  const uint4* data;
+  const float* xnb;
+  const uint32_t* xmax2;
+  uint32_t nlist;
+  int np;
+  int xexp;
+  const uint32_t* qoff;
+  const uint32_t* toff;
+  const uint32_t* tl;  // list of each tile
+  const uint2* qlist;
+  uint32_t blim;  // blocks screened per list at most
+  // dense mode: every kept value to bufA[q][offA[q][j] + row] (< capA) and
+  // the pair's bound to epsA[q][j]
+  float* bufA;
+  const uint32_t* offA;
+  float* epsA;
+  uint32_t capA;
+  // threshold mode: codes with s <= dkA[q] + eps become candidates
+  const float* dkA;
+  uint32_t* ccnt;
+  uint2* cand;
+  uint32_t cap;
+  int* force;
+  float c_dot, c_sq, cabs;  // pq16_eps coefficients
+};
+
+// |s - d| <= c_dot*|r|*X' + c_sq*(|r| + X')^2 (+ a floor), X' = X + cabs; see
+// pq16_eps_coeffs for the derivation.
+__device__ __forceinline__ float pq16_eps(float rnorm, float X, const ScreenArgs& a) {
+  const float Xp = X + a.cabs;
+  const float t = rnorm + Xp;
+  return a.c_dot * rnorm * Xp + a.c_sq * t * t + 1e-30f;
+}
+
+// a + b rounded up past the exact sum (a, b >= 0)
+__device__ __forceinline__ float add_up(float a, float b) {
+  const float t = a + b;
+  return t + t * 0x1p-22f;
+}
+
+// Stage loads of blocks bs0 .. bs0+SB-1 (unit u = (block, k-chunk, lane));
+// blocks past the chunk's end (be) re-read its last block, never multiplied.
+template <int KC, int SB, int PER>
+__device__ __forceinline__ void stage_fetch(v4u (&pre)[PER], float4& prex, const v4u* __restrict__ A,
+                                            const float* __restrict__ XN, uint32_t bs0, uint32_t be, int tid) {
+  constexpr int kUnits = SB * KC * 64;
+  if (tid < SB * 8) {  // |x^|^2 of the stage's codes, 4 per thread
+    const uint32_t b = min(bs0 + (uint32_t)(tid >> 3), be - 1);
+    prex = *reinterpret_cast<const float4*>(XN + (uint64_t)b * 32 + 4 * (tid & 7));
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int u = tid + i * kT;
+    if (kUnits % kT == 0 || u < kUnits) {
+      const int bs = u / (KC * 64);
+      const uint32_t b = min(bs0 + (uint32_t)bs, be - 1);
+      pre[i] = A[(uint64_t)b * KC * 64 + (uint32_t)(u - bs * KC * 64)];
+    }
+  }
+}
+
+// Tiles: list p owns toff[p] .. toff[p+1]: ceil(pairs_p / 128) pair tiles
+// (fastest) times ceil(min(blocks_p, blim) / kCB) block chunks; workgroups
+// stride over the tiles.  In a tile, wave w takes pairs [32w, 32w+32): lane
+// l holds pair l%32's residual on dimensions 16kc + 8(l/32) .. +7 as the B
+// operand.  The chunk's blocks go through an LDS stage of SB blocks shared
+// by the four waves, the next stage's loads issued before the current one
+// is multiplied; D[r] is code 8(r/4) + 4(l/32) + r%4 of a block against
+// pair l%32.
+//   Threshold mode: s' = fma(-2^(1-er-xexp), acc, |x^|^2) against
+//   T' = dkA + eps - |r|^2 rounded up: a code left out has s' > T', so its
+//   screened distance exceeds dkA + eps by more than the FMA's rounding,
+//   which eps covers.
+//   Dense mode: s = fma(.., acc, |r|^2 + |x^|^2) of every code is written
+//   to the pair's 32-aligned range of the query's buffer (+inf past the
+//   list's end, nothing past capA), four rows per 16-byte store.
+template <int KC, bool DENSE>
+__global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
+  constexpr int SB = KC <= 2 ? 16 : (KC <= 4 ? 8 : (KC <= 8 ? 4 : 2));  // blocks per stage (<= 32 KiB)
+  constexpr int kUnits = SB * KC * 64;
+  constexpr int kPer = (kUnits + kT - 1) / kT;
+  __shared__ v4u stage[kUnits];
+  __shared__ float4 sxn[SB * 8];
+  // threshold mode: lane-private candidate slots, moved to the query's list
+  // when full and at the end of each tile (one reservation per move)
+  __shared__ uint2 slots[DENSE ? 1 : kT * kSlots];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 31;
+  const int half = lane >> 5;
+  const uint32_t ntiles = a.toff[a.nlist];
+  for (uint32_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    const uint32_t p = a.tl[t];
+    const uint32_t qb = a.qoff[p], qend = a.qoff[p + 1];
+    const uint32_t nqt = (qend - qb + kTileQ - 1) / kTileQ;
+    const uint32_t local = t - a.toff[p];
+    const uint32_t chunk = local / nqt;
+    const uint32_t q0 = qb + (local - chunk * nqt) * kTileQ + (uint32_t)wave * 32;
+    const bool busy = q0 < qend;  // wave-uniform: the wave has pairs
+    const bool qv = busy && q0 + (uint32_t)col < qend;
+    uint32_t q = 0, j = 0;
+    if (qv) {
+      const uint2 e = a.qlist[q0 + col];
+      q = e.x;
+      j = e.y;
+    }
+    const float* __restrict__ qp = a.queries + (uint64_t)q * a.D;
+    const float* __restrict__ cp = a.centroids + (uint64_t)p * a.D;
+    float r[KC][8];
+    float mx = 0.0f, rn = 0.0f;
+    if (a.vec) {  // whole k-chunks, 16-byte aligned rows: 16-byte loads
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+        for (int h4 = 0; h4 < 2; ++h4) {
+          const int d = kc * 16 + 8 * half + 4 * h4;
+          float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = x;
+          if (qv) {
+            x = *reinterpret_cast<const float4*>(qp + d);
+            c = *reinterpret_cast<const float4*>(cp + d);
+          }
+          r[kc][4 * h4] = x.x - c.x;  // the reference's residual
+          r[kc][4 * h4 + 1] = x.y - c.y;
+          r[kc][4 * h4 + 2] = x.z - c.z;
+          r[kc][4 * h4 + 3] = x.w - c.w;
+        }
+    } else {
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int d = kc * 16 + 8 * half + i;
+          r[kc][i] = (qv && d < a.D) ? qp[d] - cp[d] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        mx = fmaxf(mx, __builtin_fabsf(r[kc][i]));
+        rn = __builtin_fmaf(r[kc][i], r[kc][i], rn);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    rn = rn + __shfl_xor(rn, 32);
+    int er = 0;
+    if (mx > 0.0f) {
+      int E;
+      (void)frexpf(mx, &E);
+      er = 13 - E;  // mx * 2^er in [2^12, 2^13)
+    }
+    const bool bad = !(rn <= 3.0e38f) || er > 100 || er < -100;
+    const bool act = qv && !bad;
+    if (qv && bad && half == 0) atomicOr(&a.force[q], 1);
+    float Tp = -f_inf();  // threshold mode: no append
+    uint32_t o = 0;       // dense mode: buffer offset of the pair
+    if (act) {
+      const float rnorm = sqrtf(rn) * (1.0f + 0x1p-16f);
+      const float X = sqrtf(__uint_as_float(a.xmax2[p])) * (1.0f + 0x1p-16f);
+      const float eps = pq16_eps(rnorm, X, a);
+      if constexpr (DENSE) {
+        o = a.offA[(uint64_t)q * a.np + j];
+        if (half == 0 && chunk == 0) a.epsA[(uint64_t)q * a.np + j] = eps;
+      } else {
+        const float f = add_up(a.dkA[q], eps) - rn;
+        Tp = f + __builtin_fabsf(f) * 0x1p-22f;
+      }
+    }
+    const float sc = ldexpf(1.0f, er);
+    v8h bq[KC];
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) bq[kc][i] = (_Float16)(r[kc][i] * sc);
+    const float cneg = -ldexpf(1.0f, 1 - er - a.xexp);
+    const uint32_t b0 = a.bo[p];
+    const uint32_t nb = min(a.bo[p + 1] - b0, a.blim);
+    const uint32_t bb = chunk * kCB;
+    const uint32_t be = min(nb, bb + kCB);
+    const uint32_t start = a.list_off[p];
+    const uint32_t len = a.list_off[p + 1] - start;
+    const v4u* __restrict__ A = reinterpret_cast<const v4u*>(a.data) + (uint64_t)b0 * KC * 64;
+    const float* __restrict__ XN = a.xnb + (uint64_t)b0 * 32;
+    // stage loads: unit u = (block bs, k-chunk, lane); blocks past the
+    // chunk's end re-read its last block (never multiplied)
+    int nslot = 0;
+    auto move = [&](int n) {
+      const uint32_t pos = atomicAdd(&a.ccnt[q], (uint32_t)n);
+      uint2* __restrict__ out = a.cand + (uint64_t)q * a.cap;
+      for (int i = 0; i < n; ++i)
+        if (pos + (uint32_t)i < a.cap) out[pos + i] = slots[tid * kSlots + i];
+    };
+    v4u pre[kPer];
+    float4 prex = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    stage_fetch<KC, SB, kPer>(pre, prex, A, XN, bb, be, tid);
+    for (uint32_t bs0 = bb; bs0 < be; bs0 += SB) {
+      __syncthreads();  // the previous stage (or tile) is consumed
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int u = tid + i * kT;
+        if (kUnits % kT == 0 || u < kUnits) stage[u] = pre[i];
+      }
+      if (tid < SB * 8) sxn[tid] = prex;
+      __syncthreads();
+      if (bs0 + SB < be) stage_fetch<KC, SB, kPer>(pre, prex, A, XN, bs0 + SB, be, tid);
+      if (!busy) continue;
+#pragma unroll 1
+      for (int bs = 0; bs < SB; ++bs) {
+        const uint32_t b = bs0 + (uint32_t)bs;
+        if (b >= be) break;
+        v16f acc = {};
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, stage[(bs * KC + kc) * 64 + lane]),
+                                                       bq[kc], acc, 0, 0, 0);
+        const uint32_t rowb = b * 32 + 4 * half;
+        float xs[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 x4 = sxn[bs * 8 + 2 * g + half];
+          xs[4 * g] = x4.x;
+          xs[4 * g + 1] = x4.y;
+          xs[4 * g + 2] = x4.z;
+          xs[4 * g + 3] = x4.w;
+        }
+        if constexpr (DENSE) {
+          if (act) {
+            const float base = rn;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const uint32_t row = rowb + 8 * g;
+              if (o + row < a.capA) {
+                float4 v;
+                v.x = row + 0 < len ? __builtin_fmaf(cneg, acc[4 * g + 0], base + xs[4 * g + 0]) : f_inf();
+                v.y = row + 1 < len ? __builtin_fmaf(cneg, acc[4 * g + 1], base + xs[4 * g + 1]) : f_inf();
+                v.z = row + 2 < len ? __builtin_fmaf(cneg, acc[4 * g + 2], base + xs[4 * g + 2]) : f_inf();
+                v.w = row + 3 < len ? __builtin_fmaf(cneg, acc[4 * g + 3], base + xs[4 * g + 3]) : f_inf();
+                *reinterpret_cast<float4*>(a.bufA + (uint64_t)q * a.capA + o + row) = v;
+              }
+            }
+          }
+        } else {
+          float sv[16];
+          bool any = false;
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) {
+            sv[rr] = __builtin_fmaf(cneg, acc[rr], xs[rr]);
+            any = any || sv[rr] <= Tp;
+          }
+          if (__ballot(any) != 0) {
+#pragma unroll
+            for (int rr = 0; rr < 16; ++rr) {
+              const uint32_t row = rowb + 8 * (rr >> 2) + (rr & 3);
+              if (sv[rr] <= Tp && row < len) {
+                slots[tid * kSlots + nslot] = make_uint2(start + row, j);
+                if (++nslot == kSlots) {
+                  move(kSlots);
+                  nslot = 0;
+                }
+              }
+            }
+          }
+        }
+      }
+    }
+    if constexpr (!DENSE) {
+      if (nslot > 0) move(nslot);
+    }
+  }
+}
+
+// One wave per query: dkA = (k-th smallest kept screened value) + the
+// largest bound among its first lists, rounded up: at least k codes of
+// those lists have reference distance <= dkA, so the final k-th does too.
+// +inf when fewer than k codes were kept (the padding holds +inf).
+template <int R>
+__global__ __launch_bounds__(64) void pq16_select_kernel(const float* __restrict__ bufA, uint32_t capA,
+                                                         const uint32_t* __restrict__ nA,
+                                                         const uint32_t* __restrict__ nreal,
+                                                         const uint32_t* __restrict__ jlim,
+                                                         const float* __restrict__ epsA, int np, int k,
+                                                         float* __restrict__ dkA) {
+  __shared__ uint2 queue[64];
+  const uint64_t q = blockIdx.x;
+  const int lane = threadIdx.x;
+  const uint32_t n = nA[q];
+  if (nreal[q] < (uint32_t)k) {
+    if (lane == 0) dkA[q] = f_inf();
+    return;
+  }
+  WaveTopK<R> tk;
+  tk.init(k);
+  int qn = 0;
+  const float4* __restrict__ v = reinterpret_cast<const float4*>(bufA + q * capA);
+  const uint32_t n4 = (n + 3) / 4;  // n is a multiple of 32 or capA
+  for (uint32_t i0 = 0; i0 < n4; i0 += 256) {
+    float4 w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t i = i0 + (uint32_t)(u * 64 + lane);
+      w[u] = i < n4 ? v[i] : make_float4(f_inf(), f_inf(), f_inf(), f_inf());
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t i = 4 * (i0 + (uint32_t)(u * 64 + lane));
+      tk.offer_queued(w[u].x, i, w[u].x < f_inf(), queue, qn);
+      tk.offer_queued(w[u].y, i + 1, w[u].y < f_inf(), queue, qn);
+      tk.offer_queued(w[u].z, i + 2, w[u].z < f_inf(), queue, qn);
+      tk.offer_queued(w[u].w, i + 3, w[u].w < f_inf(), queue, qn);
+    }
+  }
+  tk.flush(queue, qn);
+  float em = 0.0f;
+  for (uint32_t j = 0; j < jlim[q]; ++j) em = fmaxf(em, epsA[q * np + j]);
+  if (lane == 0) dkA[q] = add_up(tk.tau, em);
+}
+
+// ---- exact rescoring ----------------------------------------------------------
+
+// One table entry of the reference (l2sq_ref order on r - cb, r = q - c)
+// computed from the query, centroid and codeword rows of one subspace.
+__device__ __forceinline__ float pq_entry(const float* __restrict__ qs, const float* __restrict__ cen,
+                                          const float* __restrict__ cw, int dsub) {
+  const int nb = dsub / 8;
+  float total = 0.0f;
+  if (nb > 0) {
+    float lane[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) lane[l] = 0.0f;
+    for (int i = 0; i < nb; ++i)
+#pragma unroll
+      for (int l = 0; l < 8; ++l) {
+        const float r = qs[8 * i + l] - cen[8 * i + l];
+        const float d = r - cw[8 * i + l];
+        lane[l] = __builtin_fmaf(d, d, lane[l]);
+      }
+    total = lane[0];
+#pragma unroll
+    for (int l = 1; l < 8; ++l) total = total + lane[l];
+  }
+  for (int i = 8 * nb; i < dsub; ++i) {
+    const float r = qs[i] - cen[i];
+    const float d = r - cw[i];
+    total = total + d * d;
+  }
+  return total;
+}
+
+struct RescoreArgs16 {
+  const float* queries;
+  int D, M, dsub;
+  const int32_t* probes;
+  int np;
+  const float* centroids;
+  const float* codebooks;
+  const float* cb4;  // codebooks with codewords padded to a multiple of 4 floats
+  int nlist;
+  int cached;        // residuals of every probe in LDS
+  const uint8_t* codes;
+  const uint64_t* ids;
+  const uint32_t* ccnt;
+  const uint2* cand;
+  uint32_t cap;
+  const int* force;
+  int k, order;
+  uint64_t* out_ids;
+  float* out_d;
+  uint32_t* out_counts;
+  int* flags;
+};
+
+// One table entry from the cached residual row r of the subspace (LDS) and
+// the codeword cw (padded to a multiple of 4 floats): the l2sq_ref order on
+// r - cw.  DS: dsub at compile time (0 = runtime).
+template <int DS>
+__device__ __forceinline__ float entry_cached(const float* __restrict__ r, const float* __restrict__ cw, int dsub) {
+  if constexpr (DS > 0) {
+    constexpr int DS4 = (DS + 3) / 4 * 4;
+    float c[DS4];
+#pragma unroll
+    for (int i = 0; i < DS4 / 4; ++i) {
+      const float4 v = reinterpret_cast<const float4*>(cw)[i];
+      c[4 * i] = v.x;
+      c[4 * i + 1] = v.y;
+      c[4 * i + 2] = v.z;
+      c[4 * i + 3] = v.w;
+    }
+    constexpr int NB = DS / 8;
+    float total = 0.0f;
+    if constexpr (NB > 0) {
+      float lane[8];
+#pragma unroll
+      for (int l = 0; l < 8; ++l) {
+        const float d = r[l] - c[l];
+        lane[l] = __builtin_fmaf(d, d, 0.0f);
+      }
+#pragma unroll
+      for (int i = 1; i < NB; ++i)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+          const float d = r[8 * i + l] - c[8 * i + l];
+          lane[l] = __builtin_fmaf(d, d, lane[l]);
+        }
+      total = lane[0];
+#pragma unroll
+      for (int l = 1; l < 8; ++l) total = total + lane[l];
+    }
+#pragma unroll
+    for (int i = 8 * NB; i < DS; ++i) {
+      const float d = r[i] - c[i];
+      total = total + d * d;
+    }
+    return total;
+  } else {
+    const int nb = dsub / 8;
+    float total = 0.0f;
+    if (nb > 0) {
+      float lane[8];
+#pragma unroll
+      for (int l = 0; l < 8; ++l) lane[l] = 0.0f;
+      for (int i = 0; i < nb; ++i)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+          const float d = r[8 * i + l] - cw[8 * i + l];
+          lane[l] = __builtin_fmaf(d, d, lane[l]);
+        }
+      total = lane[0];
+#pragma unroll
+      for (int l = 1; l < 8; ++l) total = total + lane[l];
+    }
+    for (int i = 8 * nb; i < dsub; ++i) {
+      const float d = r[i] - cw[i];
+      total = total + d * d;
+    }
+    return total;
+  }
+}
+
+// The reference's distance of one code: entries v(m) summed in adc_sum order.
+template <class V>
+__device__ __forceinline__ float adc_order(int M, int order, V v) {
+  if (order == kAdcLanes8) {
+    const int mb = M / 8;
+    float total = 0.0f;
+    if (mb > 0) {
+      float lane[8];
+#pragma unroll
+      for (int l = 0; l < 8; ++l) lane[l] = v(l);
+      for (int b = 1; b < mb; ++b)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) lane[l] = lane[l] + v(8 * b + l);
+      total = lane[0];
+#pragma unroll
+      for (int l = 1; l < 8; ++l) total = total + lane[l];
+    }
+    for (int m = 8 * mb; m < M; ++m) total = total + v(m);
+    return total;
+  }
+  float sum = 0.0f;
+  int m = 0;
+  for (; m + 4 <= M; m += 4) {
+    float t = v(m) + v(m + 1);
+    t = t + v(m + 2);
+    t = t + v(m + 3);
+    sum = sum + t;
+  }
+  for (; m < M; ++m) sum = sum + v(m);
+  return sum;
+}
+
+// Four waves per query: the candidates' reference distances (wave w takes
+// every fourth batch of 64) and the top k (ties: smaller list position, as
+// the table scan), the wave lists merged by wave 0.  The residuals r_j =
+// q - c_(probe j) are computed once into LDS (rc [np][D]) when they fit
+// (cached), else per candidate.  Queries with a residual out of fp16 range
+// or more candidates than slots are flagged for the table scan.
+template <int R, int DS>
+__global__ __launch_bounds__(kT) void pq16_rescore_kernel(RescoreArgs16 a) {
+  extern __shared__ float qs[];  // [D], then rc [np][D] when cached
+  __shared__ uint2 queue[kT / 64][64];
+  __shared__ float md[kT / 64][64 * R];
+  __shared__ uint32_t mk[kT / 64][64 * R];
+  const uint64_t q = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const uint32_t cnt = a.ccnt[q];
+  const bool fall = a.force[q] != 0 || cnt > a.cap;
+  if (tid == 0) a.flags[q] = fall ? 1 : 0;
+  if (fall) return;  // the whole workgroup
+  const int D = a.D;
+  float* rc = qs + D;
+  // a few candidates are cheaper to rescore without the residual cache
+  const bool cached = a.cached && cnt >= 128;
+  for (int d = tid; d < D; d += kT) qs[d] = a.queries[q * D + d];
+  if (cached) {
+    for (int e = tid; e < a.np * D; e += kT) {
+      const int j = e / D;
+      const int d = e - j * D;
+      const int32_t p = a.probes[q * a.np + j];
+      rc[e] = (p >= 0 && p < a.nlist) ? a.queries[q * D + d] - a.centroids[(uint64_t)p * D + d] : 0.0f;
+    }
+  }
+  __syncthreads();
+  WaveTopK<R> tk;
+  tk.init(a.k);
+  int qn = 0;
+  const uint2* __restrict__ cq = a.cand + q * a.cap;
+  const int M = a.M, dsub = DS > 0 ? DS : a.dsub;
+  const int ds4 = (dsub + 3) / 4 * 4;
+  for (uint32_t c0 = (uint32_t)wave * 64; c0 < cnt; c0 += kT) {
+    const uint32_t c = c0 + (uint32_t)lane;
+    uint32_t key = kNoPos;
+    float d = f_inf();
+    if (c < cnt) {
+      const uint2 e = cq[c];
+      key = e.x;
+      const uint8_t* __restrict__ code = a.codes + (uint64_t)key * M;
+      if (cached) {
+        const float* __restrict__ rr = rc + e.y * D;
+        d = adc_order(M, a.order, [&](int m) {
+          return entry_cached<DS>(rr + m * dsub, a.cb4 + ((uint64_t)m * 256 + code[m]) * ds4, dsub);
+        });
+      } else {
+        const float* __restrict__ cen = a.centroids + (uint64_t)a.probes[q * a.np + e.y] * D;
+        d = adc_order(M, a.order, [&](int m) {
+          return pq_entry(qs + m * dsub, cen + m * dsub, a.codebooks + ((uint64_t)m * 256 + code[m]) * dsub,
+                          dsub);
+        });
+      }
+    }
+    tk.offer_queued(d, key, c < cnt, queue[wave], qn);
+  }
+  tk.flush(queue[wave], qn);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    md[wave][r * 64 + lane] = tk.d[r];
+    mk[wave][r * 64 + lane] = tk.p[r];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w = 1; w < kT / 64; ++w)
+#pragma unroll
+    for (int r = 0; r < R; ++r) tk.offer(md[w][r * 64 + lane], mk[w][r * 64 + lane]);
+  uint32_t count = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int s = r * 64 + lane;
+    const bool valid = s < a.k && tk.p[r] != kNoPos;
+    count += (uint32_t)__popcll(__ballot(valid));
+    if (s < a.k) {
+      a.out_ids[q * a.k + s] = valid ? a.ids[tk.p[r]] : ~0ull;
+      a.out_d[q * a.k + s] = valid ? tk.d[r] : f_inf();
+    }
+  }
+  if (lane == 0) a.out_counts[q] = count;
+}
+
+// One workgroup: stat[0] += queries flagged, stat[2..3] += candidates of
+// the others.
+__global__ __launch_bounds__(1024) void pq16_stats_kernel(const int* __restrict__ flags,
+                                                          const uint32_t* __restrict__ ccnt, uint64_t nq,
+                                                          uint32_t* __restrict__ stat) {
+  __shared__ unsigned long long red[2][16];
+  unsigned long long f = 0, c = 0;
+  for (uint64_t q = threadIdx.x; q < nq; q += 1024) {
+    if (flags[q]) f += 1;
+    else c += ccnt[q];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    f += __shfl_xor(f, off);
+    c += __shfl_xor(c, off);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[0][wave] = f;
+    red[1][wave] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 16; ++w) {
+      f += red[0][w];
+      c += red[1][w];
+    }
+    atomicAdd(&stat[0], (uint32_t)f);
+    atomicAdd(reinterpret_cast<unsigned long long*>(&stat[2]), c);
+  }
+}
+
+// Bound coefficients.  With u = 2^-24, uh = 2^-11 and D16 the padded
+// dimension, on components scaled into [2^12, 2^13) (rows: the codebooks'
+// largest component; a query: its residual's):
+//   each converted component is within uh relative plus 2^-26 of that
+//   largest component (flushed fp16 subnormals included), so the scaled
+//   product <r^, x^> is within h' |r| X' of <r, x^>, where
+//   h' = 2uh + uh^2 + 2.002 * 2^-26 sqrt(D16) + 1.002 g2, g2 = 2u D16/(1 - 2u D16)
+//   covers fp32 accumulation in any order (rounded or truncated), and
+//   X' = X + 2^-26 sqrt(D16) cmax for codes of norm <= X;
+//   |r|^2 and |x^|^2 in fp32 are within gamma_D16 (|r| + X)^2 together, the
+//   final add and FMA within 3u (|r| + X')^2, and the reference's own table
+//   distance within gamma_(dsub + M + 2) of the exact value (sums of
+//   non-negative terms).  Everything gets a 1.1 slack factor.
+void pq16_eps_coeffs(int D16, int M, int dsub, float cmax, float& c_dot, float& c_sq, float& cabs) {
+  const double u = std::ldexp(1.0, -24), uh = std::ldexp(1.0, -11);
+  const double g2 = 2.0 * u * D16 / (1.0 - 2.0 * u * D16);
+  const double hp = 2.0 * uh + uh * uh + 2.002 * std::ldexp(1.0, -26) * std::sqrt((double)D16) + 1.002 * g2 +
+                    D16 * std::ldexp(1.0, -52);
+  const double gD = D16 * u / (1.0 - D16 * u);
+  const int na = dsub + M + 2;
+  const double ga = na * u / (1.0 - na * u);
+  c_dot = (float)(1.1 * 2.0 * hp);
+  c_sq = (float)(1.1 * (gD + 3.0 * u + ga));
+  cabs = (float)(1.0001 * std::ldexp(1.0, -26) * std::sqrt((double)D16) * cmax);
+}
+
+}  // namespace
+
+void Pq16Lists::build(const float* d_codebooks, const uint8_t* d_codes, const uint32_t* d_off,
+                      const std::vector<uint64_t>& offsets, uint32_t nl, int m, int ds, hipStream_t s) {
+  ok = false;
+  M = m;
+  dsub = ds;
+  D = M * dsub;
+  KC = (D + 15) / 16;
+  nlist = nl;
+  // B operands beyond 64 registers, or lists beyond the LDS counting sort:
+  // the table scan only
+  if (KC > 16 || nlist == 0 || nlist > kHistMax) return;
+  std::vector<uint32_t> hbo(nlist + 1, 0);
+  uint64_t nbk = 0;
+  max_blocks = 0;
+  for (uint32_t p = 0; p < nlist; ++p) {
+    hbo[p] = (uint32_t)nbk;
+    const uint64_t nb = cdiv(offsets[p + 1] - offsets[p], 32);
+    nbk += nb;
+    max_blocks = std::max(max_blocks, nb);
+  }
+  if (nbk >= 0xFFFFFFFFull) return;
+  hbo[nlist] = (uint32_t)nbk;
+  nblocks = nbk;
+  bo.upload(hbo.data(), hbo.size(), s);
+  stats.reserve(1);
+  hipLaunchKernelGGL(pq16_fill_u32, dim3(1), dim3(kT), 0, s, stats.p, (uint64_t)1, 0u);
+  FDB_HIP(hipGetLastError());
+  const uint64_t ncb = (uint64_t)M * 256 * dsub;
+  hipLaunchKernelGGL(pq16_cb_stats_kernel, dim3((unsigned)std::min<uint64_t>(cdiv(ncb, kT), 1024)), dim3(kT), 0, s,
+                     d_codebooks, ncb, stats.p);
+  FDB_HIP(hipGetLastError());
+  uint32_t mbits = 0;
+  FDB_HIP(hipMemcpyAsync(&mbits, stats.p, 4, hipMemcpyDeviceToHost, s));
+  FDB_HIP(hipStreamSynchronize(s));
+  if (mbits >= 0x7F800000u) return;  // a non-finite codebook component
+  float mxv;
+  std::memcpy(&mxv, &mbits, 4);
+  cmax = mxv;
+  xexp = 0;
+  if (mxv > 0.0f) {
+    int E;
+    (void)std::frexp(mxv, &E);
+    xexp = 13 - E;
+  }
+  if (xexp > 100 || xexp < -100) return;
+  const int ds4 = (dsub + 3) / 4 * 4;
+  cb4.reserve((uint64_t)M * 256 * ds4);
+  hipLaunchKernelGGL(pq16_pad_cb_kernel, dim3((unsigned)cdiv((uint64_t)M * 256 * ds4, kT)), dim3(kT), 0, s,
+                     d_codebooks, (uint64_t)M * 256, dsub, ds4, cb4.p);
+  FDB_HIP(hipGetLastError());
+  data.reserve(std::max<uint64_t>(nblocks * KC * 64, 1));
+  xnb.reserve(std::max<uint64_t>(nblocks * 32, 1));
+  xmax2.reserve(nlist);
+  hipLaunchKernelGGL(pq16_fill_u32, dim3((unsigned)std::min<uint64_t>(cdiv(nlist, kT), 1024)), dim3(kT), 0, s,
+                     xmax2.p, (uint64_t)nlist, 0u);
+  FDB_HIP(hipGetLastError());
+  if (nblocks > 0) {
+    hipLaunchKernelGGL(pq16_decode_kernel, dim3((unsigned)nblocks), dim3(64 * KC), 0, s, d_codebooks, d_codes, d_off,
+                       bo.p, nlist, M, dsub, KC, std::ldexp(1.0f, xexp), data.p);
+    FDB_HIP(hipGetLastError());
+    hipLaunchKernelGGL(pq16_norms_kernel, dim3((unsigned)cdiv(nblocks * 32, kT)), dim3(kT), 0, s, d_codebooks,
+                       d_codes, d_off, bo.p, nlist, nblocks * 32, M, dsub, xnb.p, xmax2.p);
+    FDB_HIP(hipGetLastError());
+  }
+  ok = true;
+}
+
+void Pq16Searcher::reset_stats(hipStream_t s) {
+  stat_.reserve(4);
+  hipLaunchKernelGGL(pq16_fill_u32, dim3(1), dim3(kT), 0, s, stat_.p, (uint64_t)4, 0u);
+  FDB_HIP(hipGetLastError());
+}
+
+void Pq16Searcher::read_stats(uint64_t& fallbacks, uint64_t& candidates, hipStream_t s) {
+  fallbacks = candidates = 0;
+  if (!stat_.p) return;
+  uint32_t v[4] = {0, 0, 0, 0};
+  FDB_HIP(hipMemcpyAsync(v, stat_.p, 16, hipMemcpyDeviceToHost, s));
+  FDB_HIP(hipStreamSynchronize(s));
+  fallbacks = v[0];
+  candidates = (uint64_t)v[2] | ((uint64_t)v[3] << 32);
+}
+
+void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream_t s) {
+  const uint64_t nq = a.nq;
+  if (nq == 0) return;
+  const uint32_t nlist = L.nlist;
+  const int np = a.np;
+  const uint32_t cap = capacity(a.k);
+  const uint64_t npr = nq * (uint64_t)np;
+  if (ncu_ == 0) {
+    int dev = 0, v = 0;
+    FDB_HIP(hipGetDevice(&dev));
+    FDB_HIP(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev));
+    ncu_ = std::max(v, 1);
+  }
+  H_.reserve((uint64_t)kSortWG * nlist);
+  qoff_.reserve(2 * (uint64_t)(nlist + 1));
+  toff_.reserve(2 * (uint64_t)(nlist + 1));
+  qlist_.reserve(2 * std::max<uint64_t>(npr, 1));
+  jlim_.reserve(nq);
+  offA_.reserve(npr);
+  nA_.reserve(nq);
+  nreal_.reserve(nq);
+  epsA_.reserve(npr);
+  const uint32_t capA = cap_first(a.k);
+  bufA_.reserve(nq * capA);
+  dkA_.reserve(nq);
+  ccnt_.reserve(nq);
+  cand_.reserve(nq * cap);
+  force_.reserve(nq);
+  flags_.reserve(nq);
+  if (!stat_.p) reset_stats(s);
+  auto fill = [&](uint32_t* p, uint64_t n) {
+    hipLaunchKernelGGL(pq16_fill_u32, dim3((unsigned)std::min<uint64_t>(std::max<uint64_t>(cdiv(n, kT), 1), 1024)),
+                       dim3(kT), 0, s, p, n, 0u);
+    FDB_HIP(hipGetLastError());
+  };
+  fill(ccnt_.p, nq);
+  fill(reinterpret_cast<uint32_t*>(force_.p), nq);
+  fill(reinterpret_cast<uint32_t*>(epsA_.p), npr);
+  hipLaunchKernelGGL(pq16_plan_kernel, dim3((unsigned)cdiv(nq, kT)), dim3(kT), 0, s, a.probes, nq, np, nlist,
+                     a.list_off, a.k, capA, jlim_.p, offA_.p, nA_.p, nreal_.p);
+  FDB_HIP(hipGetLastError());
+
+  // (query, probe) pairs grouped by list, stage st (0: first lists, 1: all)
+  const uint32_t G = (uint32_t)std::min<uint64_t>(std::max<uint64_t>(cdiv(npr, 8192), 1), kSortWG);
+  const uint64_t chunk = cdiv(npr, G);
+  // tiles of a stage: at most (pairs / 128 + lists) pair tiles per chunk
+  auto tile_bound = [&](uint32_t blim) {
+    return (cdiv(npr, kTileQ) + nlist) * cdiv(std::min<uint64_t>(L.max_blocks, blim), kCB);
+  };
+  const uint64_t tbA = tile_bound(capA / 32), tbB = tile_bound(0xFFFFFFFFu);
+  tl_.reserve(std::max<uint64_t>(tbA + tbB, 1));
+  auto sort_pairs = [&](int st, const uint32_t* jlim, uint32_t blim) {
+    PairSet ps{a.probes, nq, np, jlim, nlist, chunk};
+    uint32_t* qoff = qoff_.p + st * (uint64_t)(nlist + 1);
+    uint32_t* toff = toff_.p + st * (uint64_t)(nlist + 1);
+    uint2* ql = qlist_.p + st * std::max<uint64_t>(npr, 1);
+    hipLaunchKernelGGL(pq16_count_kernel, dim3(G), dim3(kT), 0, s, ps, H_.p);
+    FDB_HIP(hipGetLastError());
+    hipLaunchKernelGGL(pq16_offsets_kernel, dim3(1), dim3(1024), 0, s, H_.p, G, nlist, L.bo.p, blim, qoff, toff);
+    FDB_HIP(hipGetLastError());
+    hipLaunchKernelGGL(pq16_scatter_kernel, dim3(G), dim3(kT), 0, s, ps, H_.p, ql);
+    FDB_HIP(hipGetLastError());
+    hipLaunchKernelGGL(pq16_tiles_kernel, dim3((unsigned)cdiv(nlist, kT)), dim3(kT), 0, s, toff, nlist,
+                       tl_.p + (st ? tbA : 0));
+    FDB_HIP(hipGetLastError());
+  };
+
+  ScreenArgs sa{};
+  sa.queries = a.queries;
+  sa.D = L.D;
+  sa.vec = L.D == 16 * L.KC && (reinterpret_cast<uintptr_t>(a.queries) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(a.centroids) & 15) == 0;
+  sa.centroids = a.centroids;
+  sa.list_off = a.list_off;
+  sa.bo = L.bo.p;
+  sa.data = L.data.p;
+  sa.xnb = L.xnb.p;
+  sa.xmax2 = L.xmax2.p;
+  sa.nlist = nlist;
+  sa.np = np;
+  sa.xexp = L.xexp;
+  sa.bufA = bufA_.p;
+  sa.offA = offA_.p;
+  sa.epsA = epsA_.p;
+  sa.capA = capA;
+  sa.dkA = dkA_.p;
+  sa.ccnt = ccnt_.p;
+  sa.cand = cand_.p;
+  sa.cap = cap;
+  sa.force = force_.p;
+  pq16_eps_coeffs(16 * L.KC, L.M, L.dsub, L.cmax, sa.c_dot, sa.c_sq, sa.cabs);
+  void (*dense)(ScreenArgs) = nullptr;
+  void (*thresh)(ScreenArgs) = nullptr;
+  switch (L.KC) {
+#define FDB_KC(n)                                  \
+  case n:                                          \
+    dense = pq16_screen_kernel<n, true>;           \
+    thresh = pq16_screen_kernel<n, false>;         \
+    break;
+    FDB_KC(1) FDB_KC(2) FDB_KC(3) FDB_KC(4) FDB_KC(5) FDB_KC(6) FDB_KC(7) FDB_KC(8)
+    FDB_KC(9) FDB_KC(10) FDB_KC(11) FDB_KC(12) FDB_KC(13) FDB_KC(14) FDB_KC(15) FDB_KC(16)
+#undef FDB_KC
+  }
+  if (!dense) throw Error(FDB_ERR_HIP, "no screening kernel for this dimension");
+  const unsigned grid = (unsigned)(8 * ncu_);  // workgroups stride over the tiles
+
+  // 1. the first lists of each query, every screened value kept; d_k bound
+  sort_pairs(0, jlim_.p, capA / 32);
+  sa.qoff = qoff_.p;
+  sa.toff = toff_.p;
+  sa.tl = tl_.p;
+  sa.qlist = qlist_.p;
+  sa.blim = capA / 32;
+  hipLaunchKernelGGL(dense, dim3(grid), dim3(kT), 0, s, sa);
+  FDB_HIP(hipGetLastError());
+  const int R = list_regs(a.k);
+  switch (R) {
+#define FDB_SEL(n)                                                                                              \
+  case n:                                                                                                       \
+    hipLaunchKernelGGL(pq16_select_kernel<n>, dim3((unsigned)nq), dim3(64), 0, s, bufA_.p, capA, nA_.p, nreal_.p, jlim_.p, \
+                       epsA_.p, np, a.k, dkA_.p);                                                               \
+    break;
+    FDB_SEL(1) FDB_SEL(2) FDB_SEL(4) FDB_SEL(8) FDB_SEL(16)
+#undef FDB_SEL
+    default:
+      throw Error(FDB_ERR_UNSUPPORTED, "k above 1024");
+  }
+  FDB_HIP(hipGetLastError());
+
+  // 2. every probed list against the bound
+  sort_pairs(1, nullptr, 0xFFFFFFFFu);
+  sa.qoff = qoff_.p + (nlist + 1);
+  sa.toff = toff_.p + (nlist + 1);
+  sa.tl = tl_.p + tbA;
+  sa.qlist = qlist_.p + std::max<uint64_t>(npr, 1);
+  sa.blim = 0xFFFFFFFFu;
+  hipLaunchKernelGGL(thresh, dim3(grid), dim3(kT), 0, s, sa);
+  FDB_HIP(hipGetLastError());
+
+  // 3. exact distances of the candidates
+  RescoreArgs16 r{};
+  r.queries = a.queries;
+  r.D = L.D;
+  r.M = L.M;
+  r.dsub = L.dsub;
+  r.probes = a.probes;
+  r.np = np;
+  r.centroids = a.centroids;
+  r.codebooks = a.codebooks;
+  r.codes = a.codes;
+  r.ids = a.ids;
+  r.ccnt = ccnt_.p;
+  r.cand = cand_.p;
+  r.cap = cap;
+  r.force = force_.p;
+  r.k = a.k;
+  r.order = a.order;
+  r.out_ids = a.out_ids;
+  r.out_d = a.out_d;
+  r.out_counts = a.out_counts;
+  r.flags = flags_.p;
+  r.cb4 = L.cb4.p;
+  r.nlist = (int)nlist;
+  r.cached = (uint64_t)np * L.D * sizeof(float) <= 48 * 1024;
+  const size_t lds = sizeof(float) * ((size_t)L.D + (r.cached ? (size_t)np * L.D : 0));
+  const int ds = (L.dsub == 3 || L.dsub == 4 || L.dsub == 8) ? L.dsub : 0;
+  void (*rk)(RescoreArgs16) = nullptr;
+#define FDB_RS(n)                                                                       \
+  case n:                                                                               \
+    rk = ds == 3 ? pq16_rescore_kernel<n, 3>                                            \
+                 : (ds == 4 ? pq16_rescore_kernel<n, 4>                                 \
+                            : (ds == 8 ? pq16_rescore_kernel<n, 8> : pq16_rescore_kernel<n, 0>)); \
+    break;
+  switch (R) { FDB_RS(1) FDB_RS(2) FDB_RS(4) FDB_RS(8) FDB_RS(16) }
+#undef FDB_RS
+  hipLaunchKernelGGL(rk, dim3((unsigned)nq), dim3(kT), lds, s, r);
+  FDB_HIP(hipGetLastError());
+  hipLaunchKernelGGL(pq16_stats_kernel, dim3(1), dim3(1024), 0, s, flags_.p, ccnt_.p, nq, stat_.p);
+  FDB_HIP(hipGetLastError());
+}
+
+}  // namespace fdb

@@ -398,8 +398,9 @@ void ivfpq_scan_kernel(IvfPqScanArgs a, int G) {
   const int wave = tid >> 6;
   const uint32_t w0 = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
   const uint64_t q = blockIdx.x;
+  if (a.flags && a.flags[q] == 0) return;  // the whole workgroup
   const float* __restrict__ qv = a.queries + q * D;
-  const int32_t* __restrict__ pr = a.probes + q * (uint64_t)a.np;
+  const int32_t* __restrict__ pr = a.probes + q * (uint64_t)(a.pstride ? a.pstride : a.np);
 
   WaveTopK<R> tk;
   tk.init(a.k);

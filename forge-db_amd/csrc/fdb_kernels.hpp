@@ -48,6 +48,7 @@ struct IvfPqScanArgs {
   int dim, M, dsub;
   const int32_t* probes;  // entries outside [0, nlist) are skipped
   int np;
+  int pstride;  // probes of query q start at q * pstride (0: np); the first np are scanned
   int nlist;
   const float* centroids;  // [nlist][dim]
   const float* codebooks;  // [M][256][dsub]
@@ -67,6 +68,7 @@ struct IvfPqScanArgs {
   uint32_t* out_pos;  // nullable: list positions of the results
   uint32_t* out_counts;
   const uint32_t* live;  // nullable: bitmap over list positions, clear bit = skip
+  const int* flags;      // nullable: [nq]; queries with a zero flag are not scanned
 };
 hipError_t launch_ivfpq_scan(const IvfPqScanArgs& a, hipStream_t stream);
 

@@ -30,6 +30,7 @@ LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libforgedb_hip.so")
 
 __all__ = [
     "DistanceMetric", "ForgeDbError", "IVFPQIndex", "BruteForceIndex", "IVFIndex",
+    "IVFPQ_AUTO", "IVFPQ_EXACT", "IVFPQ_SCREEN",
     "load_library", "LIB_PATH",
     "EXPORTED_SYMBOLS",
 ]
@@ -46,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "fdb_ivfpq_search_filtered", "fdb_ivfpq_delete", "fdb_ivfpq_insert", "fdb_ivfpq_compact",
     "fdb_ivfpq_len", "fdb_ivfpq_num_tombstones", "fdb_ivfpq_set_coarse_mode", "fdb_ivf_set_coarse_mode",
     "fdb_ivf_set_search_mode", "fdb_ivf_last_fallbacks", "fdb_ivf_last_search_path",
+    "fdb_ivfpq_set_search_mode", "fdb_ivfpq_last_screen_stats", "fdb_ivfpq_last_search_path",
     "fdb_bf_create", "fdb_bf_add", "fdb_bf_remove", "fdb_bf_len", "fdb_bf_dimension",
     "fdb_bf_metric", "fdb_bf_load", "fdb_bf_save", "fdb_bf_destroy", "fdb_bf_export",
     "fdb_bf_search", "fdb_bf_batch_search", "fdb_bf_batch_search_device",
@@ -59,6 +61,7 @@ EXPORTED_SYMBOLS = (
 LUT_EXACT, LUT_FAST = 0, 1
 BF_AUTO, BF_EXACT, BF_SCREEN, BF_SCREEN_F32 = 0, 1, 2, 3
 IVF_AUTO, IVF_EXACT = 0, 1
+IVFPQ_AUTO, IVFPQ_EXACT, IVFPQ_SCREEN = 0, 1, 2
 COARSE_AUTO, COARSE_EXACT, COARSE_SCREEN = 0, 1, 2
 
 
@@ -135,6 +138,9 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fdb_ivfpq_insert": [_P, _P, _P, C.c_uint64, C.c_uint32],
         "fdb_ivfpq_compact": [_P],
         "fdb_ivfpq_set_coarse_mode": [_P, C.c_uint32],
+        "fdb_ivfpq_set_search_mode": [_P, C.c_uint32],
+        "fdb_ivfpq_last_screen_stats": [_P, _P, _P, _P],
+        "fdb_ivfpq_last_search_path": [_P, _P],
         "fdb_ivf_set_coarse_mode": [_P, C.c_uint32],
         "fdb_ivf_set_search_mode": [_P, C.c_uint32],
         "fdb_ivf_last_fallbacks": [_P, _P, _P],
@@ -293,6 +299,25 @@ class IVFPQIndex:
     def set_coarse_mode(self, mode: int) -> None:
         """COARSE_AUTO, COARSE_EXACT or COARSE_SCREEN; same probes in every mode."""
         _check(self._lib, self._lib.fdb_ivfpq_set_coarse_mode(self._h, int(mode)))
+
+    def set_search_mode(self, mode: int) -> None:
+        """IVFPQ_AUTO (default: half-precision screening with exact rescoring
+        for large plain batches), IVFPQ_EXACT (table scan only) or
+        IVFPQ_SCREEN (screening wherever it applies); same results."""
+        _check(self._lib, self._lib.fdb_ivfpq_set_search_mode(self._h, int(mode)))
+
+    def last_screen_stats(self, stream: int = 0):
+        """(queries rescanned exactly, candidates rescored) of the last batch."""
+        fb, cand = C.c_uint64(), C.c_uint64()
+        _check(self._lib, self._lib.fdb_ivfpq_last_screen_stats(self._h, C.c_void_p(stream), C.byref(fb),
+                                                                C.byref(cand)))
+        return int(fb.value), int(cand.value)
+
+    def last_search_path(self) -> int:
+        """How the last batch ran: 0 table scan, 2 fp16 screening."""
+        out = C.c_uint32()
+        _check(self._lib, self._lib.fdb_ivfpq_last_search_path(self._h, C.byref(out)))
+        return int(out.value)
 
     def dim(self) -> int:
         return self._dim

@@ -137,6 +137,32 @@ FDB_API uint32_t fdb_ivfpq_lut_mode(const fdb_ivfpq* index);
 enum { FDB_COARSE_AUTO = 0, FDB_COARSE_EXACT = 1, FDB_COARSE_SCREEN = 2 };
 FDB_API fdb_status fdb_ivfpq_set_coarse_mode(fdb_ivfpq* index, uint32_t mode);
 
+/* Scan strategy for batches (no counterpart in the reference, which scores
+ * every code of the probed lists through the distance tables):
+ *   FDB_IVFPQ_AUTO (default): batches scanning at least 2^26 codes with
+ *     exact tables, no reranking, no tombstones and dim <= 256 are screened:
+ *     the exact scan of each query's nearest probed list gives d_k (its k-th
+ *     distance there); half-precision products of each residual with every
+ *     decoded code of the other probed lists (matrix cores) select the codes
+ *     whose screened distance is within a rounding-error bound of d_k; those
+ *     are rescored exactly in the reference's order.  A code left out is
+ *     provably farther than d_k, so results are identical to
+ *     FDB_IVFPQ_EXACT.  Queries with more candidates than the buffer holds,
+ *     or residuals out of half-precision range, are rescanned exactly.
+ *   FDB_IVFPQ_EXACT: the table scan for every query.
+ *   FDB_IVFPQ_SCREEN: screening wherever it applies, whatever the size.
+ * fdb_ivfpq_last_screen_stats reports, for the last batch, the queries
+ * rescanned exactly and the candidates rescored (waits for hip_stream; NULL
+ * = the handle's stream); fdb_ivfpq_last_search_path 0 (table scan) or 2
+ * (screening).  The decoded codes take 2 * roundup(dim, 16) bytes per code
+ * of device memory, built at the first screened search after the lists
+ * change. */
+enum { FDB_IVFPQ_AUTO = 0, FDB_IVFPQ_EXACT = 1, FDB_IVFPQ_SCREEN = 2 };
+FDB_API fdb_status fdb_ivfpq_set_search_mode(fdb_ivfpq* index, uint32_t mode);
+FDB_API fdb_status fdb_ivfpq_last_screen_stats(fdb_ivfpq* index, void* hip_stream, uint64_t* fallbacks,
+                                               uint64_t* candidates);
+FDB_API fdb_status fdb_ivfpq_last_search_path(fdb_ivfpq* index, uint32_t* out);
+
 /* Copies the resident artifacts back (any pointer may be NULL). */
 FDB_API fdb_status fdb_ivfpq_export(const fdb_ivfpq* index, float* centroids, float* codebooks,
                                     uint64_t* list_offsets, uint64_t* ids, uint8_t* codes);

@@ -8,14 +8,15 @@ Every workload bench.py measures, at its full size:
   only chooses which rows are rescored exactly.
 
 C3 and C5 take the index the GPU built; the oracle searches the exported
-artifacts.  One test per workload; each prints its configuration first.
+artifacts, and the screened IVF-PQ batch is compared with the table scan.  One test per workload; each prints its configuration first.
 """
 import numpy as np
 import pytest
 
 import refcpu
 
-from forgedb import BF_EXACT, BF_SCREEN, IVF_AUTO, IVF_EXACT, BruteForceIndex, DistanceMetric, IVFIndex, IVFPQIndex, datagen
+from forgedb import (BF_EXACT, BF_SCREEN, IVF_AUTO, IVF_EXACT, IVFPQ_AUTO, IVFPQ_EXACT, IVFPQ_SCREEN, BruteForceIndex,
+                     DistanceMetric, IVFIndex, IVFPQIndex, datagen)
 
 pytestmark = pytest.mark.gpu
 
@@ -40,22 +41,31 @@ def ivfpq_check(name, nlist, M, nprobe, k, n_oracle):
     ox = refcpu.IvfPq.create(art["centroids"], art["codebooks"], art["list_offsets"], art["ids"], art["codes"])
     ox.set_nprobe(nprobe)
     q = queries[:n_oracle]
-    same(gx.batch_search_arrays(q, k), ox.batch_search(q, k, parallel=True, nthreads=16), name)
-    # the whole batch: ascending, full, and the first queries as above
+    # the oracle's subset through both the screened and the table-scan paths
+    for mode in (IVFPQ_SCREEN, IVFPQ_EXACT):
+        gx.set_search_mode(mode)
+        same(gx.batch_search_arrays(q, k), ox.batch_search(q, k, parallel=True, nthreads=16), f"{name} mode {mode}")
+    # the whole batch screened (the automatic choice at this size) against the table scan
+    gx.set_search_mode(IVFPQ_AUTO)
+    screened = gx.batch_search_arrays(queries, k)
+    assert gx.last_search_path() == 2
+    fb, cand = gx.last_screen_stats()
+    print(f"  screened: {fb} of {len(queries)} rescanned, {cand / len(queries):.0f} candidates per query", flush=True)
+    gx.set_search_mode(IVFPQ_EXACT)
     gi, gd, gc = gx.batch_search_arrays(queries, k)
     assert np.all(gc == k) and np.all(np.diff(gd, axis=1) >= 0)
-    same((gi[:n_oracle], gd[:n_oracle], gc[:n_oracle]), gx.batch_search_arrays(q, k), f"{name} batch")
+    same(screened, (gi, gd, gc), f"{name} screened vs table scan")
 
 
 def test_ivfpq_1m_x128():
-    print("IVF-PQ 1M x 128 integer mixture, nlist 1024, M 16x8, nprobe 16, k 10: "
-          "GPU build, 2000 queries against the oracle", flush=True)
+    print("IVF-PQ 1M x 128 integer mixture, nlist 1024, M 16x8, nprobe 16, k 10: GPU build, 2000 queries "
+          "against the oracle (screened and table scan), 10000 screened against the table scan", flush=True)
     ivfpq_check("ivfpq_int", 1024, 16, 16, 10, 2000)
 
 
 def test_ivfpq_10m_x96():
-    print("IVF-PQ 10M x 96 mixture, nlist 4096, M 32x3, nprobe 64, k 100: "
-          "GPU build, 100 queries against the oracle", flush=True)
+    print("IVF-PQ 10M x 96 mixture, nlist 4096, M 32x3, nprobe 64, k 100: GPU build, 100 queries against "
+          "the oracle (screened and table scan), 10000 screened against the table scan", flush=True)
     ivfpq_check("ivfpq_large", 4096, 32, 64, 100, 100)
 
 
