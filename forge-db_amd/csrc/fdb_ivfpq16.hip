@@ -32,6 +32,24 @@ constexpr int kTileQ = 128;  // (query, probe) pairs per screening workgroup: 4 
 
 uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
+// The wave's index in its workgroup as a wave-uniform value (scalar
+// branches on it).
+__device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+// Direct global-to-LDS loads: each lane's 16 (4) bytes from g land at
+// lds + 16 (4) * lane; lds is wave-uniform.
+__device__ __forceinline__ void lds_load16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_load4(const void* g, void* lds) { __builtin_amdgcn_global_load_lds(g, lds, 4, 0, 0); }
+// s_waitcnt with an immediate; a workgroup barrier without a memory fence
+// (the waits before it are explicit)
+template <int IMM>
+__device__ __forceinline__ void wait_imm() {
+  __builtin_amdgcn_s_waitcnt(IMM);
+}
+__device__ __forceinline__ void bare_barrier() { __builtin_amdgcn_s_barrier(); }
+
 // WaveTopK registers for k: ceil(k / 64) rounded up to a power of two
 int list_regs(int k) {
   int r = (k + 63) / 64, p = 1;
@@ -151,6 +169,8 @@ constexpr uint32_t kHistMax = 8192;  // lists counted in LDS (32 KiB)
 constexpr int kSortWG = 32;          // workgroups of the counting sort (at most)
 constexpr uint32_t kCB = 64;         // blocks of 32 codes per screening tile
 constexpr int kSlots = 8;            // candidate slots per lane in LDS
+constexpr int kNS = 4;               // one-block stages in the screening kernel's LDS ring
+constexpr uint32_t kLight = 512;     // candidates rescored by one wave (more: four)
 
 struct PairSet {
   const int32_t* probes;
@@ -288,9 +308,15 @@ __global__ __launch_bounds__(kT) void pq16_plan_kernel(const int32_t* __restrict
                                                        uint32_t nlist, const uint32_t* __restrict__ list_off,
                                                        int k, uint32_t capA, uint32_t* __restrict__ jlim,
                                                        uint32_t* __restrict__ offA, uint32_t* __restrict__ nA,
-                                                       uint32_t* __restrict__ nreal) {
+                                                       uint32_t* __restrict__ nreal, uint32_t* __restrict__ ccnt,
+                                                       int* __restrict__ force, float* __restrict__ epsA,
+                                                       uint32_t* __restrict__ nheavy) {
   const uint64_t q = (uint64_t)blockIdx.x * kT + threadIdx.x;
+  if (q == 0) *nheavy = 0;
   if (q >= nq) return;
+  ccnt[q] = 0;  // the query's counters and bounds start clear
+  force[q] = 0;
+  for (int j = 0; j < np; ++j) epsA[q * np + j] = 0.0f;
   uint64_t cum = 0, real = 0;
   uint32_t J = 0;
   for (int j = 0; j < np; ++j) {
@@ -358,27 +384,6 @@ __device__ __forceinline__ float add_up(float a, float b) {
   return t + t * 0x1p-22f;
 }
 
-// Stage loads of blocks bs0 .. bs0+SB-1 (unit u = (block, k-chunk, lane));
-// blocks past the chunk's end (be) re-read its last block, never multiplied.
-template <int KC, int SB, int PER>
-__device__ __forceinline__ void stage_fetch(v4u (&pre)[PER], float4& prex, const v4u* __restrict__ A,
-                                            const float* __restrict__ XN, uint32_t bs0, uint32_t be, int tid) {
-  constexpr int kUnits = SB * KC * 64;
-  if (tid < SB * 8) {  // |x^|^2 of the stage's codes, 4 per thread
-    const uint32_t b = min(bs0 + (uint32_t)(tid >> 3), be - 1);
-    prex = *reinterpret_cast<const float4*>(XN + (uint64_t)b * 32 + 4 * (tid & 7));
-  }
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int u = tid + i * kT;
-    if (kUnits % kT == 0 || u < kUnits) {
-      const int bs = u / (KC * 64);
-      const uint32_t b = min(bs0 + (uint32_t)bs, be - 1);
-      pre[i] = A[(uint64_t)b * KC * 64 + (uint32_t)(u - bs * KC * 64)];
-    }
-  }
-}
-
 // Tiles: list p owns toff[p] .. toff[p+1]: ceil(pairs_p / 128) pair tiles
 // (fastest) times ceil(min(blocks_p, blim) / kCB) block chunks; workgroups
 // stride over the tiles.  In a tile, wave w takes pairs [32w, 32w+32): lane
@@ -396,17 +401,22 @@ __device__ __forceinline__ void stage_fetch(v4u (&pre)[PER], float4& prex, const
 //   list's end, nothing past capA), four rows per 16-byte store.
 template <int KC, bool DENSE>
 __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
-  constexpr int SB = KC <= 2 ? 16 : (KC <= 4 ? 8 : (KC <= 8 ? 4 : 2));  // blocks per stage (<= 32 KiB)
-  constexpr int kUnits = SB * KC * 64;
-  constexpr int kPer = (kUnits + kT - 1) / kT;
-  __shared__ v4u stage[kUnits];
-  __shared__ float4 sxn[SB * 8];
+  constexpr int kUW = (KC + 3) / 4;  // k-chunk loads per wave per block
+  // s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
+  // at their maxima): all but the newest (kNS - 2) blocks' loads, and all
+  constexpr int kRingLoads = (kNS - 2) * (kUW + 1);
+  constexpr int kWaitRing = (kRingLoads & 15) | ((kRingLoads >> 4) << 14) | 0x70 | 0xF00;
+  constexpr int kWaitAll = 0x70 | 0xF00;
+  __shared__ v4u ring[kNS][KC * 64];
+  __shared__ float rxn[kNS][64];  // |x^|^2 of the block (32 values, twice)
+  __shared__ v4u dummy[64];
+  __shared__ float dxn[64];
   // threshold mode: lane-private candidate slots, moved to the query's list
   // when full and at the end of each tile (one reservation per move)
   __shared__ uint2 slots[DENSE ? 1 : kT * kSlots];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = wave_index();
   const int col = lane & 31;
   const int half = lane >> 5;
   const uint32_t ntiles = a.toff[a.nlist];
@@ -416,7 +426,13 @@ __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
     const uint32_t nqt = (qend - qb + kTileQ - 1) / kTileQ;
     const uint32_t local = t - a.toff[p];
     const uint32_t chunk = local / nqt;
-    const uint32_t q0 = qb + (local - chunk * nqt) * kTileQ + (uint32_t)wave * 32;
+    // groups of 32 pairs in the tile; with fewer than four, the waves of a
+    // group take every split-th block of the stage
+    const uint32_t tq0 = qb + (local - chunk * nqt) * kTileQ;
+    const uint32_t ng = min((qend - tq0 + 31) / 32, 4u);
+    const int split = ng == 1 ? 4 : (ng == 2 ? 2 : 1);
+    const int phase = wave % split;
+    const uint32_t q0 = tq0 + (uint32_t)(wave / split) * 32;
     const bool busy = q0 < qend;  // wave-uniform: the wave has pairs
     const bool qv = busy && q0 + (uint32_t)col < qend;
     uint32_t q = 0, j = 0;
@@ -501,88 +517,112 @@ __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
     const uint32_t len = a.list_off[p + 1] - start;
     const v4u* __restrict__ A = reinterpret_cast<const v4u*>(a.data) + (uint64_t)b0 * KC * 64;
     const float* __restrict__ XN = a.xnb + (uint64_t)b0 * 32;
-    // stage loads: unit u = (block bs, k-chunk, lane); blocks past the
-    // chunk's end re-read its last block (never multiplied)
     int nslot = 0;
     auto move = [&](int n) {
       const uint32_t pos = atomicAdd(&a.ccnt[q], (uint32_t)n);
       uint2* __restrict__ out = a.cand + (uint64_t)q * a.cap;
+#pragma unroll 1
       for (int i = 0; i < n; ++i)
         if (pos + (uint32_t)i < a.cap) out[pos + i] = slots[tid * kSlots + i];
     };
-    v4u pre[kPer];
-    float4 prex = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    stage_fetch<KC, SB, kPer>(pre, prex, A, XN, bb, be, tid);
-    for (uint32_t bs0 = bb; bs0 < be; bs0 += SB) {
-      __syncthreads();  // the previous stage (or tile) is consumed
+    // one block from the ring: KC products, then the mode's epilogue
+    auto block_step = [&](const v4u* __restrict__ sa, const float* __restrict__ sx, uint32_t b) {
+      v16f acc = {};
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) {
-        const int u = tid + i * kT;
-        if (kUnits % kT == 0 || u < kUnits) stage[u] = pre[i];
+      for (int kc = 0; kc < KC; ++kc)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, sa[kc * 64 + lane]), bq[kc], acc, 0, 0,
+                                                     0);
+      const uint32_t rowb = b * 32 + 4 * half;
+      float xs[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 x4 = *reinterpret_cast<const float4*>(sx + 8 * g + 4 * half);
+        xs[4 * g] = x4.x;
+        xs[4 * g + 1] = x4.y;
+        xs[4 * g + 2] = x4.z;
+        xs[4 * g + 3] = x4.w;
       }
-      if (tid < SB * 8) sxn[tid] = prex;
-      __syncthreads();
-      if (bs0 + SB < be) stage_fetch<KC, SB, kPer>(pre, prex, A, XN, bs0 + SB, be, tid);
-      if (!busy) continue;
-#pragma unroll 1
-      for (int bs = 0; bs < SB; ++bs) {
-        const uint32_t b = bs0 + (uint32_t)bs;
-        if (b >= be) break;
-        v16f acc = {};
+      if constexpr (DENSE) {
+        if (act) {
 #pragma unroll
-        for (int kc = 0; kc < KC; ++kc)
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, stage[(bs * KC + kc) * 64 + lane]),
-                                                       bq[kc], acc, 0, 0, 0);
-        const uint32_t rowb = b * 32 + 4 * half;
-        float xs[16];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float4 x4 = sxn[bs * 8 + 2 * g + half];
-          xs[4 * g] = x4.x;
-          xs[4 * g + 1] = x4.y;
-          xs[4 * g + 2] = x4.z;
-          xs[4 * g + 3] = x4.w;
-        }
-        if constexpr (DENSE) {
-          if (act) {
-            const float base = rn;
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const uint32_t row = rowb + 8 * g;
-              if (o + row < a.capA) {
-                float4 v;
-                v.x = row + 0 < len ? __builtin_fmaf(cneg, acc[4 * g + 0], base + xs[4 * g + 0]) : f_inf();
-                v.y = row + 1 < len ? __builtin_fmaf(cneg, acc[4 * g + 1], base + xs[4 * g + 1]) : f_inf();
-                v.z = row + 2 < len ? __builtin_fmaf(cneg, acc[4 * g + 2], base + xs[4 * g + 2]) : f_inf();
-                v.w = row + 3 < len ? __builtin_fmaf(cneg, acc[4 * g + 3], base + xs[4 * g + 3]) : f_inf();
-                *reinterpret_cast<float4*>(a.bufA + (uint64_t)q * a.capA + o + row) = v;
-              }
+          for (int g = 0; g < 4; ++g) {
+            const uint32_t row = rowb + 8 * g;
+            if (o + row < a.capA) {
+              float4 v;
+              v.x = row + 0 < len ? __builtin_fmaf(cneg, acc[4 * g + 0], rn + xs[4 * g + 0]) : f_inf();
+              v.y = row + 1 < len ? __builtin_fmaf(cneg, acc[4 * g + 1], rn + xs[4 * g + 1]) : f_inf();
+              v.z = row + 2 < len ? __builtin_fmaf(cneg, acc[4 * g + 2], rn + xs[4 * g + 2]) : f_inf();
+              v.w = row + 3 < len ? __builtin_fmaf(cneg, acc[4 * g + 3], rn + xs[4 * g + 3]) : f_inf();
+              *reinterpret_cast<float4*>(a.bufA + (uint64_t)q * a.capA + o + row) = v;
             }
           }
-        } else {
-          float sv[16];
-          bool any = false;
+        }
+      } else {
+        uint32_t passm = 0;
 #pragma unroll
-          for (int rr = 0; rr < 16; ++rr) {
-            sv[rr] = __builtin_fmaf(cneg, acc[rr], xs[rr]);
-            any = any || sv[rr] <= Tp;
-          }
-          if (__ballot(any) != 0) {
+        for (int rr = 0; rr < 16; ++rr)
+          passm |= (__builtin_fmaf(cneg, acc[rr], xs[rr]) <= Tp ? 1u : 0u) << rr;
+        // rows past the list's end (the last block's padding) never pass
+        if (rowb + 28 > len)
 #pragma unroll
-            for (int rr = 0; rr < 16; ++rr) {
-              const uint32_t row = rowb + 8 * (rr >> 2) + (rr & 3);
-              if (sv[rr] <= Tp && row < len) {
-                slots[tid * kSlots + nslot] = make_uint2(start + row, j);
-                if (++nslot == kSlots) {
-                  move(kSlots);
-                  nslot = 0;
-                }
-              }
+          for (int rr = 0; rr < 16; ++rr)
+            if (rowb + 8 * (rr >> 2) + (rr & 3) >= len) passm &= ~(1u << rr);
+        if (__ballot(passm != 0) != 0) {
+          while (passm) {  // a compact loop: the slow path stays small
+            const int rr = __ffs(passm) - 1;
+            passm &= passm - 1;
+            slots[tid * kSlots + nslot] = make_uint2(start + rowb + 8 * (rr >> 2) + (rr & 3), j);
+            if (++nslot == kSlots) {
+              move(kSlots);
+              nslot = 0;
             }
           }
         }
       }
+    };
+    // The chunk's blocks stream through a ring of kNS one-block LDS buffers
+    // by direct global-to-LDS loads; block bb + s lands in ring[s % kNS].
+    // Every wave issues kUW + 1 loads per block (k-chunks w, w+4, ...;
+    // wave 0 also the block's |x^|^2; spare loads re-read into a dummy
+    // buffer), so waiting for all but the last (kNS-2) blocks' loads is one
+    // immediate count.  Blocks past the chunk's end re-read its last block.
+    const uint32_t nst = be - bb;
+#define FDB_ISSUE(BUF, S)                                                                               \
+    {                                                                                                   \
+      const uint32_t bl = bb + min((uint32_t)(S), nst - 1);                                             \
+      _Pragma("unroll") for (int i = 0; i < kUW; ++i) {                                                 \
+        const int u = wave + 4 * i;                                                                     \
+        if (u < KC)                                                                                     \
+          lds_load16(A + ((uint64_t)bl * KC + u) * 64 + lane, &ring[BUF][u * 64]);                     \
+        else                                                                                            \
+          lds_load16(A + (uint64_t)bl * KC * 64 + lane, &dummy[0]);                                     \
+      }                                                                                                 \
+      if (wave == 0)                                                                                    \
+        lds_load4(XN + (uint64_t)bl * 32 + (lane & 31), &rxn[BUF][0]);                                 \
+      else                                                                                              \
+        lds_load4(XN + (uint64_t)bl * 32 + (lane & 31), &dxn[0]);                                       \
     }
+    FDB_ISSUE(0, 0)
+    FDB_ISSUE(1, 1)
+    FDB_ISSUE(2, 2)
+#define FDB_STEP(BUF)                                                                                   \
+    if (s < nst) {                                                                                      \
+      wait_imm<kWaitRing>();  /* this wave's loads of block s have landed */                            \
+      bare_barrier();         /* everyone's have; ring[(s-1) % kNS] is free */                          \
+      FDB_ISSUE((BUF + kNS - 1) % kNS, s + kNS - 1)                                                     \
+      if (busy && (int)(s % split) == phase) block_step(ring[BUF], rxn[BUF], bb + s);                   \
+      ++s;                                                                                              \
+    }
+    for (uint32_t s = 0; s < nst;) {
+      FDB_STEP(0)
+      FDB_STEP(1)
+      FDB_STEP(2)
+      FDB_STEP(3)
+    }
+#undef FDB_STEP
+#undef FDB_ISSUE
+    wait_imm<kWaitAll>();  // spare loads of the ring's tail
+    bare_barrier();        // the ring is free for the next tile
     if constexpr (!DENSE) {
       if (nslot > 0) move(nslot);
     }
@@ -613,21 +653,18 @@ __global__ __launch_bounds__(64) void pq16_select_kernel(const float* __restrict
   int qn = 0;
   const float4* __restrict__ v = reinterpret_cast<const float4*>(bufA + q * capA);
   const uint32_t n4 = (n + 3) / 4;  // n is a multiple of 32 or capA
-  for (uint32_t i0 = 0; i0 < n4; i0 += 256) {
-    float4 w[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint32_t i = i0 + (uint32_t)(u * 64 + lane);
-      w[u] = i < n4 ? v[i] : make_float4(f_inf(), f_inf(), f_inf(), f_inf());
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint32_t i = 4 * (i0 + (uint32_t)(u * 64 + lane));
-      tk.offer_queued(w[u].x, i, w[u].x < f_inf(), queue, qn);
-      tk.offer_queued(w[u].y, i + 1, w[u].y < f_inf(), queue, qn);
-      tk.offer_queued(w[u].z, i + 2, w[u].z < f_inf(), queue, qn);
-      tk.offer_queued(w[u].w, i + 3, w[u].w < f_inf(), queue, qn);
-    }
+  const float4 none = make_float4(f_inf(), f_inf(), f_inf(), f_inf());
+  float4 w = (uint32_t)lane < n4 ? v[lane] : none;
+#pragma unroll 1
+  for (uint32_t i0 = 0; i0 < n4; i0 += 64) {
+    const uint32_t inext = i0 + 64 + (uint32_t)lane;
+    const float4 wn = inext < n4 ? v[inext] : none;  // the next values in flight
+    const uint32_t i = 4 * (i0 + (uint32_t)lane);
+    tk.offer_queued(w.x, i, w.x < f_inf(), queue, qn);
+    tk.offer_queued(w.y, i + 1, w.y < f_inf(), queue, qn);
+    tk.offer_queued(w.z, i + 2, w.z < f_inf(), queue, qn);
+    tk.offer_queued(w.w, i + 3, w.w < f_inf(), queue, qn);
+    w = wn;
   }
   tk.flush(queue, qn);
   float em = 0.0f;
@@ -687,6 +724,8 @@ struct RescoreArgs16 {
   float* out_d;
   uint32_t* out_counts;
   int* flags;
+  uint32_t* heavy;   // queries of more than kLight candidates, by the light kernel
+  uint32_t* nheavy;  // their number (cleared before the light kernel)
 };
 
 // One table entry from the cached residual row r of the subspace (LDS) and
@@ -788,26 +827,142 @@ __device__ __forceinline__ float adc_order(int M, int order, V v) {
   return sum;
 }
 
+// One table entry from the query (LDS), centroid and padded codeword rows
+// of one subspace, the l2sq_ref order on (q - c) - cw; DS: dsub at compile
+// time (0 = runtime), 16-byte loads where the rows allow.
+template <int DS>
+__device__ __forceinline__ float entry_direct(const float* __restrict__ qs, const float* __restrict__ cen,
+                                             const float* __restrict__ cw, int dsub) {
+  if constexpr (DS > 0) {
+    constexpr int DS4 = (DS + 3) / 4 * 4;
+    float c[DS4], cn[DS];
+#pragma unroll
+    for (int i = 0; i < DS4 / 4; ++i) {
+      const float4 v = reinterpret_cast<const float4*>(cw)[i];
+      c[4 * i] = v.x;
+      c[4 * i + 1] = v.y;
+      c[4 * i + 2] = v.z;
+      c[4 * i + 3] = v.w;
+    }
+    if constexpr (DS % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < DS / 4; ++i) {
+        const float4 v = reinterpret_cast<const float4*>(cen)[i];
+        cn[4 * i] = v.x;
+        cn[4 * i + 1] = v.y;
+        cn[4 * i + 2] = v.z;
+        cn[4 * i + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < DS; ++i) cn[i] = cen[i];
+    }
+    constexpr int NB = DS / 8;
+    float total = 0.0f;
+    if constexpr (NB > 0) {
+      float lane[8];
+#pragma unroll
+      for (int l = 0; l < 8; ++l) {
+        const float d = (qs[l] - cn[l]) - c[l];
+        lane[l] = __builtin_fmaf(d, d, 0.0f);
+      }
+#pragma unroll
+      for (int i = 1; i < NB; ++i)
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+          const float d = (qs[8 * i + l] - cn[8 * i + l]) - c[8 * i + l];
+          lane[l] = __builtin_fmaf(d, d, lane[l]);
+        }
+      total = lane[0];
+#pragma unroll
+      for (int l = 1; l < 8; ++l) total = total + lane[l];
+    }
+#pragma unroll
+    for (int i = 8 * NB; i < DS; ++i) {
+      const float d = (qs[i] - cn[i]) - c[i];
+      total = total + d * d;
+    }
+    return total;
+  } else {
+    return pq_entry(qs, cen, cw, dsub);
+  }
+}
+
+// One wave per query, four queries per workgroup: the queries with at most
+// kLight candidates (the others go to pq16_rescore_kernel) scored and
+// selected as there.  Writes every query's flag: 1 (table scan) for a
+// residual out of fp16 range or more candidates than slots.
+template <int R, int DS>
+__global__ __launch_bounds__(kT) void pq16_rescore_light_kernel(RescoreArgs16 a, uint64_t nq) {
+  __shared__ float qsm[kT / 64][256];
+  __shared__ uint2 queue[kT / 64][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_index();
+  const uint64_t q = (uint64_t)blockIdx.x * (kT / 64) + wave;
+  const bool have = q < nq;
+  const uint32_t cnt = have ? a.ccnt[q] : 0u;
+  const bool fall = have && (a.force[q] != 0 || cnt > a.cap);
+  if (have && lane == 0) a.flags[q] = fall ? 1 : 0;
+  const int D = a.D;
+  if (have)
+    for (int d = lane; d < D; d += 64) qsm[wave][d] = a.queries[q * D + d];
+  __syncthreads();
+  if (have && !fall && cnt > kLight && lane == 0) a.heavy[atomicAdd(a.nheavy, 1u)] = (uint32_t)q;
+  if (!have || fall || cnt > kLight) return;
+  const float* __restrict__ qs = qsm[wave];
+  WaveTopK<R> tk;
+  tk.init(a.k);
+  int qn = 0;
+  const uint2* __restrict__ cq = a.cand + q * a.cap;
+  const int M = a.M, dsub = DS > 0 ? DS : a.dsub;
+  const int ds4 = (dsub + 3) / 4 * 4;
+  for (uint32_t c0 = 0; c0 < cnt; c0 += 64) {
+    const uint32_t c = c0 + (uint32_t)lane;
+    uint32_t key = kNoPos;
+    float d = f_inf();
+    if (c < cnt) {
+      const uint2 e = cq[c];
+      key = e.x;
+      const uint8_t* __restrict__ code = a.codes + (uint64_t)key * M;
+      const float* __restrict__ cen = a.centroids + (uint64_t)a.probes[q * a.np + e.y] * D;
+      d = adc_order(M, a.order, [&](int m) {
+        return entry_direct<DS>(qs + m * dsub, cen + m * dsub, a.cb4 + ((uint64_t)m * 256 + code[m]) * ds4, dsub);
+      });
+    }
+    tk.offer_queued(d, key, c < cnt, queue[wave], qn);
+  }
+  tk.flush(queue[wave], qn);
+  uint32_t count = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int s = r * 64 + lane;
+    const bool valid = s < a.k && tk.p[r] != kNoPos;
+    count += (uint32_t)__popcll(__ballot(valid));
+    if (s < a.k) {
+      a.out_ids[q * a.k + s] = valid ? a.ids[tk.p[r]] : ~0ull;
+      a.out_d[q * a.k + s] = valid ? tk.d[r] : f_inf();
+    }
+  }
+  if (lane == 0) a.out_counts[q] = count;
+}
+
 // Four waves per query: the candidates' reference distances (wave w takes
 // every fourth batch of 64) and the top k (ties: smaller list position, as
 // the table scan), the wave lists merged by wave 0.  The residuals r_j =
 // q - c_(probe j) are computed once into LDS (rc [np][D]) when they fit
 // (cached), else per candidate.  Queries with a residual out of fp16 range
 // or more candidates than slots are flagged for the table scan.
+// One query of more than kLight candidates, by the whole workgroup.
 template <int R, int DS>
-__global__ __launch_bounds__(kT) void pq16_rescore_kernel(RescoreArgs16 a) {
+__device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q) {
   extern __shared__ float qs[];  // [D], then rc [np][D] when cached
   __shared__ uint2 queue[kT / 64][64];
   __shared__ float md[kT / 64][64 * R];
   __shared__ uint32_t mk[kT / 64][64 * R];
-  const uint64_t q = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const uint32_t cnt = a.ccnt[q];
-  const bool fall = a.force[q] != 0 || cnt > a.cap;
-  if (tid == 0) a.flags[q] = fall ? 1 : 0;
-  if (fall) return;  // the whole workgroup
   const int D = a.D;
   float* rc = qs + D;
   // a few candidates are cheaper to rescore without the residual cache
@@ -858,7 +1013,7 @@ __global__ __launch_bounds__(kT) void pq16_rescore_kernel(RescoreArgs16 a) {
     mk[wave][r * 64 + lane] = tk.p[r];
   }
   __syncthreads();
-  if (wave != 0) return;
+  if (wave != 0) return;  // waves 1-3 go on to the caller's barrier
   for (int w = 1; w < kT / 64; ++w)
 #pragma unroll
     for (int r = 0; r < R; ++r) tk.offer(md[w][r * 64 + lane], mk[w][r * 64 + lane]);
@@ -874,6 +1029,14 @@ __global__ __launch_bounds__(kT) void pq16_rescore_kernel(RescoreArgs16 a) {
     }
   }
   if (lane == 0) a.out_counts[q] = count;
+}
+
+template <int R, int DS>
+__global__ __launch_bounds__(kT) void pq16_rescore_kernel(RescoreArgs16 a) {
+  for (uint32_t h = blockIdx.x; h < *a.nheavy; h += gridDim.x) {
+    pq16_rescore_heavy<R, DS>(a, a.heavy[h]);
+    __syncthreads();  // the LDS is reused by the next query
+  }
 }
 
 // One workgroup: stat[0] += queries flagged, stat[2..3] += candidates of
@@ -1049,16 +1212,11 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   force_.reserve(nq);
   flags_.reserve(nq);
   if (!stat_.p) reset_stats(s);
-  auto fill = [&](uint32_t* p, uint64_t n) {
-    hipLaunchKernelGGL(pq16_fill_u32, dim3((unsigned)std::min<uint64_t>(std::max<uint64_t>(cdiv(n, kT), 1), 1024)),
-                       dim3(kT), 0, s, p, n, 0u);
-    FDB_HIP(hipGetLastError());
-  };
-  fill(ccnt_.p, nq);
-  fill(reinterpret_cast<uint32_t*>(force_.p), nq);
-  fill(reinterpret_cast<uint32_t*>(epsA_.p), npr);
+  heavy_.reserve(nq);
+  nheavy_.reserve(1);
   hipLaunchKernelGGL(pq16_plan_kernel, dim3((unsigned)cdiv(nq, kT)), dim3(kT), 0, s, a.probes, nq, np, nlist,
-                     a.list_off, a.k, capA, jlim_.p, offA_.p, nA_.p, nreal_.p);
+                     a.list_off, a.k, capA, jlim_.p, offA_.p, nA_.p, nreal_.p, ccnt_.p, force_.p, epsA_.p,
+                     nheavy_.p);
   FDB_HIP(hipGetLastError());
 
   // (query, probe) pairs grouped by list, stage st (0: first lists, 1: all)
@@ -1180,21 +1338,29 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   r.out_d = a.out_d;
   r.out_counts = a.out_counts;
   r.flags = flags_.p;
+  r.heavy = heavy_.p;
+  r.nheavy = nheavy_.p;
   r.cb4 = L.cb4.p;
   r.nlist = (int)nlist;
   r.cached = (uint64_t)np * L.D * sizeof(float) <= 48 * 1024;
   const size_t lds = sizeof(float) * ((size_t)L.D + (r.cached ? (size_t)np * L.D : 0));
   const int ds = (L.dsub == 3 || L.dsub == 4 || L.dsub == 8) ? L.dsub : 0;
   void (*rk)(RescoreArgs16) = nullptr;
+  void (*lk)(RescoreArgs16, uint64_t) = nullptr;
 #define FDB_RS(n)                                                                       \
   case n:                                                                               \
     rk = ds == 3 ? pq16_rescore_kernel<n, 3>                                            \
                  : (ds == 4 ? pq16_rescore_kernel<n, 4>                                 \
                             : (ds == 8 ? pq16_rescore_kernel<n, 8> : pq16_rescore_kernel<n, 0>)); \
+    lk = ds == 3 ? pq16_rescore_light_kernel<n, 3>                                      \
+                 : (ds == 4 ? pq16_rescore_light_kernel<n, 4>                           \
+                            : (ds == 8 ? pq16_rescore_light_kernel<n, 8> : pq16_rescore_light_kernel<n, 0>)); \
     break;
   switch (R) { FDB_RS(1) FDB_RS(2) FDB_RS(4) FDB_RS(8) FDB_RS(16) }
 #undef FDB_RS
-  hipLaunchKernelGGL(rk, dim3((unsigned)nq), dim3(kT), lds, s, r);
+  hipLaunchKernelGGL(lk, dim3((unsigned)cdiv(nq, kT / 64)), dim3(kT), 0, s, r, nq);
+  FDB_HIP(hipGetLastError());
+  hipLaunchKernelGGL(rk, dim3((unsigned)std::min<uint64_t>(nq, 4 * (uint64_t)ncu_)), dim3(kT), lds, s, r);
   FDB_HIP(hipGetLastError());
   hipLaunchKernelGGL(pq16_stats_kernel, dim3(1), dim3(1024), 0, s, flags_.p, ccnt_.p, nq, stat_.p);
   FDB_HIP(hipGetLastError());

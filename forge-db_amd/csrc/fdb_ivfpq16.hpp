@@ -90,7 +90,7 @@ class Pq16Searcher {
 
  private:
   int ncu_ = 0;
-  DevBuf<uint32_t> H_, qoff_, toff_, tl_, jlim_, offA_, nA_, nreal_, ccnt_, stat_;
+  DevBuf<uint32_t> H_, qoff_, toff_, tl_, jlim_, offA_, nA_, nreal_, ccnt_, stat_, heavy_, nheavy_;
   DevBuf<uint2> qlist_, cand_;
   DevBuf<float> epsA_, bufA_, dkA_;
   DevBuf<int> force_, flags_;
