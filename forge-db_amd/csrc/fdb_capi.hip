@@ -216,6 +216,13 @@ fdb_status fdb_ivfpq_last_search_path(fdb_ivfpq* h, uint32_t* out) {
   });
 }
 
+fdb_status fdb_ivfpq_last_screen_kernel_ms(fdb_ivfpq* h, float* out) {
+  return guarded([&] {
+    if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    *out = H(h)->last_screen_kernel_ms();
+  });
+}
+
 fdb_status fdb_ivfpq_describe(const fdb_ivfpq* h, fdb_ivfpq_desc* out) {
   return guarded([&] {
     if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");

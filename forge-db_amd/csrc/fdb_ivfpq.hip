@@ -537,6 +537,7 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
   path_ = screen ? 2 : 0;
   if (screen) {
     pq16s_.reset_stats(s);
+    pq16s_.set_timing(timed);
     const uint64_t sl = std::min<uint64_t>(nq, Pq16Searcher::slice((int)k));
     const uint64_t D = host_.dim;
     for (uint64_t q0 = 0; q0 < nq; q0 += sl) {
@@ -568,7 +569,10 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
       af.flags = pq16s_.flags();
       FDB_HIP(launch_ivfpq_scan(af, s));
     }
+    if (timed) screen_kernel_ms_ = pq16s_.screen_ms();
+    pq16s_.set_timing(false);
   } else {
+    if (timed) screen_kernel_ms_ = 0.0f;
     FDB_HIP(launch_ivfpq_scan(a, s));
   }
   if (rerank)

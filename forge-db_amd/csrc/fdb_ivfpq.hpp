@@ -59,6 +59,12 @@ class IvfPqIndex {
     return path_;
   }
   void last_screen_stats(uint64_t& fallbacks, uint64_t& candidates, hipStream_t s);
+  // duration of the threshold screening kernel in the last timed batch (0
+  // when it took the table scan)
+  float last_screen_kernel_ms() {
+    std::lock_guard<std::mutex> g(mu_);
+    return screen_kernel_ms_;
+  }
 
   // single query with search() semantics; returns count
   uint32_t search(const float* q, uint32_t k, uint64_t* ids, float* dists);
@@ -146,6 +152,7 @@ class IvfPqIndex {
   bool pq16_dirty_ = true;
   Pq16Searcher pq16s_;
   int path_ = 0;
+  float screen_kernel_ms_ = 0.0f;
 };
 
 // Seeded k-means over n host rows [n][dim] (KMeans::fit_raw, kmeans.rs:87-193):

@@ -49,6 +49,12 @@ __device__ __forceinline__ void wait_imm() {
   __builtin_amdgcn_s_waitcnt(IMM);
 }
 __device__ __forceinline__ void bare_barrier() { __builtin_amdgcn_s_barrier(); }
+// Scheduling hint: the N LDS reads of a block, then its N matrix products.
+template <int N>
+__device__ __forceinline__ void sched_reads_then_mfma() {
+  __builtin_amdgcn_sched_group_barrier(0x100, N, 0);  // DS reads
+  __builtin_amdgcn_sched_group_barrier(0x008, N, 0);  // MFMA
+}
 
 // WaveTopK registers for k: ceil(k / 64) rounded up to a power of two
 int list_regs(int k) {
@@ -168,9 +174,11 @@ __global__ __launch_bounds__(kT) void pq16_norms_kernel(const float* __restrict_
 constexpr uint32_t kHistMax = 8192;  // lists counted in LDS (32 KiB)
 constexpr int kSortWG = 32;          // workgroups of the counting sort (at most)
 constexpr uint32_t kCB = 64;         // blocks of 32 codes per screening tile
+constexpr uint32_t kXcd = 8;         // L2 domains (XCDs); workgroup b runs on XCD b % 8
+constexpr uint32_t kXcdRun = 4;      // consecutive tiles given to one XCD
 constexpr int kSlots = 8;            // candidate slots per lane in LDS
 constexpr int kNS = 4;               // one-block stages in the screening kernel's LDS ring
-constexpr uint32_t kLight = 512;     // candidates rescored by one wave (more: four)
+constexpr uint32_t kLight = 512;     // candidate entries rescored by one wave (more: four)
 
 struct PairSet {
   const int32_t* probes;
@@ -420,7 +428,14 @@ __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
   const int col = lane & 31;
   const int half = lane >> 5;
   const uint32_t ntiles = a.toff[a.nlist];
-  for (uint32_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+  // Tiles of one list chunk (its pair tiles are consecutive) read the same
+  // blocks: runs of kXcdRun consecutive tiles go to workgroups b, b + 8,
+  // b + 16, ... of one XCD, dispatched together, so the repeat reads hit
+  // that XCD's L2.  A bijection on each round of gridDim.x tiles (a
+  // multiple of kXcd * kXcdRun).
+  const uint32_t xcd = blockIdx.x % kXcd, y = blockIdx.x / kXcd;
+  const uint32_t slot = ((y / kXcdRun) * kXcd + xcd) * kXcdRun + y % kXcdRun;
+  for (uint32_t t = slot; t < ntiles; t += gridDim.x) {
     const uint32_t p = a.tl[t];
     const uint32_t qb = a.qoff[p], qend = a.qoff[p + 1];
     const uint32_t nqt = (qend - qb + kTileQ - 1) / kTileQ;
@@ -435,12 +450,10 @@ __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
     const uint32_t q0 = tq0 + (uint32_t)(wave / split) * 32;
     const bool busy = q0 < qend;  // wave-uniform: the wave has pairs
     const bool qv = busy && q0 + (uint32_t)col < qend;
-    uint32_t q = 0, j = 0;
-    if (qv) {
-      const uint2 e = a.qlist[q0 + col];
-      q = e.x;
-      j = e.y;
-    }
+    // lanes past the tile's pairs repeat its last pair, so that every load
+    // below is in bounds without a branch per load (qv keeps them inactive)
+    const uint2 e = a.qlist[min(q0 + (uint32_t)col, qend - 1)];
+    const uint32_t q = e.x, j = e.y;
     const float* __restrict__ qp = a.queries + (uint64_t)q * a.D;
     const float* __restrict__ cp = a.centroids + (uint64_t)p * a.D;
     float r[KC][8];
@@ -451,11 +464,8 @@ __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
 #pragma unroll
         for (int h4 = 0; h4 < 2; ++h4) {
           const int d = kc * 16 + 8 * half + 4 * h4;
-          float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = x;
-          if (qv) {
-            x = *reinterpret_cast<const float4*>(qp + d);
-            c = *reinterpret_cast<const float4*>(cp + d);
-          }
+          const float4 x = *reinterpret_cast<const float4*>(qp + d);
+          const float4 c = *reinterpret_cast<const float4*>(cp + d);
           r[kc][4 * h4] = x.x - c.x;  // the reference's residual
           r[kc][4 * h4 + 1] = x.y - c.y;
           r[kc][4 * h4 + 2] = x.z - c.z;
@@ -467,7 +477,7 @@ __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int d = kc * 16 + 8 * half + i;
-          r[kc][i] = (qv && d < a.D) ? qp[d] - cp[d] : 0.0f;
+          r[kc][i] = d < a.D ? qp[d] - cp[d] : 0.0f;
         }
     }
 #pragma unroll
@@ -527,11 +537,16 @@ __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
     };
     // one block from the ring: KC products, then the mode's epilogue
     auto block_step = [&](const v4u* __restrict__ sa, const float* __restrict__ sx, uint32_t b) {
+      // every k-chunk read from LDS before the first product: one LDS
+      // round trip per block instead of one per pair of products
+      v4u av[KC];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) av[kc] = sa[kc * 64 + lane];
       v16f acc = {};
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, sa[kc * 64 + lane]), bq[kc], acc, 0, 0,
-                                                     0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, av[kc]), bq[kc], acc, 0, 0, 0);
+      sched_reads_then_mfma<KC>();
       const uint32_t rowb = b * 32 + 4 * half;
       float xs[16];
 #pragma unroll
@@ -567,11 +582,12 @@ __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
 #pragma unroll
           for (int rr = 0; rr < 16; ++rr)
             if (rowb + 8 * (rr >> 2) + (rr & 3) >= len) passm &= ~(1u << rr);
+        // one entry per lane and block with a passing row: the list
+        // position of the lane's row base, the probe index and the 16-row
+        // mask (rows 8(i/4) + i%4 from the base), expanded by the rescoring
         if (__ballot(passm != 0) != 0) {
-          while (passm) {  // a compact loop: the slow path stays small
-            const int rr = __ffs(passm) - 1;
-            passm &= passm - 1;
-            slots[tid * kSlots + nslot] = make_uint2(start + rowb + 8 * (rr >> 2) + (rr & 3), j);
+          if (passm != 0) {
+            slots[tid * kSlots + nslot] = make_uint2(start + rowb, (j << 16) | passm);
             if (++nslot == kSlots) {
               move(kSlots);
               nslot = 0;
@@ -724,9 +740,65 @@ struct RescoreArgs16 {
   float* out_d;
   uint32_t* out_counts;
   int* flags;
-  uint32_t* heavy;   // queries of more than kLight candidates, by the light kernel
+  uint32_t* nexp;    // [nq] candidates of each entry list, expanded (statistics)
+  uint32_t* heavy;   // queries of more than kLight entries, by the light kernel
   uint32_t* nheavy;  // their number (cleared before the light kernel)
 };
+
+// The row offset, from an entry's row base, of the lowest set bit i of its
+// mask: 8(i/4) + i%4 (the MFMA output layout of the lane's 16 rows).
+__device__ __forceinline__ uint32_t entry_row(uint32_t mask) {
+  const uint32_t i = (uint32_t)__ffs(mask) - 1u;
+  return 8u * (i >> 2) + (i & 3u);
+}
+
+// Expands one wave's batch of entries (lane l: entry e, valid v) into its
+// candidates, 64 per round: f(has, key, probe index) is called by every lane
+// each round, has false past the last candidate.  ent and pre: the wave's
+// 64-entry LDS arrays.
+template <class F>
+__device__ __forceinline__ void expand_entries(uint2 e, bool v, uint2* ent, uint32_t* pre, F&& f) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t n = v ? (uint32_t)__popc(e.y & 0xFFFFu) : 0u;
+  uint32_t x = n;  // inclusive prefix over the lanes
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = (uint32_t)__shfl_up((int)x, off);
+    if (lane >= off) x += y;
+  }
+  const uint32_t total = (uint32_t)__shfl((int)x, 63);
+  ent[lane] = e;
+  pre[lane] = x;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  for (uint32_t r0 = 0; r0 < total; r0 += 64) {
+    const uint32_t t = r0 + (uint32_t)lane;
+    const bool has = t < total;
+    uint32_t key = kNoPos, jj = 0;
+    if (has) {
+      uint32_t lo = 0, hi = 63;  // the first entry whose inclusive prefix exceeds t
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (pre[mid] > t) hi = mid;
+        else lo = mid + 1;
+      }
+      const uint2 en = ent[lo];
+      uint32_t m = en.y & 0xFFFFu;
+      for (uint32_t rank = t - (lo ? pre[lo - 1] : 0u); rank > 0; --rank) m &= m - 1;
+      key = en.x + entry_row(m);
+      jj = en.y >> 16;
+    }
+    f(has, key, jj);
+  }
+  __builtin_amdgcn_wave_barrier();  // ent and pre are rewritten by the next batch
+}
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off);
+  return v;
+}
 
 // One table entry from the cached residual row r of the subspace (LDS) and
 // the codeword cw (padded to a multiple of 4 floats): the l2sq_ref order on
@@ -889,13 +961,15 @@ __device__ __forceinline__ float entry_direct(const float* __restrict__ qs, cons
 }
 
 // One wave per query, four queries per workgroup: the queries with at most
-// kLight candidates (the others go to pq16_rescore_kernel) scored and
+// kLight candidate entries (the others go to pq16_rescore_kernel) scored and
 // selected as there.  Writes every query's flag: 1 (table scan) for a
 // residual out of fp16 range or more candidates than slots.
 template <int R, int DS>
 __global__ __launch_bounds__(kT) void pq16_rescore_light_kernel(RescoreArgs16 a, uint64_t nq) {
   __shared__ float qsm[kT / 64][256];
   __shared__ uint2 queue[kT / 64][64];
+  __shared__ uint2 xent[kT / 64][64];
+  __shared__ uint32_t xpre[kT / 64][64];
   const int lane = threadIdx.x & 63;
   const int wave = wave_index();
   const uint64_t q = (uint64_t)blockIdx.x * (kT / 64) + wave;
@@ -916,22 +990,26 @@ __global__ __launch_bounds__(kT) void pq16_rescore_light_kernel(RescoreArgs16 a,
   const uint2* __restrict__ cq = a.cand + q * a.cap;
   const int M = a.M, dsub = DS > 0 ? DS : a.dsub;
   const int ds4 = (dsub + 3) / 4 * 4;
+  uint32_t ncand = 0;
   for (uint32_t c0 = 0; c0 < cnt; c0 += 64) {
     const uint32_t c = c0 + (uint32_t)lane;
-    uint32_t key = kNoPos;
-    float d = f_inf();
-    if (c < cnt) {
-      const uint2 e = cq[c];
-      key = e.x;
-      const uint8_t* __restrict__ code = a.codes + (uint64_t)key * M;
-      const float* __restrict__ cen = a.centroids + (uint64_t)a.probes[q * a.np + e.y] * D;
-      d = adc_order(M, a.order, [&](int m) {
-        return entry_direct<DS>(qs + m * dsub, cen + m * dsub, a.cb4 + ((uint64_t)m * 256 + code[m]) * ds4, dsub);
-      });
-    }
-    tk.offer_queued(d, key, c < cnt, queue[wave], qn);
+    const uint2 e = c < cnt ? cq[c] : make_uint2(0u, 0u);
+    expand_entries(e, c < cnt, xent[wave], xpre[wave], [&](bool has, uint32_t key, uint32_t jj) {
+      float d = f_inf();
+      if (has) {
+        ++ncand;
+        const uint8_t* __restrict__ code = a.codes + (uint64_t)key * M;
+        const float* __restrict__ cen = a.centroids + (uint64_t)a.probes[q * a.np + jj] * D;
+        d = adc_order(M, a.order, [&](int m) {
+          return entry_direct<DS>(qs + m * dsub, cen + m * dsub, a.cb4 + ((uint64_t)m * 256 + code[m]) * ds4, dsub);
+        });
+      }
+      tk.offer_queued(d, key, has, queue[wave], qn);
+    });
   }
   tk.flush(queue[wave], qn);
+  ncand = wave_sum(ncand);
+  if (lane == 0) a.nexp[q] = ncand;
   uint32_t count = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -952,13 +1030,16 @@ __global__ __launch_bounds__(kT) void pq16_rescore_light_kernel(RescoreArgs16 a,
 // q - c_(probe j) are computed once into LDS (rc [np][D]) when they fit
 // (cached), else per candidate.  Queries with a residual out of fp16 range
 // or more candidates than slots are flagged for the table scan.
-// One query of more than kLight candidates, by the whole workgroup.
+// One query of more than kLight candidate entries, by the whole workgroup.
 template <int R, int DS>
 __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q) {
   extern __shared__ float qs[];  // [D], then rc [np][D] when cached
   __shared__ uint2 queue[kT / 64][64];
   __shared__ float md[kT / 64][64 * R];
   __shared__ uint32_t mk[kT / 64][64 * R];
+  __shared__ uint32_t nsum[kT / 64];
+  __shared__ uint2 xent[kT / 64][64];
+  __shared__ uint32_t xpre[kT / 64][64];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -983,30 +1064,34 @@ __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q) 
   const uint2* __restrict__ cq = a.cand + q * a.cap;
   const int M = a.M, dsub = DS > 0 ? DS : a.dsub;
   const int ds4 = (dsub + 3) / 4 * 4;
+  uint32_t ncand = 0;
   for (uint32_t c0 = (uint32_t)wave * 64; c0 < cnt; c0 += kT) {
     const uint32_t c = c0 + (uint32_t)lane;
-    uint32_t key = kNoPos;
-    float d = f_inf();
-    if (c < cnt) {
-      const uint2 e = cq[c];
-      key = e.x;
-      const uint8_t* __restrict__ code = a.codes + (uint64_t)key * M;
-      if (cached) {
-        const float* __restrict__ rr = rc + e.y * D;
-        d = adc_order(M, a.order, [&](int m) {
-          return entry_cached<DS>(rr + m * dsub, a.cb4 + ((uint64_t)m * 256 + code[m]) * ds4, dsub);
-        });
-      } else {
-        const float* __restrict__ cen = a.centroids + (uint64_t)a.probes[q * a.np + e.y] * D;
-        d = adc_order(M, a.order, [&](int m) {
-          return pq_entry(qs + m * dsub, cen + m * dsub, a.codebooks + ((uint64_t)m * 256 + code[m]) * dsub,
-                          dsub);
-        });
+    const uint2 e = c < cnt ? cq[c] : make_uint2(0u, 0u);
+    expand_entries(e, c < cnt, xent[wave], xpre[wave], [&](bool has, uint32_t key, uint32_t jj) {
+      float d = f_inf();
+      if (has) {
+        ++ncand;
+        const uint8_t* __restrict__ code = a.codes + (uint64_t)key * M;
+        if (cached) {
+          const float* __restrict__ rr = rc + jj * D;
+          d = adc_order(M, a.order, [&](int m) {
+            return entry_cached<DS>(rr + m * dsub, a.cb4 + ((uint64_t)m * 256 + code[m]) * ds4, dsub);
+          });
+        } else {
+          const float* __restrict__ cen = a.centroids + (uint64_t)a.probes[q * a.np + jj] * D;
+          d = adc_order(M, a.order, [&](int m) {
+            return pq_entry(qs + m * dsub, cen + m * dsub, a.codebooks + ((uint64_t)m * 256 + code[m]) * dsub,
+                            dsub);
+          });
+        }
       }
-    }
-    tk.offer_queued(d, key, c < cnt, queue[wave], qn);
+      tk.offer_queued(d, key, has, queue[wave], qn);
+    });
   }
   tk.flush(queue[wave], qn);
+  ncand = wave_sum(ncand);
+  if (lane == 0) nsum[wave] = ncand;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     md[wave][r * 64 + lane] = tk.d[r];
@@ -1014,6 +1099,7 @@ __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q) 
   }
   __syncthreads();
   if (wave != 0) return;  // waves 1-3 go on to the caller's barrier
+  if (lane == 0) a.nexp[q] = nsum[0] + nsum[1] + nsum[2] + nsum[3];
   for (int w = 1; w < kT / 64; ++w)
 #pragma unroll
     for (int r = 0; r < R; ++r) tk.offer(md[w][r * 64 + lane], mk[w][r * 64 + lane]);
@@ -1039,16 +1125,16 @@ __global__ __launch_bounds__(kT) void pq16_rescore_kernel(RescoreArgs16 a) {
   }
 }
 
-// One workgroup: stat[0] += queries flagged, stat[2..3] += candidates of
-// the others.
+// One workgroup: stat[0] += queries flagged, stat[2..3] += expanded
+// candidates (ncand) of the others.
 __global__ __launch_bounds__(1024) void pq16_stats_kernel(const int* __restrict__ flags,
-                                                          const uint32_t* __restrict__ ccnt, uint64_t nq,
+                                                          const uint32_t* __restrict__ ncand, uint64_t nq,
                                                           uint32_t* __restrict__ stat) {
   __shared__ unsigned long long red[2][16];
   unsigned long long f = 0, c = 0;
   for (uint64_t q = threadIdx.x; q < nq; q += 1024) {
     if (flags[q]) f += 1;
-    else c += ccnt[q];
+    else c += ncand[q];
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
@@ -1172,6 +1258,19 @@ void Pq16Searcher::reset_stats(hipStream_t s) {
   FDB_HIP(hipGetLastError());
 }
 
+Pq16Searcher::~Pq16Searcher() {
+  for (auto& e : tev_)
+    if (e) (void)hipEventDestroy(e);
+}
+
+void Pq16Searcher::set_timing(bool on) {
+  timing_ = on;
+  screen_ms_ = 0.0f;
+  if (on)
+    for (auto& e : tev_)
+      if (!e) FDB_HIP(hipEventCreate(&e));
+}
+
 void Pq16Searcher::read_stats(uint64_t& fallbacks, uint64_t& candidates, hipStream_t s) {
   fallbacks = candidates = 0;
   if (!stat_.p) return;
@@ -1281,7 +1380,8 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
 #undef FDB_KC
   }
   if (!dense) throw Error(FDB_ERR_HIP, "no screening kernel for this dimension");
-  const unsigned grid = (unsigned)(8 * ncu_);  // workgroups stride over the tiles
+  // workgroups stride over the tiles; a multiple of kXcd * kXcdRun
+  const unsigned grid = (unsigned)std::max<uint64_t>(cdiv(8 * (uint64_t)ncu_, kXcd * kXcdRun), 1) * kXcd * kXcdRun;
 
   // 1. the first lists of each query, every screened value kept; d_k bound
   sort_pairs(0, jlim_.p, capA / 32);
@@ -1313,8 +1413,16 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   sa.tl = tl_.p + tbA;
   sa.qlist = qlist_.p + std::max<uint64_t>(npr, 1);
   sa.blim = 0xFFFFFFFFu;
+  if (timing_) FDB_HIP(hipEventRecord(tev_[0], s));
   hipLaunchKernelGGL(thresh, dim3(grid), dim3(kT), 0, s, sa);
   FDB_HIP(hipGetLastError());
+  if (timing_) {
+    FDB_HIP(hipEventRecord(tev_[1], s));
+    FDB_HIP(hipEventSynchronize(tev_[1]));
+    float ms = 0.0f;
+    FDB_HIP(hipEventElapsedTime(&ms, tev_[0], tev_[1]));
+    screen_ms_ += ms;
+  }
 
   // 3. exact distances of the candidates
   RescoreArgs16 r{};
@@ -1338,6 +1446,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   r.out_d = a.out_d;
   r.out_counts = a.out_counts;
   r.flags = flags_.p;
+  r.nexp = nreal_.p;  // free after the d_k selection
   r.heavy = heavy_.p;
   r.nheavy = nheavy_.p;
   r.cb4 = L.cb4.p;
@@ -1362,7 +1471,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   FDB_HIP(hipGetLastError());
   hipLaunchKernelGGL(rk, dim3((unsigned)std::min<uint64_t>(nq, 4 * (uint64_t)ncu_)), dim3(kT), lds, s, r);
   FDB_HIP(hipGetLastError());
-  hipLaunchKernelGGL(pq16_stats_kernel, dim3(1), dim3(1024), 0, s, flags_.p, ccnt_.p, nq, stat_.p);
+  hipLaunchKernelGGL(pq16_stats_kernel, dim3(1), dim3(1024), 0, s, flags_.p, nreal_.p, nq, stat_.p);
   FDB_HIP(hipGetLastError());
 }
 

@@ -73,7 +73,13 @@ struct Pq16SearchArgs {
 
 class Pq16Searcher {
  public:
-  // Candidate slots per query (a query with more is rescanned exactly).
+  Pq16Searcher() = default;
+  Pq16Searcher(const Pq16Searcher&) = delete;
+  Pq16Searcher& operator=(const Pq16Searcher&) = delete;
+  ~Pq16Searcher();
+  // Candidate entries per query (a query with more is rescanned exactly).
+  // An entry is one lane's passing rows of one block: a row base, the probe
+  // index and a 16-row mask.
   static uint32_t capacity(int k) { return k <= 64 ? 2048u : 16384u; }
   // Screened values kept per query from its first lists for the d_k bound
   // (a multiple of 32): more give a tighter bound and fewer candidates.
@@ -87,9 +93,17 @@ class Pq16Searcher {
   // [0] queries rescanned, [2..3] candidates (64-bit) since reset_stats
   void reset_stats(hipStream_t s);
   void read_stats(uint64_t& fallbacks, uint64_t& candidates, hipStream_t s);
+  // With timing on, search() brackets the threshold screening kernel with
+  // events, waits for it and adds its duration to screen_ms() (cleared by
+  // set_timing).
+  void set_timing(bool on);
+  float screen_ms() const { return screen_ms_; }
 
  private:
   int ncu_ = 0;
+  bool timing_ = false;
+  float screen_ms_ = 0.0f;
+  hipEvent_t tev_[2] = {nullptr, nullptr};
   DevBuf<uint32_t> H_, qoff_, toff_, tl_, jlim_, offA_, nA_, nreal_, ccnt_, stat_, heavy_, nheavy_;
   DevBuf<uint2> qlist_, cand_;
   DevBuf<float> epsA_, bufA_, dkA_;

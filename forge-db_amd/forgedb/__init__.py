@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "fdb_ivfpq_len", "fdb_ivfpq_num_tombstones", "fdb_ivfpq_set_coarse_mode", "fdb_ivf_set_coarse_mode",
     "fdb_ivf_set_search_mode", "fdb_ivf_last_fallbacks", "fdb_ivf_last_search_path",
     "fdb_ivfpq_set_search_mode", "fdb_ivfpq_last_screen_stats", "fdb_ivfpq_last_search_path",
+    "fdb_ivfpq_last_screen_kernel_ms",
     "fdb_bf_create", "fdb_bf_add", "fdb_bf_remove", "fdb_bf_len", "fdb_bf_dimension",
     "fdb_bf_metric", "fdb_bf_load", "fdb_bf_save", "fdb_bf_destroy", "fdb_bf_export",
     "fdb_bf_search", "fdb_bf_batch_search", "fdb_bf_batch_search_device",
@@ -141,6 +142,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fdb_ivfpq_set_search_mode": [_P, C.c_uint32],
         "fdb_ivfpq_last_screen_stats": [_P, _P, _P, _P],
         "fdb_ivfpq_last_search_path": [_P, _P],
+        "fdb_ivfpq_last_screen_kernel_ms": [_P, _P],
         "fdb_ivf_set_coarse_mode": [_P, C.c_uint32],
         "fdb_ivf_set_search_mode": [_P, C.c_uint32],
         "fdb_ivf_last_fallbacks": [_P, _P, _P],
@@ -318,6 +320,13 @@ class IVFPQIndex:
         out = C.c_uint32()
         _check(self._lib, self._lib.fdb_ivfpq_last_search_path(self._h, C.byref(out)))
         return int(out.value)
+
+    def last_screen_kernel_ms(self) -> float:
+        """The threshold screening kernel's duration in the last timed batch
+        (HIP events on its stream; 0 after a table scan)."""
+        out = C.c_float()
+        _check(self._lib, self._lib.fdb_ivfpq_last_screen_kernel_ms(self._h, C.byref(out)))
+        return float(out.value)
 
     def dim(self) -> int:
         return self._dim

@@ -162,6 +162,12 @@ FDB_API fdb_status fdb_ivfpq_set_search_mode(fdb_ivfpq* index, uint32_t mode);
 FDB_API fdb_status fdb_ivfpq_last_screen_stats(fdb_ivfpq* index, void* hip_stream, uint64_t* fallbacks,
                                                uint64_t* candidates);
 FDB_API fdb_status fdb_ivfpq_last_search_path(fdb_ivfpq* index, uint32_t* out);
+/* Measurement (no counterpart in the reference): the duration in ms of the
+ * screening kernel that tests every probed code against its query's bound
+ * (pq16_screen_kernel, summed over slices) in the last call of
+ * fdb_ivfpq_batch_search_device_timed, from HIP events on the call's
+ * stream; 0 when that call took the table scan. */
+FDB_API fdb_status fdb_ivfpq_last_screen_kernel_ms(fdb_ivfpq* index, float* out);
 
 /* Copies the resident artifacts back (any pointer may be NULL). */
 FDB_API fdb_status fdb_ivfpq_export(const fdb_ivfpq* index, float* centroids, float* codebooks,
