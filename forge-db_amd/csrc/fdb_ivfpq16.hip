@@ -200,8 +200,27 @@ __device__ __forceinline__ bool pair_list(const PairSet& s, uint32_t e, uint32_t
   return true;
 }
 
-__global__ __launch_bounds__(kT) void pq16_count_kernel(PairSet s, uint32_t* __restrict__ H) {
+// Both stages in one launch each (grid y = stage): 0 pairs the first lists
+// (jlim), 1 every probe.  Stage st uses H + st*G*nlist, qoff and toff +
+// st*(nlist+1), qlist + st*npr and tl + st*tl1.
+struct PairStages {
+  PairSet s0, s1;
+  uint32_t blim0, blim1;  // blocks screened per list
+  uint32_t G;             // sorting workgroups per stage
+  uint32_t* H;
+  uint32_t* qoff;
+  uint32_t* toff;
+  uint2* qlist;
+  uint32_t* tl;
+  uint64_t npr, tl1;
+};
+
+__device__ __forceinline__ PairSet stage_set(const PairStages& ps, uint32_t st) { return st ? ps.s1 : ps.s0; }
+
+__global__ __launch_bounds__(kT) void pq16_count_kernel(PairStages ps) {
   __shared__ uint32_t hist[kHistMax];
+  const PairSet s = stage_set(ps, blockIdx.y);
+  uint32_t* __restrict__ H = ps.H + (uint64_t)blockIdx.y * ps.G * s.nlist;
   const uint32_t w = blockIdx.x;
   for (uint32_t i = threadIdx.x; i < s.nlist; i += kT) hist[i] = 0;
   __syncthreads();
@@ -215,14 +234,19 @@ __global__ __launch_bounds__(kT) void pq16_count_kernel(PairSet s, uint32_t* __r
   for (uint32_t i = threadIdx.x; i < s.nlist; i += kT) H[(uint64_t)w * s.nlist + i] = hist[i];
 }
 
-// One workgroup of 1024 threads.  cnt_p = sum over w of H[w][p]; qoff =
+// One workgroup of 1024 threads per stage.  cnt_p = sum over w of H[w][p]; qoff =
 // exclusive prefix of cnt; tiles_p = ceil(cnt_p / kTileQ) * ceil(min(nb_p,
 // blim) / kCB) (nb_p = bo[p+1] - bo[p]), toff = their exclusive prefix; both
-// totals at [nlist].  H[w][p] is replaced by the pair base of (w, p).
-__global__ __launch_bounds__(1024) void pq16_offsets_kernel(uint32_t* __restrict__ H, uint32_t G, uint32_t nlist,
-                                                            const uint32_t* __restrict__ bo, uint32_t blim,
-                                                            uint32_t* __restrict__ qoff,
-                                                            uint32_t* __restrict__ toff) {
+// totals at [nlist]; tl[t] = the list of tile t.  H[w][p] is replaced by the
+// pair base of (w, p).
+__global__ __launch_bounds__(1024) void pq16_offsets_kernel(PairStages ps, const uint32_t* __restrict__ bo) {
+  const uint32_t stage = blockIdx.x;
+  const uint32_t nlist = ps.s0.nlist, G = ps.G;
+  const uint32_t blim = stage ? ps.blim1 : ps.blim0;
+  uint32_t* __restrict__ H = ps.H + (uint64_t)stage * G * nlist;
+  uint32_t* __restrict__ qoff = ps.qoff + (uint64_t)stage * (nlist + 1);
+  uint32_t* __restrict__ toff = ps.toff + (uint64_t)stage * (nlist + 1);
+  uint32_t* __restrict__ tl = ps.tl + stage * ps.tl1;
   __shared__ uint32_t wq[16], wt[16];
   __shared__ uint32_t carry[2];
   const int tid = threadIdx.x;
@@ -263,6 +287,7 @@ __global__ __launch_bounds__(1024) void pq16_offsets_kernel(uint32_t* __restrict
       uint32_t run = pq + sc - c;
       qoff[i] = run;
       toff[i] = pt + st - t;
+      for (uint32_t u = 0; u < t; ++u) tl[pt + st - t + u] = i;  // the list of each of its tiles
       for (uint32_t w = 0; w < G; ++w) {
         const uint32_t h = H[(uint64_t)w * nlist + i];
         H[(uint64_t)w * nlist + i] = run;
@@ -282,9 +307,11 @@ __global__ __launch_bounds__(1024) void pq16_offsets_kernel(uint32_t* __restrict
   }
 }
 
-__global__ __launch_bounds__(kT) void pq16_scatter_kernel(PairSet s, const uint32_t* __restrict__ base,
-                                                          uint2* __restrict__ qlist) {
+__global__ __launch_bounds__(kT) void pq16_scatter_kernel(PairStages ps) {
   __shared__ uint32_t hist[kHistMax];
+  const PairSet s = stage_set(ps, blockIdx.y);
+  const uint32_t* __restrict__ base = ps.H + (uint64_t)blockIdx.y * ps.G * s.nlist;
+  uint2* __restrict__ qlist = ps.qlist + blockIdx.y * ps.npr;
   const uint32_t w = blockIdx.x;
   for (uint32_t i = threadIdx.x; i < s.nlist; i += kT) hist[i] = 0;
   __syncthreads();
@@ -298,14 +325,6 @@ __global__ __launch_bounds__(kT) void pq16_scatter_kernel(PairSet s, const uint3
       qlist[base[(uint64_t)w * s.nlist + p] + slot] = make_uint2(q, e - q * (uint32_t)s.np);
     }
   }
-}
-
-// Thread per list: the list of each of its tiles (tl [tiles]).
-__global__ __launch_bounds__(kT) void pq16_tiles_kernel(const uint32_t* __restrict__ toff, uint32_t nlist,
-                                                        uint32_t* __restrict__ tl) {
-  const uint32_t p = blockIdx.x * kT + threadIdx.x;
-  if (p >= nlist) return;
-  for (uint32_t t = toff[p]; t < toff[p + 1]; ++t) tl[t] = p;
 }
 
 // Thread per query: the first probes whose lists hold at least k codes
@@ -767,6 +786,10 @@ __device__ __forceinline__ void expand_entries(uint2 e, bool v, uint2* ent, uint
     if (lane >= off) x += y;
   }
   const uint32_t total = (uint32_t)__shfl((int)x, 63);
+  if (total == (uint32_t)__popcll(__ballot(v))) {  // one row per entry (the usual case)
+    f(v, v ? e.x + entry_row(e.y & 0xFFFFu) : kNoPos, e.y >> 16);
+    return;
+  }
   ent[lane] = e;
   pre[lane] = x;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -965,7 +988,7 @@ __device__ __forceinline__ float entry_direct(const float* __restrict__ qs, cons
 // selected as there.  Writes every query's flag: 1 (table scan) for a
 // residual out of fp16 range or more candidates than slots.
 template <int R, int DS>
-__global__ __launch_bounds__(kT) void pq16_rescore_light_kernel(RescoreArgs16 a, uint64_t nq) {
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void pq16_rescore_light_kernel(RescoreArgs16 a, uint64_t nq) {
   __shared__ float qsm[kT / 64][256];
   __shared__ uint2 queue[kT / 64][64];
   __shared__ uint2 xent[kT / 64][64];
@@ -1294,7 +1317,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
     FDB_HIP(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev));
     ncu_ = std::max(v, 1);
   }
-  H_.reserve((uint64_t)kSortWG * nlist);
+  H_.reserve(2ull * kSortWG * nlist);
   qoff_.reserve(2 * (uint64_t)(nlist + 1));
   toff_.reserve(2 * (uint64_t)(nlist + 1));
   qlist_.reserve(2 * std::max<uint64_t>(npr, 1));
@@ -1327,21 +1350,26 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   };
   const uint64_t tbA = tile_bound(capA / 32), tbB = tile_bound(0xFFFFFFFFu);
   tl_.reserve(std::max<uint64_t>(tbA + tbB, 1));
-  auto sort_pairs = [&](int st, const uint32_t* jlim, uint32_t blim) {
-    PairSet ps{a.probes, nq, np, jlim, nlist, chunk};
-    uint32_t* qoff = qoff_.p + st * (uint64_t)(nlist + 1);
-    uint32_t* toff = toff_.p + st * (uint64_t)(nlist + 1);
-    uint2* ql = qlist_.p + st * std::max<uint64_t>(npr, 1);
-    hipLaunchKernelGGL(pq16_count_kernel, dim3(G), dim3(kT), 0, s, ps, H_.p);
-    FDB_HIP(hipGetLastError());
-    hipLaunchKernelGGL(pq16_offsets_kernel, dim3(1), dim3(1024), 0, s, H_.p, G, nlist, L.bo.p, blim, qoff, toff);
-    FDB_HIP(hipGetLastError());
-    hipLaunchKernelGGL(pq16_scatter_kernel, dim3(G), dim3(kT), 0, s, ps, H_.p, ql);
-    FDB_HIP(hipGetLastError());
-    hipLaunchKernelGGL(pq16_tiles_kernel, dim3((unsigned)cdiv(nlist, kT)), dim3(kT), 0, s, toff, nlist,
-                       tl_.p + (st ? tbA : 0));
-    FDB_HIP(hipGetLastError());
-  };
+  // both stages' pairs grouped by list: 0 the first lists, 1 every probe
+  PairStages pst{};
+  pst.s0 = PairSet{a.probes, nq, np, jlim_.p, nlist, chunk};
+  pst.s1 = PairSet{a.probes, nq, np, nullptr, nlist, chunk};
+  pst.blim0 = capA / 32;
+  pst.blim1 = 0xFFFFFFFFu;
+  pst.G = G;
+  pst.H = H_.p;
+  pst.qoff = qoff_.p;
+  pst.toff = toff_.p;
+  pst.qlist = qlist_.p;
+  pst.tl = tl_.p;
+  pst.npr = std::max<uint64_t>(npr, 1);
+  pst.tl1 = tbA;
+  hipLaunchKernelGGL(pq16_count_kernel, dim3(G, 2), dim3(kT), 0, s, pst);
+  FDB_HIP(hipGetLastError());
+  hipLaunchKernelGGL(pq16_offsets_kernel, dim3(2), dim3(1024), 0, s, pst, L.bo.p);
+  FDB_HIP(hipGetLastError());
+  hipLaunchKernelGGL(pq16_scatter_kernel, dim3(G, 2), dim3(kT), 0, s, pst);
+  FDB_HIP(hipGetLastError());
 
   ScreenArgs sa{};
   sa.queries = a.queries;
@@ -1384,7 +1412,6 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   const unsigned grid = (unsigned)std::max<uint64_t>(cdiv(8 * (uint64_t)ncu_, kXcd * kXcdRun), 1) * kXcd * kXcdRun;
 
   // 1. the first lists of each query, every screened value kept; d_k bound
-  sort_pairs(0, jlim_.p, capA / 32);
   sa.qoff = qoff_.p;
   sa.toff = toff_.p;
   sa.tl = tl_.p;
@@ -1407,7 +1434,6 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   FDB_HIP(hipGetLastError());
 
   // 2. every probed list against the bound
-  sort_pairs(1, nullptr, 0xFFFFFFFFu);
   sa.qoff = qoff_.p + (nlist + 1);
   sa.toff = toff_.p + (nlist + 1);
   sa.tl = tl_.p + tbA;
