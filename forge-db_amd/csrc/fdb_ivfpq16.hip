@@ -8,6 +8,7 @@
 //                      the probed (query, probe) pairs grouped by list
 // pq16_screen_kernel   fp16 products of residuals and codes, threshold test,
 //                      candidate append
+// pq16_classify_kernel the queries' flags and rescoring order
 // pq16_rescore_kernel  exact table distances of the candidates in the
 //                      reference's order (pq.rs:149-189 entries, :218-245 or
 //                      :318-485 sums) and the final top k
@@ -179,6 +180,7 @@ constexpr uint32_t kXcdRun = 4;      // consecutive tiles given to one XCD
 constexpr int kSlots = 8;            // candidate slots per lane in LDS
 constexpr int kNS = 4;               // one-block stages in the screening kernel's LDS ring
 constexpr uint32_t kLight = 512;     // candidate entries rescored by one wave (more: four)
+constexpr uint32_t kRound = 64;      // entries of one rescoring round
 
 struct PairSet {
   const int32_t* probes;
@@ -337,9 +339,9 @@ __global__ __launch_bounds__(kT) void pq16_plan_kernel(const int32_t* __restrict
                                                        uint32_t* __restrict__ offA, uint32_t* __restrict__ nA,
                                                        uint32_t* __restrict__ nreal, uint32_t* __restrict__ ccnt,
                                                        int* __restrict__ force, float* __restrict__ epsA,
-                                                       uint32_t* __restrict__ nheavy) {
+                                                       uint32_t* __restrict__ counters) {
   const uint64_t q = (uint64_t)blockIdx.x * kT + threadIdx.x;
-  if (q == 0) *nheavy = 0;
+  if (q < 3) counters[q] = 0;
   if (q >= nq) return;
   ccnt[q] = 0;  // the query's counters and bounds start clear
   force[q] = 0;
@@ -760,8 +762,9 @@ struct RescoreArgs16 {
   uint32_t* out_counts;
   int* flags;
   uint32_t* nexp;    // [nq] candidates of each entry list, expanded (statistics)
-  uint32_t* heavy;   // queries of more than kLight entries, by the light kernel
-  uint32_t* nheavy;  // their number (cleared before the light kernel)
+  const uint32_t* heavy;     // queries of more than kLight entries
+  const uint32_t* qorder;    // the other queries: counters[1] at the front, counters[2] at the back
+  const uint32_t* counters;  // pq16_classify_kernel's
 };
 
 // The row offset, from an entry's row base, of the lowest set bit i of its
@@ -983,29 +986,59 @@ __device__ __forceinline__ float entry_direct(const float* __restrict__ qs, cons
   }
 }
 
-// One wave per query, four queries per workgroup: the queries with at most
-// kLight candidate entries (the others go to pq16_rescore_kernel) scored and
-// selected as there.  Writes every query's flag: 1 (table scan) for a
-// residual out of fp16 range or more candidates than slots.
+// Thread per query: its flag (1: table scan, for a residual out of fp16
+// range or more candidate entries than slots) and its place in the
+// rescoring: more than kLight entries, the heavy list (a workgroup each);
+// more than kRound, the front of order; else its back (filled from the end),
+// so that the longer lists start first.  counters: [0] heavy, [1] front,
+// [2] back.  One atomic per class and wave.
+__global__ __launch_bounds__(kT) void pq16_classify_kernel(const uint32_t* __restrict__ ccnt,
+                                                           const int* __restrict__ force, uint32_t cap,
+                                                           uint64_t nq, int* __restrict__ flags,
+                                                           uint32_t* __restrict__ order,
+                                                           uint32_t* __restrict__ heavy,
+                                                           uint32_t* __restrict__ counters) {
+  const uint64_t q = (uint64_t)blockIdx.x * kT + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const bool valid = q < nq;
+  const uint32_t cnt = valid ? ccnt[q] : 0u;
+  const bool fall = valid && (force[q] != 0 || cnt > cap);
+  if (valid) flags[q] = fall ? 1 : 0;
+  const int cls = (!valid || fall) ? -1 : (cnt > kLight ? 0 : (cnt > kRound ? 1 : 2));
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const uint64_t m = __ballot(cls == c);
+    if (m == 0) continue;
+    const int leader = __ffsll((long long)m) - 1;
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd(&counters[c], (uint32_t)__popcll(m));
+    base = (uint32_t)__shfl((int)base, leader);
+    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    if (cls == c) {
+      if (c == 0) heavy[base + rank] = (uint32_t)q;
+      else if (c == 1) order[base + rank] = (uint32_t)q;
+      else order[nq - 1 - (base + rank)] = (uint32_t)q;
+    }
+  }
+}
+
+// One wave per query (have: the wave has one): a query of at most kLight
+// candidate entries scored and selected as in pq16_rescore_heavy.  Every wave
+// of the workgroup calls it (one workgroup barrier).
 template <int R, int DS>
-__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void pq16_rescore_light_kernel(RescoreArgs16 a, uint64_t nq) {
+__device__ __forceinline__ void pq16_rescore_light(const RescoreArgs16& a, uint64_t q, bool have) {
   __shared__ float qsm[kT / 64][256];
   __shared__ uint2 queue[kT / 64][64];
   __shared__ uint2 xent[kT / 64][64];
   __shared__ uint32_t xpre[kT / 64][64];
   const int lane = threadIdx.x & 63;
   const int wave = wave_index();
-  const uint64_t q = (uint64_t)blockIdx.x * (kT / 64) + wave;
-  const bool have = q < nq;
   const uint32_t cnt = have ? a.ccnt[q] : 0u;
-  const bool fall = have && (a.force[q] != 0 || cnt > a.cap);
-  if (have && lane == 0) a.flags[q] = fall ? 1 : 0;
   const int D = a.D;
   if (have)
     for (int d = lane; d < D; d += 64) qsm[wave][d] = a.queries[q * D + d];
   __syncthreads();
-  if (have && !fall && cnt > kLight && lane == 0) a.heavy[atomicAdd(a.nheavy, 1u)] = (uint32_t)q;
-  if (!have || fall || cnt > kLight) return;
+  if (!have) return;
   const float* __restrict__ qs = qsm[wave];
   WaveTopK<R> tk;
   tk.init(a.k);
@@ -1140,12 +1173,23 @@ __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q) 
   if (lane == 0) a.out_counts[q] = count;
 }
 
+// Workgroups [0, nh) take the heavy list, one query at a time; the others
+// four queries of order each, the longer lists (front) dispatched first.
 template <int R, int DS>
-__global__ __launch_bounds__(kT) void pq16_rescore_kernel(RescoreArgs16 a) {
-  for (uint32_t h = blockIdx.x; h < *a.nheavy; h += gridDim.x) {
-    pq16_rescore_heavy<R, DS>(a, a.heavy[h]);
-    __syncthreads();  // the LDS is reused by the next query
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void pq16_rescore_kernel(RescoreArgs16 a,
+                                                                                                   uint64_t nq,
+                                                                                                   uint32_t nh) {
+  if (blockIdx.x < nh) {
+    for (uint32_t h = blockIdx.x; h < a.counters[0]; h += nh) {
+      pq16_rescore_heavy<R, DS>(a, a.heavy[h]);
+      __syncthreads();  // the LDS is reused by the next query
+    }
+    return;
   }
+  const uint64_t i = (uint64_t)(blockIdx.x - nh) * (kT / 64) + wave_index();
+  const uint32_t nf = a.counters[1], nb = a.counters[2];
+  const bool have = i < nq && (i < nf || i >= nq - nb);
+  pq16_rescore_light<R, DS>(a, have ? a.qorder[i] : 0, have);
 }
 
 // One workgroup: stat[0] += queries flagged, stat[2..3] += expanded
@@ -1335,7 +1379,8 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   flags_.reserve(nq);
   if (!stat_.p) reset_stats(s);
   heavy_.reserve(nq);
-  nheavy_.reserve(1);
+  nheavy_.reserve(3);
+  order_.reserve(nq);
   hipLaunchKernelGGL(pq16_plan_kernel, dim3((unsigned)cdiv(nq, kT)), dim3(kT), 0, s, a.probes, nq, np, nlist,
                      a.list_off, a.k, capA, jlim_.p, offA_.p, nA_.p, nreal_.p, ccnt_.p, force_.p, epsA_.p,
                      nheavy_.p);
@@ -1474,28 +1519,27 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   r.flags = flags_.p;
   r.nexp = nreal_.p;  // free after the d_k selection
   r.heavy = heavy_.p;
-  r.nheavy = nheavy_.p;
+  r.qorder = order_.p;
+  r.counters = nheavy_.p;
   r.cb4 = L.cb4.p;
   r.nlist = (int)nlist;
-  r.cached = (uint64_t)np * L.D * sizeof(float) <= 48 * 1024;
+  r.cached = (uint64_t)np * L.D * sizeof(float) <= 32 * 1024;
   const size_t lds = sizeof(float) * ((size_t)L.D + (r.cached ? (size_t)np * L.D : 0));
   const int ds = (L.dsub == 3 || L.dsub == 4 || L.dsub == 8) ? L.dsub : 0;
-  void (*rk)(RescoreArgs16) = nullptr;
-  void (*lk)(RescoreArgs16, uint64_t) = nullptr;
+  void (*rk)(RescoreArgs16, uint64_t, uint32_t) = nullptr;
 #define FDB_RS(n)                                                                       \
   case n:                                                                               \
     rk = ds == 3 ? pq16_rescore_kernel<n, 3>                                            \
                  : (ds == 4 ? pq16_rescore_kernel<n, 4>                                 \
                             : (ds == 8 ? pq16_rescore_kernel<n, 8> : pq16_rescore_kernel<n, 0>)); \
-    lk = ds == 3 ? pq16_rescore_light_kernel<n, 3>                                      \
-                 : (ds == 4 ? pq16_rescore_light_kernel<n, 4>                           \
-                            : (ds == 8 ? pq16_rescore_light_kernel<n, 8> : pq16_rescore_light_kernel<n, 0>)); \
     break;
   switch (R) { FDB_RS(1) FDB_RS(2) FDB_RS(4) FDB_RS(8) FDB_RS(16) }
 #undef FDB_RS
-  hipLaunchKernelGGL(lk, dim3((unsigned)cdiv(nq, kT / 64)), dim3(kT), 0, s, r, nq);
+  hipLaunchKernelGGL(pq16_classify_kernel, dim3((unsigned)cdiv(nq, kT)), dim3(kT), 0, s, ccnt_.p, force_.p, cap, nq,
+                     flags_.p, order_.p, heavy_.p, nheavy_.p);
   FDB_HIP(hipGetLastError());
-  hipLaunchKernelGGL(rk, dim3((unsigned)std::min<uint64_t>(nq, 4 * (uint64_t)ncu_)), dim3(kT), lds, s, r);
+  const uint32_t nh = (uint32_t)std::min<uint64_t>(nq, 2 * (uint64_t)ncu_);  // heavy-list workgroups
+  hipLaunchKernelGGL(rk, dim3((unsigned)(nh + cdiv(nq, kT / 64))), dim3(kT), lds, s, r, nq, nh);
   FDB_HIP(hipGetLastError());
   hipLaunchKernelGGL(pq16_stats_kernel, dim3(1), dim3(1024), 0, s, flags_.p, nreal_.p, nq, stat_.p);
   FDB_HIP(hipGetLastError());
