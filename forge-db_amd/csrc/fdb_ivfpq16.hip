@@ -29,7 +29,12 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // 8 halves as a native vector
 
 constexpr int kT = 256;
-constexpr int kTileQ = 128;  // (query, probe) pairs per screening workgroup: 4 waves x 32
+// (query, probe) pairs per screening workgroup, 32 per wave: 4 waves for the
+// first lists (few pairs per list); for every probe, 8 waves up to 96
+// dimensions (KC <= 6), else 4 (measured: 8 waves took C5's 10M x 96 screen
+// from 2.4 to 2.1-2.3 ms and C3's 1M x 128 one from 0.23 to 0.26 ms)
+constexpr int kWavesA = 4;
+constexpr int waves_b(int KC) { return KC <= 6 ? 8 : 4; }
 
 uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
@@ -208,6 +213,7 @@ __device__ __forceinline__ bool pair_list(const PairSet& s, uint32_t e, uint32_t
 struct PairStages {
   PairSet s0, s1;
   uint32_t blim0, blim1;  // blocks screened per list
+  uint32_t tq0, tq1;      // pairs per tile
   uint32_t G;             // sorting workgroups per stage
   uint32_t* H;
   uint32_t* qoff;
@@ -237,7 +243,7 @@ __global__ __launch_bounds__(kT) void pq16_count_kernel(PairStages ps) {
 }
 
 // One workgroup of 1024 threads per stage.  cnt_p = sum over w of H[w][p]; qoff =
-// exclusive prefix of cnt; tiles_p = ceil(cnt_p / kTileQ) * ceil(min(nb_p,
+// exclusive prefix of cnt; tiles_p = ceil(cnt_p / tq) * ceil(min(nb_p,
 // blim) / kCB) (nb_p = bo[p+1] - bo[p]), toff = their exclusive prefix; both
 // totals at [nlist]; tl[t] = the list of tile t.  H[w][p] is replaced by the
 // pair base of (w, p).
@@ -245,6 +251,7 @@ __global__ __launch_bounds__(1024) void pq16_offsets_kernel(PairStages ps, const
   const uint32_t stage = blockIdx.x;
   const uint32_t nlist = ps.s0.nlist, G = ps.G;
   const uint32_t blim = stage ? ps.blim1 : ps.blim0;
+  const uint32_t tq = stage ? ps.tq1 : ps.tq0;
   uint32_t* __restrict__ H = ps.H + (uint64_t)stage * G * nlist;
   uint32_t* __restrict__ qoff = ps.qoff + (uint64_t)stage * (nlist + 1);
   uint32_t* __restrict__ toff = ps.toff + (uint64_t)stage * (nlist + 1);
@@ -263,7 +270,7 @@ __global__ __launch_bounds__(1024) void pq16_offsets_kernel(PairStages ps, const
 #pragma unroll 4
       for (uint32_t w = 0; w < G; ++w) c += H[(uint64_t)w * nlist + i];
       const uint32_t nb = min(bo[i + 1] - bo[i], blim);
-      t = (c + kTileQ - 1) / kTileQ * ((nb + kCB - 1) / kCB);
+      t = (c + tq - 1) / tq * ((nb + kCB - 1) / kCB);
     }
     uint32_t sc = c, st = t;  // inclusive wave scans
 #pragma unroll
@@ -428,9 +435,11 @@ __device__ __forceinline__ float add_up(float a, float b) {
 //   Dense mode: s = fma(.., acc, |r|^2 + |x^|^2) of every code is written
 //   to the pair's 32-aligned range of the query's buffer (+inf past the
 //   list's end, nothing past capA), four rows per 16-byte store.
-template <int KC, bool DENSE>
-__global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
-  constexpr int kUW = (KC + 3) / 4;  // k-chunk loads per wave per block
+template <int KC, bool DENSE, int NW>
+__global__ __launch_bounds__(64 * NW) void pq16_screen_kernel(ScreenArgs a) {
+  // NW: waves per workgroup
+  constexpr uint32_t TQ = 32 * NW;               // pairs per tile
+  constexpr int kUW = (KC + NW - 1) / NW;         // k-chunk loads per wave per block
   // s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
   // at their maxima): all but the newest (kNS - 2) blocks' loads, and all
   constexpr int kRingLoads = (kNS - 2) * (kUW + 1);
@@ -442,7 +451,7 @@ __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
   __shared__ float dxn[64];
   // threshold mode: lane-private candidate slots, moved to the query's list
   // when full and at the end of each tile (one reservation per move)
-  __shared__ uint2 slots[DENSE ? 1 : kT * kSlots];
+  __shared__ uint2 slots[DENSE ? 1 : 64 * NW * kSlots];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = wave_index();
@@ -459,14 +468,14 @@ __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
   for (uint32_t t = slot; t < ntiles; t += gridDim.x) {
     const uint32_t p = a.tl[t];
     const uint32_t qb = a.qoff[p], qend = a.qoff[p + 1];
-    const uint32_t nqt = (qend - qb + kTileQ - 1) / kTileQ;
+    const uint32_t nqt = (qend - qb + TQ - 1) / TQ;
     const uint32_t local = t - a.toff[p];
     const uint32_t chunk = local / nqt;
-    // groups of 32 pairs in the tile; with fewer than four, the waves of a
-    // group take every split-th block of the stage
-    const uint32_t tq0 = qb + (local - chunk * nqt) * kTileQ;
-    const uint32_t ng = min((qend - tq0 + 31) / 32, 4u);
-    const int split = ng == 1 ? 4 : (ng == 2 ? 2 : 1);
+    // groups of 32 pairs in the tile; with fewer than NW, each group has
+    // split waves, which take every split-th block of the chunk
+    const uint32_t tq0 = qb + (local - chunk * nqt) * TQ;
+    const uint32_t ng = min((qend - tq0 + 31) / 32, (uint32_t)NW);
+    const int split = NW / (ng == 1 ? 1 : (ng == 2 ? 2 : (ng <= 4 ? 4 : 8)));
     const int phase = wave % split;
     const uint32_t q0 = tq0 + (uint32_t)(wave / split) * 32;
     const bool busy = q0 < qend;  // wave-uniform: the wave has pairs
@@ -619,7 +628,7 @@ __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
     };
     // The chunk's blocks stream through a ring of kNS one-block LDS buffers
     // by direct global-to-LDS loads; block bb + s lands in ring[s % kNS].
-    // Every wave issues kUW + 1 loads per block (k-chunks w, w+4, ...;
+    // Every wave issues kUW + 1 loads per block (k-chunks w, w+NW, ...;
     // wave 0 also the block's |x^|^2; spare loads re-read into a dummy
     // buffer), so waiting for all but the last (kNS-2) blocks' loads is one
     // immediate count.  Blocks past the chunk's end re-read its last block.
@@ -628,7 +637,7 @@ __global__ __launch_bounds__(kT) void pq16_screen_kernel(ScreenArgs a) {
     {                                                                                                   \
       const uint32_t bl = bb + min((uint32_t)(S), nst - 1);                                             \
       _Pragma("unroll") for (int i = 0; i < kUW; ++i) {                                                 \
-        const int u = wave + 4 * i;                                                                     \
+        const int u = wave + NW * i;                                                                    \
         if (u < KC)                                                                                     \
           lds_load16(A + ((uint64_t)bl * KC + u) * 64 + lane, &ring[BUF][u * 64]);                     \
         else                                                                                            \
@@ -1193,10 +1202,10 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void pq
 }
 
 // One workgroup: stat[0] += queries flagged, stat[2..3] += expanded
-// candidates (ncand) of the others.
+// candidates (ncand) of the others (= with clear).
 __global__ __launch_bounds__(1024) void pq16_stats_kernel(const int* __restrict__ flags,
                                                           const uint32_t* __restrict__ ncand, uint64_t nq,
-                                                          uint32_t* __restrict__ stat) {
+                                                          int clear, uint32_t* __restrict__ stat) {
   __shared__ unsigned long long red[2][16];
   unsigned long long f = 0, c = 0;
   for (uint64_t q = threadIdx.x; q < nq; q += 1024) {
@@ -1219,8 +1228,13 @@ __global__ __launch_bounds__(1024) void pq16_stats_kernel(const int* __restrict_
       f += red[0][w];
       c += red[1][w];
     }
-    atomicAdd(&stat[0], (uint32_t)f);
-    atomicAdd(reinterpret_cast<unsigned long long*>(&stat[2]), c);
+    if (clear) {
+      stat[0] = (uint32_t)f;
+      *reinterpret_cast<unsigned long long*>(&stat[2]) = c;
+    } else {
+      stat[0] += (uint32_t)f;
+      *reinterpret_cast<unsigned long long*>(&stat[2]) += c;
+    }
   }
 }
 
@@ -1319,10 +1333,21 @@ void Pq16Lists::build(const float* d_codebooks, const uint8_t* d_codes, const ui
   ok = true;
 }
 
-void Pq16Searcher::reset_stats(hipStream_t s) {
+void Pq16Searcher::reset_stats(hipStream_t) {
   stat_.reserve(4);
-  hipLaunchKernelGGL(pq16_fill_u32, dim3(1), dim3(kT), 0, s, stat_.p, (uint64_t)4, 0u);
+  clear_ = true;
+  pending_nq_ = 0;
+}
+
+// The statistics of the last slice searched, from its flags and candidate
+// counts (before the next slice overwrites them).
+void Pq16Searcher::flush_stats(hipStream_t s) {
+  if (pending_nq_ == 0) return;
+  hipLaunchKernelGGL(pq16_stats_kernel, dim3(1), dim3(1024), 0, s, flags_.p, nreal_.p, pending_nq_, clear_ ? 1 : 0,
+                     stat_.p);
   FDB_HIP(hipGetLastError());
+  clear_ = false;
+  pending_nq_ = 0;
 }
 
 Pq16Searcher::~Pq16Searcher() {
@@ -1340,7 +1365,8 @@ void Pq16Searcher::set_timing(bool on) {
 
 void Pq16Searcher::read_stats(uint64_t& fallbacks, uint64_t& candidates, hipStream_t s) {
   fallbacks = candidates = 0;
-  if (!stat_.p) return;
+  flush_stats(s);
+  if (!stat_.p || clear_) return;
   uint32_t v[4] = {0, 0, 0, 0};
   FDB_HIP(hipMemcpyAsync(v, stat_.p, 16, hipMemcpyDeviceToHost, s));
   FDB_HIP(hipStreamSynchronize(s));
@@ -1378,6 +1404,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   force_.reserve(nq);
   flags_.reserve(nq);
   if (!stat_.p) reset_stats(s);
+  flush_stats(s);  // the previous slice's, before its buffers are reused
   heavy_.reserve(nq);
   nheavy_.reserve(3);
   order_.reserve(nq);
@@ -1391,7 +1418,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   const uint64_t chunk = cdiv(npr, G);
   // tiles of a stage: at most (pairs / 128 + lists) pair tiles per chunk
   auto tile_bound = [&](uint32_t blim) {
-    return (cdiv(npr, kTileQ) + nlist) * cdiv(std::min<uint64_t>(L.max_blocks, blim), kCB);
+    return (cdiv(npr, 32 * kWavesA) + nlist) * cdiv(std::min<uint64_t>(L.max_blocks, blim), kCB);
   };
   const uint64_t tbA = tile_bound(capA / 32), tbB = tile_bound(0xFFFFFFFFu);
   tl_.reserve(std::max<uint64_t>(tbA + tbB, 1));
@@ -1401,6 +1428,8 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   pst.s1 = PairSet{a.probes, nq, np, nullptr, nlist, chunk};
   pst.blim0 = capA / 32;
   pst.blim1 = 0xFFFFFFFFu;
+  pst.tq0 = 32 * kWavesA;
+  pst.tq1 = 32 * waves_b(L.KC);
   pst.G = G;
   pst.H = H_.p;
   pst.qoff = qoff_.p;
@@ -1445,8 +1474,8 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   switch (L.KC) {
 #define FDB_KC(n)                                  \
   case n:                                          \
-    dense = pq16_screen_kernel<n, true>;           \
-    thresh = pq16_screen_kernel<n, false>;         \
+    dense = pq16_screen_kernel<n, true, kWavesA>;   \
+    thresh = pq16_screen_kernel<n, false, waves_b(n)>; \
     break;
     FDB_KC(1) FDB_KC(2) FDB_KC(3) FDB_KC(4) FDB_KC(5) FDB_KC(6) FDB_KC(7) FDB_KC(8)
     FDB_KC(9) FDB_KC(10) FDB_KC(11) FDB_KC(12) FDB_KC(13) FDB_KC(14) FDB_KC(15) FDB_KC(16)
@@ -1462,7 +1491,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   sa.tl = tl_.p;
   sa.qlist = qlist_.p;
   sa.blim = capA / 32;
-  hipLaunchKernelGGL(dense, dim3(grid), dim3(kT), 0, s, sa);
+  hipLaunchKernelGGL(dense, dim3(grid), dim3(64 * kWavesA), 0, s, sa);
   FDB_HIP(hipGetLastError());
   const int R = list_regs(a.k);
   switch (R) {
@@ -1485,7 +1514,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   sa.qlist = qlist_.p + std::max<uint64_t>(npr, 1);
   sa.blim = 0xFFFFFFFFu;
   if (timing_) FDB_HIP(hipEventRecord(tev_[0], s));
-  hipLaunchKernelGGL(thresh, dim3(grid), dim3(kT), 0, s, sa);
+  hipLaunchKernelGGL(thresh, dim3(grid), dim3(64 * waves_b(L.KC)), 0, s, sa);
   FDB_HIP(hipGetLastError());
   if (timing_) {
     FDB_HIP(hipEventRecord(tev_[1], s));
@@ -1541,8 +1570,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   const uint32_t nh = (uint32_t)std::min<uint64_t>(nq, 2 * (uint64_t)ncu_);  // heavy-list workgroups
   hipLaunchKernelGGL(rk, dim3((unsigned)(nh + cdiv(nq, kT / 64))), dim3(kT), lds, s, r, nq, nh);
   FDB_HIP(hipGetLastError());
-  hipLaunchKernelGGL(pq16_stats_kernel, dim3(1), dim3(1024), 0, s, flags_.p, nreal_.p, nq, stat_.p);
-  FDB_HIP(hipGetLastError());
+  pending_nq_ = nq;  // counted by flush_stats
 }
 
 }  // namespace fdb

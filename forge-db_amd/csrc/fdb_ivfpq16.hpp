@@ -90,7 +90,8 @@ class Pq16Searcher {
   // 1 for the queries left to the exact scan, 0 for those written.
   void search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream_t s);
   const int* flags() const { return flags_.p; }
-  // [0] queries rescanned, [2..3] candidates (64-bit) since reset_stats
+  // Queries rescanned and candidates rescored since reset_stats, counted
+  // when read (or when the next slice is searched).
   void reset_stats(hipStream_t s);
   void read_stats(uint64_t& fallbacks, uint64_t& candidates, hipStream_t s);
   // With timing on, search() brackets the threshold screening kernel with
@@ -100,7 +101,10 @@ class Pq16Searcher {
   float screen_ms() const { return screen_ms_; }
 
  private:
+  void flush_stats(hipStream_t s);
   int ncu_ = 0;
+  bool clear_ = true;        // the next count replaces stat_
+  uint64_t pending_nq_ = 0;  // queries of the last slice, not yet counted
   bool timing_ = false;
   float screen_ms_ = 0.0f;
   hipEvent_t tev_[2] = {nullptr, nullptr};
