@@ -184,7 +184,8 @@ constexpr uint32_t kXcd = 8;         // L2 domains (XCDs); workgroup b runs on X
 constexpr uint32_t kXcdRun = 4;      // consecutive tiles given to one XCD
 constexpr int kSlots = 8;            // candidate slots per lane in LDS
 constexpr int kNS = 4;               // one-block stages in the screening kernel's LDS ring
-constexpr uint32_t kLight = 512;     // candidate entries rescored by one wave (more: four)
+constexpr uint32_t kLight = 256;     // candidate entries rescored by one wave (more: in parts)
+constexpr uint32_t kPart = 256;      // entries of one part of a heavy query (a workgroup)
 constexpr uint32_t kRound = 64;      // entries of one rescoring round
 
 struct PairSet {
@@ -348,7 +349,7 @@ __global__ __launch_bounds__(kT) void pq16_plan_kernel(const int32_t* __restrict
                                                        int* __restrict__ force, float* __restrict__ epsA,
                                                        uint32_t* __restrict__ counters) {
   const uint64_t q = (uint64_t)blockIdx.x * kT + threadIdx.x;
-  if (q < 3) counters[q] = 0;
+  if (q < 4) counters[q] = 0;
   if (q >= nq) return;
   ccnt[q] = 0;  // the query's counters and bounds start clear
   force[q] = 0;
@@ -771,7 +772,11 @@ struct RescoreArgs16 {
   uint32_t* out_counts;
   int* flags;
   uint32_t* nexp;    // [nq] candidates of each entry list, expanded (statistics)
-  const uint32_t* heavy;     // queries of more than kLight entries
+  const uint2* heavy;        // parts of the queries of more than kLight entries:
+                             // (query, part | parts << 16), or (~0, 0) for none
+  uint32_t pmax;             // part slots
+  float* part_d;             // [pmax][k] each part's list, when a query has several
+  uint32_t* part_k;
   const uint32_t* qorder;    // the other queries: counters[1] at the front, counters[2] at the back
   const uint32_t* counters;  // pq16_classify_kernel's
 };
@@ -997,25 +1002,41 @@ __device__ __forceinline__ float entry_direct(const float* __restrict__ qs, cons
 
 // Thread per query: its flag (1: table scan, for a residual out of fp16
 // range or more candidate entries than slots) and its place in the
-// rescoring: more than kLight entries, the heavy list (a workgroup each);
-// more than kRound, the front of order; else its back (filled from the end),
-// so that the longer lists start first.  counters: [0] heavy, [1] front,
-// [2] back.  One atomic per class and wave.
+// rescoring: more than kLight entries, ceil(entries / kPart) parts in the
+// heavy list (a workgroup each; multi-part queries also in multi as (query,
+// first part), merged afterwards); more than kRound, the front of order;
+// else its back (filled from the end), so that the longer lists start
+// first.  counters: [0] heavy parts, [1] front, [2] back, [3] multi.  A
+// query whose parts do not fit the pmax part slots is flagged.
 __global__ __launch_bounds__(kT) void pq16_classify_kernel(const uint32_t* __restrict__ ccnt,
                                                            const int* __restrict__ force, uint32_t cap,
                                                            uint64_t nq, int* __restrict__ flags,
                                                            uint32_t* __restrict__ order,
-                                                           uint32_t* __restrict__ heavy,
+                                                           uint2* __restrict__ heavy, uint32_t pmax,
+                                                           uint2* __restrict__ multi,
+                                                           uint32_t* __restrict__ nexp,
                                                            uint32_t* __restrict__ counters) {
   const uint64_t q = (uint64_t)blockIdx.x * kT + threadIdx.x;
   const int lane = threadIdx.x & 63;
   const bool valid = q < nq;
   const uint32_t cnt = valid ? ccnt[q] : 0u;
-  const bool fall = valid && (force[q] != 0 || cnt > cap);
+  bool fall = valid && (force[q] != 0 || cnt > cap);
+  if (valid && !fall && cnt > kLight) {
+    const uint32_t parts = (cnt + kPart - 1) / kPart;
+    const uint32_t base = atomicAdd(&counters[0], parts);
+    if (base + parts <= pmax) {
+      for (uint32_t i = 0; i < parts; ++i) heavy[base + i] = make_uint2((uint32_t)q, i | (parts << 16));
+      multi[atomicAdd(&counters[3], 1u)] = make_uint2((uint32_t)q, base);
+      nexp[q] = 0;  // the parts add theirs
+    } else {
+      for (uint32_t i = base; i < min(base + parts, pmax); ++i) heavy[i] = make_uint2(~0u, 0u);
+      fall = true;
+    }
+  }
   if (valid) flags[q] = fall ? 1 : 0;
   const int cls = (!valid || fall) ? -1 : (cnt > kLight ? 0 : (cnt > kRound ? 1 : 2));
 #pragma unroll
-  for (int c = 0; c < 3; ++c) {
+  for (int c = 1; c < 3; ++c) {
     const uint64_t m = __ballot(cls == c);
     if (m == 0) continue;
     const int leader = __ffsll((long long)m) - 1;
@@ -1024,8 +1045,7 @@ __global__ __launch_bounds__(kT) void pq16_classify_kernel(const uint32_t* __res
     base = (uint32_t)__shfl((int)base, leader);
     const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
     if (cls == c) {
-      if (c == 0) heavy[base + rank] = (uint32_t)q;
-      else if (c == 1) order[base + rank] = (uint32_t)q;
+      if (c == 1) order[base + rank] = (uint32_t)q;
       else order[nq - 1 - (base + rank)] = (uint32_t)q;
     }
   }
@@ -1095,9 +1115,12 @@ __device__ __forceinline__ void pq16_rescore_light(const RescoreArgs16& a, uint6
 // q - c_(probe j) are computed once into LDS (rc [np][D]) when they fit
 // (cached), else per candidate.  Queries with a residual out of fp16 range
 // or more candidates than slots are flagged for the table scan.
-// One query of more than kLight candidate entries, by the whole workgroup.
+// Part `part` of `parts` (entries [part*kPart, +kPart)) of a query of more
+// than kLight candidate entries, by the whole workgroup; its list goes to
+// part slot `slot` for pq16_merge_kernel.
 template <int R, int DS>
-__device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q) {
+__device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q, uint32_t part, uint32_t parts,
+                                                   uint32_t slot) {
   extern __shared__ float qs[];  // [D], then rc [np][D] when cached
   __shared__ uint2 queue[kT / 64][64];
   __shared__ float md[kT / 64][64 * R];
@@ -1108,11 +1131,11 @@ __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q) 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const uint32_t cnt = a.ccnt[q];
+  const uint32_t e0 = part * kPart, cnt = min(a.ccnt[q], e0 + kPart);
   const int D = a.D;
   float* rc = qs + D;
   // a few candidates are cheaper to rescore without the residual cache
-  const bool cached = a.cached && cnt >= 128;
+  const bool cached = a.cached && cnt - e0 >= 128;
   for (int d = tid; d < D; d += kT) qs[d] = a.queries[q * D + d];
   if (cached) {
     for (int e = tid; e < a.np * D; e += kT) {
@@ -1130,7 +1153,7 @@ __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q) 
   const int M = a.M, dsub = DS > 0 ? DS : a.dsub;
   const int ds4 = (dsub + 3) / 4 * 4;
   uint32_t ncand = 0;
-  for (uint32_t c0 = (uint32_t)wave * 64; c0 < cnt; c0 += kT) {
+  for (uint32_t c0 = e0 + (uint32_t)wave * 64; c0 < cnt; c0 += kT) {
     const uint32_t c = c0 + (uint32_t)lane;
     const uint2 e = c < cnt ? cq[c] : make_uint2(0u, 0u);
     expand_entries(e, c < cnt, xent[wave], xpre[wave], [&](bool has, uint32_t key, uint32_t jj) {
@@ -1164,10 +1187,21 @@ __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q) 
   }
   __syncthreads();
   if (wave != 0) return;  // waves 1-3 go on to the caller's barrier
-  if (lane == 0) a.nexp[q] = nsum[0] + nsum[1] + nsum[2] + nsum[3];
+  if (lane == 0) atomicAdd(&a.nexp[q], nsum[0] + nsum[1] + nsum[2] + nsum[3]);
   for (int w = 1; w < kT / 64; ++w)
 #pragma unroll
     for (int r = 0; r < R; ++r) tk.offer(md[w][r * 64 + lane], mk[w][r * 64 + lane]);
+  if (parts > 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int s = r * 64 + lane;
+      if (s < a.k) {
+        a.part_d[(uint64_t)slot * a.k + s] = tk.d[r];
+        a.part_k[(uint64_t)slot * a.k + s] = tk.p[r];
+      }
+    }
+    return;
+  }
   uint32_t count = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -1189,9 +1223,12 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void pq
                                                                                                    uint64_t nq,
                                                                                                    uint32_t nh) {
   if (blockIdx.x < nh) {
-    for (uint32_t h = blockIdx.x; h < a.counters[0]; h += nh) {
-      pq16_rescore_heavy<R, DS>(a, a.heavy[h]);
-      __syncthreads();  // the LDS is reused by the next query
+    const uint32_t nparts = min(a.counters[0], a.pmax);
+    for (uint32_t h = blockIdx.x; h < nparts; h += nh) {
+      const uint2 it = a.heavy[h];
+      if (it.x == ~0u) continue;  // a query whose parts did not fit (flagged)
+      pq16_rescore_heavy<R, DS>(a, it.x, it.y & 0xFFFFu, it.y >> 16, h);
+      __syncthreads();  // the LDS is reused by the next part
     }
     return;
   }
@@ -1199,6 +1236,44 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void pq
   const uint32_t nf = a.counters[1], nb = a.counters[2];
   const bool have = i < nq && (i < nf || i >= nq - nb);
   pq16_rescore_light<R, DS>(a, have ? a.qorder[i] : 0, have);
+}
+
+// One wave per query of several parts (multi [counters[3]]: query, first
+// part slot): the parts' lists merged by (distance, list position), as one
+// pass over every entry would select.
+template <int R>
+__global__ __launch_bounds__(64) void pq16_merge_kernel(RescoreArgs16 a, const uint2* __restrict__ multi) {
+  __shared__ uint2 queue[64];
+  const int lane = threadIdx.x;
+  for (uint32_t m = blockIdx.x; m < a.counters[3]; m += gridDim.x) {
+    const uint2 mq = multi[m];
+    const uint64_t q = mq.x;
+    const uint32_t parts = (a.ccnt[q] + kPart - 1) / kPart;
+    WaveTopK<R> tk;
+    tk.init(a.k);
+    int qn = 0;
+    for (uint32_t pt = 0; pt < parts; ++pt)
+      for (int r0 = 0; r0 < a.k; r0 += 64) {
+        const int s = r0 + lane;
+        const uint64_t i = (uint64_t)(mq.y + pt) * a.k + s;
+        const uint32_t key = s < a.k ? a.part_k[i] : kNoPos;
+        const bool valid = key != kNoPos;
+        tk.offer_queued(valid ? a.part_d[i] : f_inf(), key, valid, queue, qn);
+      }
+    tk.flush(queue, qn);
+    uint32_t count = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int s = r * 64 + lane;
+      const bool valid = s < a.k && tk.p[r] != kNoPos;
+      count += (uint32_t)__popcll(__ballot(valid));
+      if (s < a.k) {
+        a.out_ids[q * a.k + s] = valid ? a.ids[tk.p[r]] : ~0ull;
+        a.out_d[q * a.k + s] = valid ? tk.d[r] : f_inf();
+      }
+    }
+    if (lane == 0) a.out_counts[q] = count;
+  }
 }
 
 // One workgroup: stat[0] += queries flagged, stat[2..3] += expanded
@@ -1405,8 +1480,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   flags_.reserve(nq);
   if (!stat_.p) reset_stats(s);
   flush_stats(s);  // the previous slice's, before its buffers are reused
-  heavy_.reserve(nq);
-  nheavy_.reserve(3);
+  nheavy_.reserve(4);
   order_.reserve(nq);
   hipLaunchKernelGGL(pq16_plan_kernel, dim3((unsigned)cdiv(nq, kT)), dim3(kT), 0, s, a.probes, nq, np, nlist,
                      a.list_off, a.k, capA, jlim_.p, offA_.p, nA_.p, nreal_.p, ccnt_.p, force_.p, epsA_.p,
@@ -1547,7 +1621,17 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   r.out_counts = a.out_counts;
   r.flags = flags_.p;
   r.nexp = nreal_.p;  // free after the d_k selection
+  // part slots: every heavy part of the slice, within 256 MiB of lists
+  const uint64_t pmax = std::max<uint64_t>(
+      1, std::min<uint64_t>(nq * cdiv(cap, kPart), (256ull << 20) / (8ull * (uint64_t)a.k)));
+  heavy_.reserve(pmax);
+  multi_.reserve(nq);
+  part_d_.reserve(pmax * a.k);
+  part_k_.reserve(pmax * a.k);
   r.heavy = heavy_.p;
+  r.pmax = (uint32_t)pmax;
+  r.part_d = part_d_.p;
+  r.part_k = part_k_.p;
   r.qorder = order_.p;
   r.counters = nheavy_.p;
   r.cb4 = L.cb4.p;
@@ -1565,10 +1649,20 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   switch (R) { FDB_RS(1) FDB_RS(2) FDB_RS(4) FDB_RS(8) FDB_RS(16) }
 #undef FDB_RS
   hipLaunchKernelGGL(pq16_classify_kernel, dim3((unsigned)cdiv(nq, kT)), dim3(kT), 0, s, ccnt_.p, force_.p, cap, nq,
-                     flags_.p, order_.p, heavy_.p, nheavy_.p);
+                     flags_.p, order_.p, heavy_.p, (uint32_t)pmax, multi_.p, nreal_.p, nheavy_.p);
   FDB_HIP(hipGetLastError());
   const uint32_t nh = (uint32_t)std::min<uint64_t>(nq, 2 * (uint64_t)ncu_);  // heavy-list workgroups
   hipLaunchKernelGGL(rk, dim3((unsigned)(nh + cdiv(nq, kT / 64))), dim3(kT), lds, s, r, nq, nh);
+  FDB_HIP(hipGetLastError());
+  const unsigned mg = (unsigned)std::min<uint64_t>(nq, 4 * (uint64_t)ncu_);
+  switch (R) {
+#define FDB_MG(n)                                                                  \
+  case n:                                                                          \
+    hipLaunchKernelGGL(pq16_merge_kernel<n>, dim3(mg), dim3(64), 0, s, r, multi_.p); \
+    break;
+    FDB_MG(1) FDB_MG(2) FDB_MG(4) FDB_MG(8) FDB_MG(16)
+#undef FDB_MG
+  }
   FDB_HIP(hipGetLastError());
   pending_nq_ = nq;  // counted by flush_stats
 }

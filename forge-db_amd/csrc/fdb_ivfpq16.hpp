@@ -108,9 +108,10 @@ class Pq16Searcher {
   bool timing_ = false;
   float screen_ms_ = 0.0f;
   hipEvent_t tev_[2] = {nullptr, nullptr};
-  DevBuf<uint32_t> H_, qoff_, toff_, tl_, jlim_, offA_, nA_, nreal_, ccnt_, stat_, heavy_, nheavy_, order_;
-  DevBuf<uint2> qlist_, cand_;
-  DevBuf<float> epsA_, bufA_, dkA_;
+  DevBuf<uint32_t> H_, qoff_, toff_, tl_, jlim_, offA_, nA_, nreal_, ccnt_, stat_, nheavy_, order_;
+  DevBuf<uint2> qlist_, cand_, heavy_, multi_;
+  DevBuf<uint32_t> part_k_;
+  DevBuf<float> epsA_, bufA_, dkA_, part_d_;
   DevBuf<int> force_, flags_;
 };
 
