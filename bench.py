@@ -274,7 +274,7 @@ def bench_ivfpq(args, w, base, queries):
         roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(tflops / FP16_PEAK_TFLOPS, 4),
                 "traffic": read_traffic(f"ivfpq_screen_{args.workload_tag}_traffic.txt"),
-                "kernel": f"pq16_screen_kernel<{d16 // 16}, false>", "kernel_ms": round(screen_kernel_ms, 4),
+                "kernel": f"pq16_screen_kernel<{d16 // 16}, false, {8 if d16 <= 96 else 4}>", "kernel_ms": round(screen_kernel_ms, 4),
                 "algorithmic_flops": flops, "scan_stage_ms": round(scan_ms, 4),
                 "scan_stage_tflops": round(stage, 1), "adc_code_bytes_per_s": round(achieved * 1e9, 1),
                 "coarse_ms": round(coarse_ms, 4), "fallbacks": fallbacks,
