@@ -917,6 +917,7 @@ __device__ __forceinline__ float adc_order(int M, int order, V v) {
       float lane[8];
 #pragma unroll
       for (int l = 0; l < 8; ++l) lane[l] = v(l);
+#pragma unroll
       for (int b = 1; b < mb; ++b)
 #pragma unroll
         for (int l = 0; l < 8; ++l) lane[l] = lane[l] + v(8 * b + l);
@@ -929,6 +930,7 @@ __device__ __forceinline__ float adc_order(int M, int order, V v) {
   }
   float sum = 0.0f;
   int m = 0;
+#pragma unroll
   for (; m + 4 <= M; m += 4) {
     float t = v(m) + v(m + 1);
     t = t + v(m + 2);
@@ -938,6 +940,30 @@ __device__ __forceinline__ float adc_order(int M, int order, V v) {
   for (; m < M; ++m) sum = sum + v(m);
   return sum;
 }
+
+// A candidate's code row: MM (a multiple of 16, at compile time) bytes read
+// as 16-byte words, else byte by byte from the row.
+template <int MM>
+struct CodeRow {
+  uint32_t w[MM > 0 ? MM / 4 : 1];
+  const uint8_t* row;
+  __device__ __forceinline__ CodeRow(const uint8_t* r) : row(r) {
+    if constexpr (MM > 0) {
+#pragma unroll
+      for (int i = 0; i < MM / 16; ++i) {
+        const uint4 v = reinterpret_cast<const uint4*>(r)[i];
+        w[4 * i] = v.x;
+        w[4 * i + 1] = v.y;
+        w[4 * i + 2] = v.z;
+        w[4 * i + 3] = v.w;
+      }
+    }
+  }
+  __device__ __forceinline__ uint32_t operator[](int m) const {
+    if constexpr (MM > 0) return (w[m >> 2] >> (8 * (m & 3))) & 0xFFu;
+    else return row[m];
+  }
+};
 
 // One table entry from the query (LDS), centroid and padded codeword rows
 // of one subspace, the l2sq_ref order on (q - c) - cw; DS: dsub at compile
@@ -1054,7 +1080,7 @@ __global__ __launch_bounds__(kT) void pq16_classify_kernel(const uint32_t* __res
 // One wave per query (have: the wave has one): a query of at most kLight
 // candidate entries scored and selected as in pq16_rescore_heavy.  Every wave
 // of the workgroup calls it (one workgroup barrier).
-template <int R, int DS>
+template <int R, int DS, int MM>
 __device__ __forceinline__ void pq16_rescore_light(const RescoreArgs16& a, uint64_t q, bool have) {
   __shared__ float qsm[kT / 64][256];
   __shared__ uint2 queue[kT / 64][64];
@@ -1073,7 +1099,7 @@ __device__ __forceinline__ void pq16_rescore_light(const RescoreArgs16& a, uint6
   tk.init(a.k);
   int qn = 0;
   const uint2* __restrict__ cq = a.cand + q * a.cap;
-  const int M = a.M, dsub = DS > 0 ? DS : a.dsub;
+  const int M = MM > 0 ? MM : a.M, dsub = DS > 0 ? DS : a.dsub;
   const int ds4 = (dsub + 3) / 4 * 4;
   uint32_t ncand = 0;
   for (uint32_t c0 = 0; c0 < cnt; c0 += 64) {
@@ -1083,7 +1109,7 @@ __device__ __forceinline__ void pq16_rescore_light(const RescoreArgs16& a, uint6
       float d = f_inf();
       if (has) {
         ++ncand;
-        const uint8_t* __restrict__ code = a.codes + (uint64_t)key * M;
+        const CodeRow<MM> code(a.codes + (uint64_t)key * M);
         const float* __restrict__ cen = a.centroids + (uint64_t)a.probes[q * a.np + jj] * D;
         d = adc_order(M, a.order, [&](int m) {
           return entry_direct<DS>(qs + m * dsub, cen + m * dsub, a.cb4 + ((uint64_t)m * 256 + code[m]) * ds4, dsub);
@@ -1118,7 +1144,7 @@ __device__ __forceinline__ void pq16_rescore_light(const RescoreArgs16& a, uint6
 // Part `part` of `parts` (entries [part*kPart, +kPart)) of a query of more
 // than kLight candidate entries, by the whole workgroup; its list goes to
 // part slot `slot` for pq16_merge_kernel.
-template <int R, int DS>
+template <int R, int DS, int MM>
 __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q, uint32_t part, uint32_t parts,
                                                    uint32_t slot) {
   extern __shared__ float qs[];  // [D], then rc [np][D] when cached
@@ -1150,7 +1176,7 @@ __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q, 
   tk.init(a.k);
   int qn = 0;
   const uint2* __restrict__ cq = a.cand + q * a.cap;
-  const int M = a.M, dsub = DS > 0 ? DS : a.dsub;
+  const int M = MM > 0 ? MM : a.M, dsub = DS > 0 ? DS : a.dsub;
   const int ds4 = (dsub + 3) / 4 * 4;
   uint32_t ncand = 0;
   for (uint32_t c0 = e0 + (uint32_t)wave * 64; c0 < cnt; c0 += kT) {
@@ -1160,7 +1186,7 @@ __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q, 
       float d = f_inf();
       if (has) {
         ++ncand;
-        const uint8_t* __restrict__ code = a.codes + (uint64_t)key * M;
+        const CodeRow<MM> code(a.codes + (uint64_t)key * M);
         if (cached) {
           const float* __restrict__ rr = rc + jj * D;
           d = adc_order(M, a.order, [&](int m) {
@@ -1218,7 +1244,7 @@ __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q, 
 
 // Workgroups [0, nh) take the heavy list, one query at a time; the others
 // four queries of order each, the longer lists (front) dispatched first.
-template <int R, int DS>
+template <int R, int DS, int MM>
 __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void pq16_rescore_kernel(RescoreArgs16 a,
                                                                                                    uint64_t nq,
                                                                                                    uint32_t nh) {
@@ -1227,7 +1253,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void pq
     for (uint32_t h = blockIdx.x; h < nparts; h += nh) {
       const uint2 it = a.heavy[h];
       if (it.x == ~0u) continue;  // a query whose parts did not fit (flagged)
-      pq16_rescore_heavy<R, DS>(a, it.x, it.y & 0xFFFFu, it.y >> 16, h);
+      pq16_rescore_heavy<R, DS, MM>(a, it.x, it.y & 0xFFFFu, it.y >> 16, h);
       __syncthreads();  // the LDS is reused by the next part
     }
     return;
@@ -1235,7 +1261,7 @@ __global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void pq
   const uint64_t i = (uint64_t)(blockIdx.x - nh) * (kT / 64) + wave_index();
   const uint32_t nf = a.counters[1], nb = a.counters[2];
   const bool have = i < nq && (i < nf || i >= nq - nb);
-  pq16_rescore_light<R, DS>(a, have ? a.qorder[i] : 0, have);
+  pq16_rescore_light<R, DS, MM>(a, have ? a.qorder[i] : 0, have);
 }
 
 // One wave per query of several parts (multi [counters[3]]: query, first
@@ -1642,9 +1668,10 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   void (*rk)(RescoreArgs16, uint64_t, uint32_t) = nullptr;
 #define FDB_RS(n)                                                                       \
   case n:                                                                               \
-    rk = ds == 3 ? pq16_rescore_kernel<n, 3>                                            \
-                 : (ds == 4 ? pq16_rescore_kernel<n, 4>                                 \
-                            : (ds == 8 ? pq16_rescore_kernel<n, 8> : pq16_rescore_kernel<n, 0>)); \
+    rk = ds == 3 ? (L.M == 32 ? pq16_rescore_kernel<n, 3, 32> : pq16_rescore_kernel<n, 3, 0>)        \
+                 : (ds == 4 ? pq16_rescore_kernel<n, 4, 0>                                           \
+                            : (ds == 8 ? (L.M == 16 ? pq16_rescore_kernel<n, 8, 16> : pq16_rescore_kernel<n, 8, 0>) \
+                                       : pq16_rescore_kernel<n, 0, 0>));                             \
     break;
   switch (R) { FDB_RS(1) FDB_RS(2) FDB_RS(4) FDB_RS(8) FDB_RS(16) }
 #undef FDB_RS
