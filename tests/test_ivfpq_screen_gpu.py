@@ -168,3 +168,25 @@ def test_screen_auto_mode(small_ivfpq):
     gx.set_search_mode(IVFPQ_AUTO)
     gx.batch_search_arrays(small_ivfpq["queries"], 10)
     assert gx.last_search_path() == 0  # 64 queries x ~5k codes is below the threshold
+
+
+def test_screen_several_slices(small_ivfpq):
+    """k = 100 holds 16,384 queries per slice: 20,000 queries take two
+    slices, whose statistics add up and whose results equal the table
+    scan's."""
+    print("screening in two slices (20,000 queries, k 100)", flush=True)
+    gx = gpu_index(small_ivfpq["art"])
+    gx.set_nprobe(8)
+    rng = np.random.default_rng(11)
+    base = small_ivfpq["base"]
+    q = (base[rng.integers(0, len(base), 20_000)] + rng.normal(0, 4, (20_000, base.shape[1]))).astype(np.float32)
+    got, fb = screened(gx, q, 100, "two slices")
+    _, cand = gx.last_screen_stats()
+    assert cand >= 100 * (len(q) - fb)  # every query settled by screening rescored at least k candidates
+    gx.set_search_mode(IVFPQ_EXACT)
+    same(got, gx.batch_search_arrays(q, 100), "two slices vs table scan")
+    # a second batch of one slice reports its own counts
+    gx.set_search_mode(IVFPQ_SCREEN)
+    gx.batch_search_arrays(q[:500], 100)
+    fb2, cand2 = gx.last_screen_stats()
+    assert fb2 <= 500 and 0 < cand2 < cand
