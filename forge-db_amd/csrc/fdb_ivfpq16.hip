@@ -701,16 +701,36 @@ __global__ __launch_bounds__(64) void pq16_select_kernel(const float* __restrict
   const float4* __restrict__ v = reinterpret_cast<const float4*>(bufA + q * capA);
   const uint32_t n4 = (n + 3) / 4;  // n is a multiple of 32 or capA
   const float4 none = make_float4(f_inf(), f_inf(), f_inf(), f_inf());
+  // k <= 64: each lane's smallest value goes in first; the k-th smallest of
+  // those bounds the k-th overall, so that few of the others get past the
+  // list's threshold (one merge instead of one per 64 early values).  Every
+  // value is offered once either way.
+  uint32_t skip = kNoPos;
+  if constexpr (R == 1) {
+    float mn = f_inf();
+#pragma unroll 1
+    for (uint32_t i0 = 0; i0 < n4; i0 += 64) {
+      const uint32_t il = i0 + (uint32_t)lane;
+      const float4 w = il < n4 ? v[il] : none;
+      const uint32_t i = 4 * il;
+      if (w.x < mn) { mn = w.x; skip = i; }
+      if (w.y < mn) { mn = w.y; skip = i + 1; }
+      if (w.z < mn) { mn = w.z; skip = i + 2; }
+      if (w.w < mn) { mn = w.w; skip = i + 3; }
+    }
+    tk.offer_queued(mn, skip, mn < f_inf(), queue, qn);
+    tk.flush(queue, qn);
+  }
   float4 w = (uint32_t)lane < n4 ? v[lane] : none;
 #pragma unroll 1
   for (uint32_t i0 = 0; i0 < n4; i0 += 64) {
     const uint32_t inext = i0 + 64 + (uint32_t)lane;
     const float4 wn = inext < n4 ? v[inext] : none;  // the next values in flight
     const uint32_t i = 4 * (i0 + (uint32_t)lane);
-    tk.offer_queued(w.x, i, w.x < f_inf(), queue, qn);
-    tk.offer_queued(w.y, i + 1, w.y < f_inf(), queue, qn);
-    tk.offer_queued(w.z, i + 2, w.z < f_inf(), queue, qn);
-    tk.offer_queued(w.w, i + 3, w.w < f_inf(), queue, qn);
+    tk.offer_queued(w.x, i, w.x < f_inf() && i != skip, queue, qn);
+    tk.offer_queued(w.y, i + 1, w.y < f_inf() && i + 1 != skip, queue, qn);
+    tk.offer_queued(w.z, i + 2, w.z < f_inf() && i + 2 != skip, queue, qn);
+    tk.offer_queued(w.w, i + 3, w.w < f_inf() && i + 3 != skip, queue, qn);
     w = wn;
   }
   tk.flush(queue, qn);
