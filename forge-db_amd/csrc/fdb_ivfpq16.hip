@@ -4,14 +4,19 @@
 // pq16_decode_kernel   decoded residuals (codewords of each code, pq.rs:114-139
 //                      inverted) to fp16 MFMA blocks, per list
 // pq16_norms_kernel    |x^|^2 per code and the largest per list
+// pq16_plan_kernel     each query's first lists and their buffer offsets
 // pq16_count/offsets/scatter_kernel
 //                      the probed (query, probe) pairs grouped by list
-// pq16_screen_kernel   fp16 products of residuals and codes, threshold test,
-//                      candidate append
+// pq16_screen_kernel   fp16 products of residuals and codes: every value of
+//                      the first lists kept (dense), or the threshold test
+//                      and candidate append
+// pq16_select_kernel   the bound d_k from the kept values
 // pq16_classify_kernel the queries' flags and rescoring order
 // pq16_rescore_kernel  exact table distances of the candidates in the
 //                      reference's order (pq.rs:149-189 entries, :218-245 or
-//                      :318-485 sums) and the final top k
+//                      :318-485 sums) and the top k, per query or per part
+// pq16_merge_kernel    the parts' lists of a query merged
+// pq16_stats_kernel    rescans and candidates, counted when read
 #include "fdb_ivfpq16.hpp"
 
 #include <algorithm>
