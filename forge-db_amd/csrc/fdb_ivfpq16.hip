@@ -36,8 +36,9 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // 8 halves as a nati
 constexpr int kT = 256;
 // (query, probe) pairs per screening workgroup, 32 per wave: 4 waves for the
 // first lists (few pairs per list); for every probe, 8 waves up to 96
-// dimensions (KC <= 6), else 4 (measured: 8 waves took C5's 10M x 96 screen
-// from 2.4 to 2.1-2.3 ms and C3's 1M x 128 one from 0.23 to 0.26 ms)
+// dimensions (KC <= 6), else 4 (measured: 8 waves took the screen of 10M x 96
+// codes at nprobe 64 from 2.4 to 2.1-2.3 ms, and that of 1M x 128 codes at
+// nprobe 16 from 0.23 to 0.26 ms)
 constexpr int kWavesA = 4;
 constexpr int waves_b(int KC) { return KC <= 6 ? 8 : 4; }
 

@@ -3,12 +3,13 @@
 Every workload bench.py measures, at its full size:
 - the GPU index against the oracle on a subset of the queries: bit-exact
   distances, identical ids (ties by list position or row);
-- for the screened paths (brute force and IVF), the screened result against
-  the GPU's exact scan on many more queries: bit-exact, since screening
-  only chooses which rows are rescored exactly.
+- for the screened paths (brute force, IVF and IVF-PQ), the screened result
+  against the GPU's exact scan on many more queries: bit-exact, since
+  screening only chooses which rows are rescored exactly.
 
-C3 and C5 take the index the GPU built; the oracle searches the exported
-artifacts, and the screened IVF-PQ batch is compared with the table scan.  One test per workload; each prints its configuration first.
+The two IVF-PQ workloads (1M x 128 and 10M x 96) take the index the GPU
+built; the oracle searches the exported artifacts.  One test per workload;
+each prints its configuration first.
 """
 import numpy as np
 import pytest
