@@ -8,7 +8,9 @@ ordered by list position on both sides (the reference leaves that order to
 its BinaryHeap, so this is one of the orders it can return).
 """
 import os
+import struct
 import tempfile
+import zlib
 
 import numpy as np
 import pytest
@@ -235,6 +237,101 @@ def test_save_load_roundtrip(small_ivfpq):
         with pytest.raises(ForgeDbError) as e:
             IVFPQIndex.load(p)
         assert e.value.kind == "ChecksumMismatch"
+
+
+def _bincode_vector(vid, data):
+    """SerializableVector {id: u64, data: Vec<f32>} (ivf_pq.rs:198-202)."""
+    data = np.ascontiguousarray(data, dtype="<f4")
+    return struct.pack("<QQ", vid, data.size) + data.tobytes()
+
+
+def _bincode_ivfpq(art, nprobe, metric, rerank_factor, originals=None):
+    """An independent writer of SerializableIVFPQ (ivf_pq.rs:318-327) in
+    bincode 1.3's default encoding (`bincode::serialize`, ivf_pq.rs:1972):
+    fixed-width little-endian integers, usize as u64, Vec as a u64 length then
+    its elements, a unit enum variant as its u32 index, Option as a u8 tag
+    (0 = None, 1 = Some) then the value, struct fields in declaration order.
+    Centroid and codebook vectors carry their k-means cluster index as id
+    (kmeans.rs:183)."""
+    cen, cb = art["centroids"], art["codebooks"]
+    off, ids, codes = art["list_offsets"], art["ids"], art["codes"]
+    nlist, dim = cen.shape
+    M, ncb, dsub = cb.shape
+    out = [struct.pack("<Q", nlist)]
+    out += [_bincode_vector(c, cen[c]) for c in range(nlist)]
+    # SerializablePQ {codebooks: Vec<Vec<SerializableVector>>, n_subvectors, subvector_dim, dim}
+    out.append(struct.pack("<Q", M))
+    for m in range(M):
+        out.append(struct.pack("<Q", ncb))
+        out += [_bincode_vector(j, cb[m, j]) for j in range(ncb)]
+    out.append(struct.pack("<QQQ", M, dsub, dim))
+    # partitions: Vec<SerializablePartition {ids: Vec<u64>, codes: Vec<Vec<u8>>}>
+    out.append(struct.pack("<Q", nlist))
+    for l in range(nlist):
+        s, e = int(off[l]), int(off[l + 1])
+        out.append(struct.pack("<Q", e - s) + ids[s:e].astype("<u8").tobytes())
+        out.append(struct.pack("<Q", e - s))
+        out += [struct.pack("<Q", M) + codes[i].tobytes() for i in range(s, e)]
+    out.append(struct.pack("<QI", nprobe, metric))
+    if originals is None:
+        out.append(b"\x00")
+    else:
+        out.append(b"\x01" + struct.pack("<Q", len(originals)))
+        out += [_bincode_vector(i, v) for i, v in originals]
+    out.append(struct.pack("<Q", rerank_factor))
+    return b"".join(out)
+
+
+def _fdb_file(index_type, payload):
+    """[MAGIC 8B][VERSION u32][INDEX_TYPE u32][FLAGS u32][CHECKSUM u32]
+    (persistence/format.rs:79), CRC-32 (IEEE) of the payload."""
+    return b"FORGEDB\0" + struct.pack("<IIII", 1, index_type, 0, zlib.crc32(payload)) + payload
+
+
+def test_save_bincode_bytes():
+    """The IVF-PQ payload byte for byte against the independent writer above,
+    with an empty list, a non-default metric and both Option states; then the
+    reader loads the independently written file."""
+    print("IVF-PQ bincode bytes", flush=True)
+    rng = np.random.default_rng(7)
+    nlist, dim, M = 3, 4, 2
+    art = dict(centroids=rng.standard_normal((nlist, dim)).astype(np.float32),
+               codebooks=rng.standard_normal((M, 256, dim // M)).astype(np.float32),
+               list_offsets=np.array([0, 2, 2, 5], np.uint64),
+               ids=np.array([10, 3, 7, 42, 1], np.uint64),
+               codes=rng.integers(0, 256, (5, M), dtype=np.uint8))
+    gx = gpu_index(art, DistanceMetric.Cosine)
+    gx.set_nprobe(2)
+    with tempfile.TemporaryDirectory() as d:
+        p = os.path.join(d, "ix.fdb")
+        gx.save(p)
+        raw = open(p, "rb").read()
+        want = _bincode_ivfpq(art, nprobe=2, metric=int(DistanceMetric.Cosine), rerank_factor=1)
+        assert raw == _fdb_file(1, want)
+
+        # original_vectors comes from a HashMap's values() (ivf_pq.rs:1905-1910), so its
+        # record order is unspecified: compare the records as a set, everything else exactly
+        orig = rng.standard_normal((5, dim)).astype(np.float32)
+        gx.enable_reranking(orig, 3)
+        gx.save(p)
+        payload = open(p, "rb").read()[24:]
+        head = _bincode_ivfpq(art, 2, int(DistanceMetric.Cosine), 3)[:-9]
+        assert payload[:len(head)] == head
+        rest = payload[len(head):]
+        assert rest[0] == 1 and struct.unpack_from("<Q", rest, 1)[0] == 5
+        rec = 8 + 8 + 4 * dim
+        got = {rest[9 + r * rec: 9 + (r + 1) * rec] for r in range(5)}
+        assert got == {_bincode_vector(int(i), v) for i, v in zip(art["ids"], orig)}
+        assert len(rest) == 9 + 5 * rec + 8
+        assert struct.unpack_from("<Q", rest, 9 + 5 * rec)[0] == 3
+
+        # the reader on a file written independently
+        open(p, "wb").write(_fdb_file(1, want))
+        lx = IVFPQIndex.load(p)
+        assert lx.nprobe() == 2
+        ex = lx.export()
+        for key in art:
+            assert np.array_equal(ex[key], art[key]), key
 
 
 @pytest.mark.parametrize("shape", ["16x8", "32x3"])
