@@ -140,11 +140,11 @@ fdb_status fdb_ivfpq_build(const float* vectors, const uint64_t* ids, uint64_t n
 fdb_status fdb_ivfpq_load(const char* path, fdb_ivfpq** out) {
   return guarded([&] {
     if (!out || !path) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
-    std::vector<uint8_t> file;
-    IoResult r = read_file(path, file);
+    MappedFile file;
+    IoResult r = map_file(path, file);
     if (r.status) throw Error(r.status, r.message);
     size_t off = 0;
-    r = verify_header(file, IndexType::IvfPq, off);
+    r = verify_header(file.data(), file.size(), IndexType::IvfPq, off);
     if (r.status) throw Error(r.status, r.message);
     IvfPqArtifacts a;
     r = decode_ivfpq(file.data() + off, file.size() - off, a);
@@ -397,11 +397,11 @@ uint32_t fdb_bf_metric(const fdb_bf* h) { return (h && h->impl) ? h->impl->metri
 fdb_status fdb_bf_load(const char* path, fdb_bf** out) {
   return guarded([&] {
     if (!out || !path) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
-    std::vector<uint8_t> file;
-    IoResult r = read_file(path, file);
+    MappedFile file;
+    IoResult r = map_file(path, file);
     if (r.status) throw Error(r.status, r.message);
     size_t off = 0;
-    r = verify_header(file, IndexType::BruteForce, off);
+    r = verify_header(file.data(), file.size(), IndexType::BruteForce, off);
     if (r.status) throw Error(r.status, r.message);
     BruteForceArtifacts a;
     r = decode_bf(file.data() + off, file.size() - off, a);

@@ -1,6 +1,11 @@
 // .fdb container and payload codecs.  See fdb_format.hpp for the layouts.
 #include "fdb_format.hpp"
 
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include <cstdio>
 #include <cstring>
 #include <unordered_map>
@@ -112,20 +117,34 @@ uint32_t crc32_ieee(const uint8_t* data, size_t n) {
   return c ^ 0xFFFFFFFFu;
 }
 
-IoResult read_file(const std::string& path, std::vector<uint8_t>& out) {
-  FILE* f = std::fopen(path.c_str(), "rb");
-  if (!f) return fail(FDB_ERR_IO, "cannot open " + path);
-  std::fseek(f, 0, SEEK_END);
-  long sz = std::ftell(f);
-  std::fseek(f, 0, SEEK_SET);
-  if (sz < 0) {
-    std::fclose(f);
+MappedFile::~MappedFile() {
+  if (base_) ::munmap(base_, size_);
+}
+
+// Persistable::load_mmap (persistence/mod.rs:70-73, ivf_pq.rs:1983-1993): the
+// payload is decoded straight from a read-only private mapping, so a load
+// holds no second copy of the file in host memory.
+IoResult map_file(const std::string& path, MappedFile& out) {
+  int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+  if (fd < 0) return fail(FDB_ERR_IO, "cannot open " + path);
+  struct stat st;
+  if (::fstat(fd, &st) != 0 || st.st_size < 0) {
+    ::close(fd);
     return fail(FDB_ERR_IO, "cannot size " + path);
   }
-  out.resize((size_t)sz);
-  size_t got = sz ? std::fread(out.data(), 1, (size_t)sz, f) : 0;
-  std::fclose(f);
-  if (got != (size_t)sz) return fail(FDB_ERR_IO, "short read on " + path);
+  const size_t sz = (size_t)st.st_size;
+  void* p = nullptr;
+  if (sz) {
+    p = ::mmap(nullptr, sz, PROT_READ, MAP_PRIVATE, fd, 0);
+    if (p == MAP_FAILED) {
+      ::close(fd);
+      return fail(FDB_ERR_IO, "cannot map " + path);
+    }
+    ::madvise(p, sz, MADV_SEQUENTIAL);  // one front-to-back pass: CRC, then decode
+  }
+  ::close(fd);  // the mapping stays valid after the descriptor closes
+  out.base_ = p;
+  out.size_ = sz;
   return {};
 }
 
@@ -149,11 +168,11 @@ IoResult write_file(const std::string& path, IndexType type, const std::vector<u
 
 // verify_header, persistence/mod.rs:77-94 with FileHeader::from_bytes/verify,
 // format.rs:133-184.
-IoResult verify_header(const std::vector<uint8_t>& file, IndexType expected, size_t& payload_off) {
-  if (file.size() < kHeaderSize) return fail(FDB_ERR_INVALID_FORMAT, "file too small for header");
-  if (std::memcmp(file.data(), kMagic, 8) != 0)
+IoResult verify_header(const uint8_t* file, size_t n, IndexType expected, size_t& payload_off) {
+  if (n < kHeaderSize) return fail(FDB_ERR_INVALID_FORMAT, "file too small for header");
+  if (std::memcmp(file, kMagic, 8) != 0)
     return fail(FDB_ERR_INVALID_FORMAT, "invalid magic bytes");
-  Reader r{file.data() + 8, 16};
+  Reader r{file + 8, 16};
   uint32_t version = r.u32();
   uint32_t type = r.u32();
   (void)r.u32();  // flags
@@ -162,7 +181,7 @@ IoResult verify_header(const std::vector<uint8_t>& file, IndexType expected, siz
   if (version > kFormatVersion)
     return fail(FDB_ERR_INVALID_FORMAT, "unsupported version " + std::to_string(version));
   if (type != (uint32_t)expected) return fail(FDB_ERR_INVALID_FORMAT, "index type mismatch");
-  if (crc32_ieee(file.data() + kHeaderSize, file.size() - kHeaderSize) != checksum)
+  if (crc32_ieee(file + kHeaderSize, n - kHeaderSize) != checksum)
     return fail(FDB_ERR_CHECKSUM_MISMATCH, "checksum mismatch");
   payload_off = kHeaderSize;
   return {};

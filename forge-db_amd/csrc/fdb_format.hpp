@@ -45,10 +45,27 @@ struct IoResult {
   std::string message;
 };
 
-IoResult read_file(const std::string& path, std::vector<uint8_t>& out);
+// A read-only mapping of a whole file, unmapped on destruction.
+class MappedFile {
+ public:
+  MappedFile() = default;
+  MappedFile(const MappedFile&) = delete;
+  MappedFile& operator=(const MappedFile&) = delete;
+  ~MappedFile();
+  const uint8_t* data() const { return static_cast<const uint8_t*>(base_); }
+  size_t size() const { return size_; }
+
+ private:
+  friend IoResult map_file(const std::string& path, MappedFile& out);
+  void* base_ = nullptr;
+  size_t size_ = 0;
+};
+
+// Maps `path` into `out`, which must be empty.
+IoResult map_file(const std::string& path, MappedFile& out);
 IoResult write_file(const std::string& path, IndexType type, const std::vector<uint8_t>& payload);
 // verify_header: returns the payload offset in `file` through payload_off.
-IoResult verify_header(const std::vector<uint8_t>& file, IndexType expected, size_t& payload_off);
+IoResult verify_header(const uint8_t* file, size_t n, IndexType expected, size_t& payload_off);
 
 std::vector<uint8_t> encode_ivfpq(const IvfPqArtifacts& a);
 IoResult decode_ivfpq(const uint8_t* p, size_t n, IvfPqArtifacts& a);
