@@ -52,3 +52,46 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(forgedb, "_lib_handle", None)
     with pytest.raises(RuntimeError, match="not found"):
         forgedb.load_library(str(tmp_path / "nope.so"))
+
+
+def test_load_errors_are_reported_before_any_device_work(tmp_path):
+    """Persistable::load error paths (persistence/mod.rs:77-94): the file is
+    mapped, its header and CRC checked and its payload decoded on the host, so
+    every malformed file fails with its status before a device is needed."""
+    import struct
+    import zlib
+
+    def fdb(index_type, payload, magic=b"FORGEDB\0", version=1, crc=None):
+        crc = zlib.crc32(payload) if crc is None else crc
+        return magic + struct.pack("<IIII", version, index_type, 0, crc) + payload
+
+    payload = b"\x05" * 40  # a bincode length far beyond the payload
+    cases = {
+        "missing": (None, "Io"),
+        "dir": ("dir", "Io"),
+        "empty": (b"", "InvalidFormat"),
+        "short": (b"FORGEDB\0\x01", "InvalidFormat"),
+        "magic": (fdb(1, payload, magic=b"FORGEDX\0"), "InvalidFormat"),
+        "version": (fdb(1, payload, version=2), "InvalidFormat"),
+        "crc": (fdb(1, payload, crc=zlib.crc32(payload) ^ 1), "ChecksumMismatch"),
+        "payload": (fdb(1, payload), "InvalidFormat"),
+        "type": (fdb(4, payload), "InvalidFormat"),
+    }
+    for name, (content, kind) in cases.items():
+        p = tmp_path / name
+        if content == "dir":
+            p.mkdir()
+        elif content is not None:
+            p.write_bytes(content)
+        with pytest.raises(forgedb.ForgeDbError) as e:
+            forgedb.IVFPQIndex.load(str(p))
+        assert e.value.kind == kind, (name, e.value)
+    # the brute-force loader on an IVF-PQ file and on a bad checksum
+    (tmp_path / "bf").write_bytes(fdb(1, payload))
+    with pytest.raises(forgedb.ForgeDbError) as e:
+        forgedb.BruteForceIndex.load(str(tmp_path / "bf"))
+    assert e.value.kind == "InvalidFormat"
+    (tmp_path / "bf").write_bytes(fdb(4, payload, crc=7))
+    with pytest.raises(forgedb.ForgeDbError) as e:
+        forgedb.BruteForceIndex.load(str(tmp_path / "bf"))
+    assert e.value.kind == "ChecksumMismatch"
