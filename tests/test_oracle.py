@@ -417,3 +417,239 @@ def test_search_filtered_is_brute_force_over_admitted_live_entries():
         assert [int(i) for i in ids] == [i for i, _ in want]
         assert np.array_equal(d, np.array([x for _, x in want], np.float32))
     assert len(ix.search_filtered(queries[0], 10, np.array([], np.uint64))[0]) == 0
+
+
+# ---- independent models of the ADC sums, written from pq.rs ----------------------
+def _lanes8_model(lut, code):
+    """asymmetric_distance_simd_avx2 (pq.rs:435-485): lane l of an 8-wide f32
+    accumulator adds table[m][code[m]] for m = l (mod 8) below 8*floor(M/8);
+    the lanes are added left to right, then the tail m >= 8*floor(M/8) one
+    by one.  Every add is one f32 rounding."""
+    M = len(code)
+    lanes = [np.float32(0.0)] * 8
+    full = M // 8 * 8
+    for i in range(0, full, 8):
+        for l in range(8):
+            lanes[l] = np.float32(lanes[l] + lut[i + l, code[i + l]])
+    total = lanes[0]
+    for l in range(1, 8):
+        total = np.float32(total + lanes[l])
+    for m in range(full, M):
+        total = np.float32(total + lut[m, code[m]])
+    return total
+
+
+def _groups4_model(lut, code):
+    """asymmetric_distance_fast (pq.rs:218-245): per group of 4 the value
+    ((t0 + t1) + t2) + t3 is added to the running sum; the tail one by one."""
+    M = len(code)
+    s = np.float32(0.0)
+    i = 0
+    while i + 4 <= M:
+        g = np.float32(lut[i, code[i]] + lut[i + 1, code[i + 1]])
+        g = np.float32(g + lut[i + 2, code[i + 2]])
+        g = np.float32(g + lut[i + 3, code[i + 3]])
+        s = np.float32(s + g)
+        i += 4
+    while i < M:
+        s = np.float32(s + lut[i, code[i]])
+        i += 1
+    return s
+
+
+@pytest.mark.parametrize("M", [4, 8, 12, 16, 20, 24, 32, 40])
+def test_adc_orders_match_independent_lane_models(M):
+    # 8,000 random codes per M; tables with a wide dynamic range so that the
+    # orders round differently.  A sequential sum in place of either order
+    # (or a different grouping) fails: the test also requires that the
+    # models differ from the sequential sum on a good share of the inputs.
+    rng = np.random.default_rng(100 + M)
+    lut = (rng.random((M, 256)) * 10.0 ** rng.integers(0, 5, (M, 256))).astype(np.float32)
+    differ8 = differ4 = 0
+    for _ in range(8000):
+        code = rng.integers(0, 256, M).astype(np.uint8)
+        seq = _seq_sum_f32(lut[m, code[m]] for m in range(M))
+        m8, m4 = _lanes8_model(lut, code), _groups4_model(lut, code)
+        assert np.float32(refcpu.adc("lanes8", lut, code)) == m8
+        assert np.float32(refcpu.adc("groups4", lut, code)) == m4
+        differ8 += m8 != seq
+        differ4 += m4 != seq
+    # below 16 terms each lane holds at most one term and the 8-lane order is
+    # the sequential sum; below 8 terms so is the groups-of-4 order
+    if M >= 16:
+        assert differ8 > 800, differ8
+    if M >= 8:
+        assert differ4 > 400, differ4
+
+
+@pytest.mark.parametrize("M", [8, 16, 32, 20])
+def test_adc_batch4_matches_lane_model(M):
+    # batch_asymmetric_distance_avx2 (pq.rs:318-402): per query the same
+    # 8-lane accumulation; the lane array is folded with iter().sum() (from
+    # zero, left to right), then the tail; queries beyond a multiple of 4 go
+    # through asymmetric_distance_simd_avx2.  Both equal the lane model.
+    rng = np.random.default_rng(7 + M)
+    for _ in range(500):
+        luts = [(rng.random((M, 256)) * 10.0 ** rng.integers(0, 4, (M, 256))).astype(np.float32)
+                for _ in range(4)]
+        code = rng.integers(0, 256, M).astype(np.uint8)
+        got = refcpu.adc_batch4(luts, code)
+        for t in range(4):
+            assert got[t] == _lanes8_model(luts[t], code)
+
+
+# ---- splitmix64 streams and the build's shuffles ---------------------------------
+def _splitmix64(seed, i):
+    m = (1 << 64) - 1
+    z = (seed + (i + 1) * 0x9E3779B97F4A7C15) & m
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+    return z ^ (z >> 31)
+
+
+def test_shuffle_is_fisher_yates_from_the_back():
+    # rand 0.8 SliceRandom::shuffle: for i = n..2, swap v[i-1] with v[j],
+    # j uniform in [0, i); here j = (draw * i) >> 64 with the stream's next
+    # 64-bit draw (splitmix64 output number 0, 1, 2, ...)
+    for seed, n in ((5, 1), (5, 2), (123, 17), (0xF0DB0031, 1000)):
+        v = list(range(n))
+        draw = 0
+        for i in range(n, 1, -1):
+            j = (_splitmix64(seed, draw) * i) >> 64
+            draw += 1
+            v[i - 1], v[j] = v[j], v[i - 1]
+        assert refcpu.shuffle_indices(seed, n).tolist() == v
+
+
+# ---- IVFPQIndex::build composition (ivf_pq.rs:374-506) ---------------------------
+def test_ivfpq_build_composition():
+    """The build is: a 30k training sample (the first 30k of a shuffle) ->
+    k-means with nlist clusters and 25 iterations (:383-400); every vector in
+    the list of its first-minimum centroid, lists in input order (:403-414);
+    a 100k residual sample (the first of another shuffle) -> per subspace
+    k-means with 256 clusters (:422-446, pq.rs:60-105); every code the
+    first-argmin encode of its vector's residual (:450-478).  Each step is
+    recomputed here from the pinned primitives (shuffle, l2sq, encode) and
+    the oracle's k-means."""
+    from forgedb import datagen
+    n, dim, nlist, M, seed = 31_000, 8, 6, 4, 9
+    x = datagen.gaussian_mixture(seed + 1, seed + 2, n, dim, ncomp=12, centre_std=4.0)
+    ix = refcpu.IvfPq.build(x, nlist=nlist, M=M, seed=seed)
+    art = ix.export()
+    cen = art["centroids"]
+    # 1. coarse centroids from the first 30,000 of a shuffle
+    sample = x[refcpu.shuffle_indices(refcpu.splitmix64_at(seed, 0), n)[:30_000].astype(np.int64)]
+    assert np.array_equal(cen, refcpu.kmeans_fit(sample, nlist, 25, refcpu.splitmix64_at(seed, 1)))
+    # 2. first-minimum assignment (l2sq in the reference order; numpy's
+    # argmin returns the first minimum), lists in input order
+    d = np.array([[refcpu.dist("l2sq", v, c) for c in cen] for v in x[:4000]], np.float32)
+    want_list = np.argmin(d, axis=1)
+    off = art["list_offsets"].astype(np.int64)
+    pos_of = np.empty(n, np.int64)
+    pos_of[art["ids"].astype(np.int64)] = np.arange(n)
+    list_of = np.searchsorted(off, pos_of, side="right") - 1
+    assert np.array_equal(list_of[:4000], want_list)
+    for l in range(nlist):
+        assert np.all(np.diff(art["ids"][off[l]:off[l + 1]].astype(np.int64)) > 0)
+    # 3. codebooks from the residuals of the first 100,000 (here all n) of
+    # a second shuffle, each subspace with its own seed
+    idx = refcpu.shuffle_indices(refcpu.splitmix64_at(seed, 2), n).astype(np.int64)
+    resid = (x[idx] - cen[list_of[idx]]).astype(np.float32)
+    dsub = dim // M
+    for m in range(M):
+        sub = np.ascontiguousarray(resid[:, m * dsub:(m + 1) * dsub])
+        want = refcpu.kmeans_fit(sub, 256, 25, refcpu.splitmix64_at(seed, 16 + m))
+        assert np.array_equal(art["codebooks"][m], want), m
+    # 4. codes = first-argmin encode of each residual
+    for i in range(0, n, 97):
+        r = (x[i] - cen[list_of[i]]).astype(np.float32)
+        assert np.array_equal(art["codes"][pos_of[i]], refcpu.pq_encode(art["codebooks"], r))
+
+
+# ---- rerank_results (ivf_pq.rs:555-582, 1022-1040) -------------------------------
+def _rerank_model(q, pool_ids, originals_by_id, k):
+    """filter_map over the ADC candidates in their ascending order: sqrt of the
+    reference-order l2sq to the candidate's original vector (dropped when it
+    has none), a stable ascending sort by that distance, truncated to k."""
+    rr = []
+    for i in pool_ids:
+        v = originals_by_id.get(int(i))
+        if v is None:
+            continue
+        rr.append((int(i), np.float32(np.sqrt(np.float32(refcpu.dist("l2sq", q, v))))))
+    rr.sort(key=lambda t: t[1])  # Python's sort is stable
+    return rr[:k]
+
+
+def test_rerank_is_exact_sqrt_l2_over_the_adc_pool():
+    from forgedb import datagen
+    base, queries = datagen.workload("ivfpq_int", n=4000, nq=24)
+    # duplicated rows: equal ADC distances and equal exact distances, so the
+    # stable sort's order (the ADC order) is exercised
+    base[3000:3200] = base[100:300]
+    ix = refcpu.IvfPq.build(base, nlist=16, M=16, seed=2)
+    art = ix.export()
+    plain = refcpu.IvfPq.create(art["centroids"], art["codebooks"], art["list_offsets"],
+                                art["ids"], art["codes"])
+    rf, k = 4, 10
+    ix.enable_reranking(base[art["ids"].astype(np.int64)], rf)
+    orig = {int(i): base[int(i)] for i in art["ids"]}
+    for nprobe in (1, 3, 16):
+        ix.set_nprobe(nprobe)
+        plain.set_nprobe(nprobe)
+        qs = np.concatenate([queries, base[100:104] + 0.0])
+        # search (:590-677): the pool is search()'s k*rf ADC best
+        for q in qs:
+            pool, _ = plain.search(q, k * rf)
+            want = _rerank_model(q, pool, orig, k)
+            gi, gd = ix.search(q, k)
+            assert [int(i) for i in gi] == [i for i, _ in want]
+            assert np.array_equal(gd, np.array([d for _, d in want], np.float32))
+        # batch_search (:1022-1040): the pool is batch_search's k*rf best
+        pi, _, pc = plain.batch_search(qs, k * rf)
+        bi, bd, bc = ix.batch_search(qs, k)
+        for t, q in enumerate(qs):
+            want = _rerank_model(q, pi[t][:pc[t]], orig, k)
+            assert int(bc[t]) == len(want)
+            assert [int(i) for i in bi[t][:bc[t]]] == [i for i, _ in want]
+            assert np.array_equal(bd[t][:bc[t]], np.array([d for _, d in want], np.float32))
+
+
+# ---- brute-force top-k (brute_force.rs:105-157) -----------------------------------
+@pytest.mark.parametrize("metric", [EUC, EUC2, COS, DOT, L1])
+def test_bf_topk_is_full_sort_by_distance_then_row(metric):
+    # scan_range keeps a row only when strictly closer than the heap's worst,
+    # so among equal distances the earlier row wins; the result is the k
+    # smallest (distance, row) pairs in ascending order.  Duplicated rows
+    # make exact ties.
+    rng = np.random.default_rng(40 + metric)
+    data = rng.integers(0, 4, (1500, 12)).astype(np.float32)
+    data[700:900] = data[0:200]
+    ids = (np.arange(1500, dtype=np.uint64) * 7 + 3)
+    for _ in range(6):
+        q = rng.integers(0, 4, 12).astype(np.float32)
+        every = [refcpu.metric(metric, q, r) for r in data]
+        order = sorted(range(len(data)), key=lambda i: (every[i], i))
+        for k in (1, 10, 57, 1500, 2000):
+            oi, od = refcpu.bf_search(data, ids, metric, q, k)
+            want = order[:k]
+            assert oi.tolist() == [int(ids[i]) for i in want]
+            assert np.array_equal(od, np.array([every[i] for i in want], np.float32))
+
+
+def test_assignment_takes_the_first_of_twin_centroids():
+    # ivf_pq.rs:403-414 and :1740-1747 (min_by keeps the first minimum):
+    # with two identical centroids every vector nearest to them goes to the
+    # lower list.  Random data almost never ties exactly, so twins are
+    # planted; the same assignment routine serves build and insert.
+    rng = np.random.default_rng(12)
+    dim, M = 8, 4
+    cen = rng.standard_normal((5, dim)).astype(np.float32) * 10
+    cen[3] = cen[1]
+    cb = rng.standard_normal((M, 256, dim // M)).astype(np.float32)
+    ix = refcpu.IvfPq.create(cen, cb, np.zeros(6, np.uint64), np.zeros(0, np.uint64),
+                             np.zeros((0, M), np.uint8))
+    v = (cen[1] + rng.standard_normal((40, dim)) * 0.1).astype(np.float32)
+    ix.insert(v, np.arange(40, dtype=np.uint64))
+    off = ix.export()["list_offsets"].astype(np.int64)
+    assert off[2] - off[1] == 40 and off[4] - off[3] == 0
