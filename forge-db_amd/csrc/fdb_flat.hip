@@ -891,6 +891,9 @@ bool BruteForceIndex::remove(uint64_t id) {
 
 void BruteForceIndex::sync_device() {
   if (!dirty_) return;
+  // the rows are replaced on the handle's own stream: the previous call's
+  // kernels (on any stream) finish first
+  order_.wait_host();
   const uint64_t n = h_ids_.size();
   ld_ = std::max<uint64_t>(256, (n + 255) / 256 * 256);
   if (n) {
@@ -1136,6 +1139,7 @@ void BruteForceIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* 
 
 uint64_t BruteForceIndex::last_fallbacks(hipStream_t s) {
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, s ? s : stream_);
   if (path_ == 0 || !srch_.fallbacks()) return 0;  // the last search did not screen
   FDB_HIP(hipStreamSynchronize(s ? s : stream_));
   uint32_t v = 0;
@@ -1153,6 +1157,7 @@ void BruteForceIndex::batch_search(const float* qs, uint64_t nq, uint32_t k, uin
                                    float* dists, uint32_t* counts) {
   if (nq == 0) return;
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, stream_);
   sync_device();
   q_.upload(qs, nq * dim_, stream_);
   const uint32_t kk = std::max<uint32_t>(k, 1);
@@ -1172,6 +1177,7 @@ void BruteForceIndex::batch_search_device(const float* d_qs, uint64_t nq, uint32
                                           float* d_dists, uint32_t* d_counts, hipStream_t s,
                                           float* ms) {
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, s ? s : stream_);
   sync_device();
   hipStream_t st = s ? s : stream_;
   if (ms) FDB_HIP(hipEventRecord(ev_[0], st));
@@ -1406,6 +1412,7 @@ void IvfFlatIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_i
 
 uint64_t IvfFlatIndex::last_fallbacks(hipStream_t s) {
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, s ? s : stream_);
   if (path_ == 0 || !fallbacks_.p) return 0;  // the last search did not screen
   FDB_HIP(hipStreamSynchronize(s ? s : stream_));
   uint32_t v = 0;
@@ -1416,6 +1423,7 @@ uint64_t IvfFlatIndex::last_fallbacks(hipStream_t s) {
 void IvfFlatIndex::probe(const float* qs, uint64_t nq, uint32_t nprobe, int32_t* lists) {
   if (nq == 0 || nprobe == 0) return;
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, stream_);
   if (nprobe > nlist_) throw Error(FDB_ERR_INVALID_ARGUMENT, "nprobe above nlist");
   if (nprobe > 1024) throw Error(FDB_ERR_UNSUPPORTED, "nprobe above 1024");
   q_.upload(qs, nq * dim_, stream_);
@@ -1442,6 +1450,7 @@ void IvfFlatIndex::batch_search(const float* qs, uint64_t nq, uint32_t k, uint64
                                 uint32_t* counts) {
   if (nq == 0) return;
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, stream_);
   q_.upload(qs, nq * dim_, stream_);
   const uint32_t kk = std::max<uint32_t>(k, 1);
   out_i_.reserve(nq * kk);
@@ -1467,6 +1476,7 @@ void IvfFlatIndex::batch_search_device(const float* d_qs, uint64_t nq, uint32_t 
                                        float* d_dists, uint32_t* d_counts, hipStream_t s,
                                        float* coarse_ms, float* scan_ms) {
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, s ? s : stream_);
   run(d_qs, nq, k, d_ids, d_dists, d_counts, s ? s : stream_, coarse_ms, scan_ms);
 }
 

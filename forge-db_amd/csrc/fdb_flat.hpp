@@ -314,6 +314,7 @@ class BruteForceIndex {
   uint64_t n_dev_ = 0;  // rows resident on the device
   hipStream_t stream_ = nullptr;
   std::mutex mu_;
+  StreamOrder order_;  // calls on different streams share the scratch below
   DevBuf<float> dataT_, row_norm_, rows_;
   DevBuf<uint64_t> ids_;
   uint64_t ld_ = 0;
@@ -391,6 +392,7 @@ class IvfFlatIndex {
   std::vector<uint64_t> h_offsets_, h_ids_;
   hipStream_t stream_ = nullptr;
   std::mutex mu_;
+  StreamOrder order_;  // calls on different streams share the scratch below
   DevBuf<float> centT_, cent_, data_, row_norm_;
   DevBuf<float> rowsl_;  // [N][dim] row-major, list order (rescoring)
   Ivf16Lists l16_;

@@ -190,11 +190,20 @@ IoResult verify_header(const uint8_t* file, size_t n, IndexType expected, size_t
 // SerializableIVFPQ field order (ivf_pq.rs:307-316): centroids, pq
 // {codebooks, n_subvectors, subvector_dim, dim}, partitions [{ids, codes}],
 // nprobe, metric, original_vectors, rerank_factor.
+// original_vectors holds one record per id that has an original vector (the
+// map's entries; a deleted id has none), at its first entry in list order.
 std::vector<uint8_t> encode_ivfpq(const IvfPqArtifacts& a) {
   std::vector<uint8_t> o;
   const uint64_t n = a.ids.size();
+  std::vector<uint64_t> rec;  // list positions of the records
+  if (a.has_originals) {
+    std::unordered_map<uint64_t, bool> seen;
+    seen.reserve(n);
+    for (uint64_t i = 0; i < n; ++i)
+      if (a.orig_ok[i] && seen.emplace(a.ids[i], true).second) rec.push_back(i);
+  }
   o.reserve(64 + a.centroids.size() * 4 + a.codebooks.size() * 4 + n * (8 + 8 + a.M) +
-            a.nlist * 16 + (a.has_originals ? n * (16 + 4 * a.dim) : 0));
+            a.nlist * 16 + rec.size() * (16 + 4 * a.dim));
   put_u64(o, a.nlist);
   for (uint32_t c = 0; c < a.nlist; ++c) put_vector(o, c, &a.centroids[(size_t)c * a.dim], a.dim);
   put_u64(o, a.M);
@@ -221,8 +230,8 @@ std::vector<uint8_t> encode_ivfpq(const IvfPqArtifacts& a) {
   put_u32(o, a.metric);
   if (a.has_originals) {
     put_u8(o, 1);
-    put_u64(o, n);
-    for (uint64_t i = 0; i < n; ++i) put_vector(o, a.ids[i], &a.originals[i * a.dim], a.dim);
+    put_u64(o, rec.size());
+    for (uint64_t i : rec) put_vector(o, a.ids[i], &a.originals[i * a.dim], a.dim);
   } else {
     put_u8(o, 0);
   }
@@ -246,6 +255,8 @@ IoResult decode_ivfpq(const uint8_t* p, size_t n, IvfPqArtifacts& a) {
     if (c == 0) {
       dim = len;
       if (dim == 0 || dim > 0xFFFFFFFFull) return fail(FDB_ERR_INVALID_FORMAT, "zero dimension");
+      // every centroid record takes 16 + 4*dim bytes: check before reserving
+      if (nlist > (r.n - r.at + 16) / (16 + 4 * dim)) return fail(FDB_ERR_INVALID_FORMAT, bad);
       a.centroids.reserve(nlist * dim);
     } else if (len != dim) {
       return fail(FDB_ERR_INVALID_FORMAT, "centroid dimensions differ");
@@ -258,6 +269,7 @@ IoResult decode_ivfpq(const uint8_t* p, size_t n, IvfPqArtifacts& a) {
   if (!r.ok || M == 0 || dim % M != 0) return fail(FDB_ERR_INVALID_FORMAT, "bad codebook count");
   const uint64_t dsub = dim / M;
   a.codebooks.clear();
+  if (M > (r.n - r.at) / (8 + 256 * (16 + 4 * dsub))) return fail(FDB_ERR_INVALID_FORMAT, bad);
   a.codebooks.reserve(M * 256 * dsub);
   for (uint64_t m = 0; m < M; ++m) {
     uint64_t kc = r.len(16);
@@ -299,9 +311,12 @@ IoResult decode_ivfpq(const uint8_t* p, size_t n, IvfPqArtifacts& a) {
   if (!r.ok || tag > 1) return fail(FDB_ERR_INVALID_FORMAT, "bad Option tag");
   a.has_originals = false;
   a.originals.clear();
+  a.orig_ok.clear();
   if (tag == 1) {
     uint64_t nv = r.len(16);
-    if (!r.ok) return fail(FDB_ERR_INVALID_FORMAT, bad);
+    if (!r.ok || nv > (r.n - r.at) / (16 + 4 * dim)) return fail(FDB_ERR_INVALID_FORMAT, bad);
+    // from_serializable (ivf_pq.rs:1918-1925) collects the records into a
+    // map: a later record of an id replaces an earlier one
     std::unordered_map<uint64_t, uint64_t> where;
     std::vector<float> vecs;
     vecs.reserve(nv * dim);
@@ -310,13 +325,18 @@ IoResult decode_ivfpq(const uint8_t* p, size_t n, IvfPqArtifacts& a) {
       if (!read_vector(r, vecs, dim, &id)) return fail(FDB_ERR_INVALID_FORMAT, bad);
       where[id] = i;
     }
+    // an entry whose id has no record (the reference's delete removes the
+    // id's vector but saves the entry, tombstones being unsaved) has no
+    // original; reranking drops it (filter_map, ivf_pq.rs:562-571).
+    // Records of ids no list holds are not kept.
     const uint64_t N = a.ids.size();
-    a.originals.resize(N * dim);
+    a.originals.assign(N * dim, 0.0f);
+    a.orig_ok.assign(N, 0);
     for (uint64_t i = 0; i < N; ++i) {
       auto it = where.find(a.ids[i]);
-      if (it == where.end())
-        return fail(FDB_ERR_UNSUPPORTED, "original vector missing for an indexed id");
+      if (it == where.end()) continue;
       std::memcpy(&a.originals[i * dim], &vecs[it->second * dim], 4 * dim);
+      a.orig_ok[i] = 1;
     }
     a.has_originals = true;
   }

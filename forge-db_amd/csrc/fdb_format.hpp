@@ -35,7 +35,12 @@ struct IvfPqArtifacts {
   uint64_t nprobe = 1;
   uint32_t metric = 0;
   bool has_originals = false;
-  std::vector<float> originals;     // [N][dim], list order, when has_originals
+  // original_vectors (ivf_pq.rs:356) is a map id -> vector; here it is held
+  // per list entry.  When has_originals: originals [N][dim] in list order and
+  // orig_ok [N], 1 where the entry's id has an original vector.  Entries
+  // sharing an id share its vector and flag, as map lookups by id would.
+  std::vector<float> originals;
+  std::vector<uint8_t> orig_ok;
   uint64_t rerank_factor = 1;
 };
 

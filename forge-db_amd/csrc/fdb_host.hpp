@@ -57,6 +57,51 @@ struct DevBuf {
   }
 };
 
+// Orders a handle's device work across streams.  Every call shares the
+// handle's device scratch, so a call enqueued on stream s first makes s wait
+// (on the GPU) for the work the previous call enqueued, when that call used
+// another stream; same-stream calls are ordered by the stream already.
+// Used under the handle's mutex, through OrderedOn.
+struct StreamOrder {
+  hipEvent_t ev = nullptr;
+  hipStream_t last = nullptr;
+  bool pending = false;
+  StreamOrder() = default;
+  StreamOrder(const StreamOrder&) = delete;
+  StreamOrder& operator=(const StreamOrder&) = delete;
+  ~StreamOrder() {
+    if (ev) (void)hipEventDestroy(ev);
+  }
+  void begin(hipStream_t s) {
+    if (pending && last != s) FDB_HIP(hipStreamWaitEvent(s, ev, 0));
+  }
+  // the host waits for the previous call's work
+  void wait_host() {
+    if (pending) FDB_HIP(hipEventSynchronize(ev));
+  }
+  // no throw: runs from a destructor, also after a failed call
+  void end(hipStream_t s) noexcept {
+    if (!ev && hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+      ev = nullptr;
+      return;
+    }
+    if (hipEventRecord(ev, s) == hipSuccess) {
+      last = s;
+      pending = true;
+    }
+  }
+};
+
+// The scope of one call's device work on stream s.
+struct OrderedOn {
+  StreamOrder& o;
+  hipStream_t s;
+  OrderedOn(StreamOrder& order, hipStream_t stream) : o(order), s(stream) { o.begin(s); }
+  ~OrderedOn() { o.end(s); }
+  OrderedOn(const OrderedOn&) = delete;
+  OrderedOn& operator=(const OrderedOn&) = delete;
+};
+
 // Squared L2 in the reference's AVX2 order (src/distance/simd.rs:335-366),
 // scalar: 8 FMA lanes, lanes summed from -0.0 left to right, scalar tail.
 inline float host_l2sq_ref(const float* a, const float* b, int n) {

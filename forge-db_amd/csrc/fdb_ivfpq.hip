@@ -3,6 +3,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <unordered_map>
 
 #include "fdb_device.hpp"
 #include "fdb_kernels.hpp"
@@ -38,11 +39,13 @@ __global__ void nan_check_kernel(const float* __restrict__ q, uint64_t n, int* e
 // rerank_results, ivf_pq.rs:556-582: candidates arrive sorted by ADC
 // distance; each gets sqrt of the exact reference-order squared L2 to its
 // original vector, and a stable ascending sort of those (ties keep the ADC
-// order: the tie key is the candidate's rank) is truncated to k.  One wave
-// per query.
+// order: the tie key is the candidate's rank) is truncated to k.  Entries
+// whose bit in orig_bits is clear (null: every entry has one) have no
+// original and are left out.  One wave per query.
 template <int R>
 __global__ __launch_bounds__(64) void rerank_kernel(const float* __restrict__ queries, int dim,
                                                     const float* __restrict__ originals,
+                                                    const uint32_t* __restrict__ orig_bits,
                                                     const uint64_t* __restrict__ ids,
                                                     const uint32_t* __restrict__ cand_pos,
                                                     const uint32_t* __restrict__ cand_cnt,
@@ -62,8 +65,11 @@ __global__ __launch_bounds__(64) void rerank_kernel(const float* __restrict__ qu
     uint32_t rank = kNoPos;
     if (c < cnt) {
       const uint32_t pos = cand_pos[q * fetch_k + c];
-      d = __builtin_sqrtf(l2sq_ref_rt(qv, originals + (uint64_t)pos * dim, dim));
-      rank = c;
+      // an entry without an original vector is dropped (filter_map)
+      if (!orig_bits || ((orig_bits[pos >> 5] >> (pos & 31)) & 1u)) {
+        d = __builtin_sqrtf(l2sq_ref_rt(qv, originals + (uint64_t)pos * dim, dim));
+        rank = c;
+      }
     }
     tk.offer(d, rank);
   }
@@ -88,13 +94,13 @@ int regs_for(uint32_t k) {
 }
 
 hipError_t launch_rerank(const float* queries, uint64_t nq, int dim, const float* originals,
-                         const uint64_t* ids, const uint32_t* cand_pos, const uint32_t* cand_cnt,
-                         uint32_t fetch_k, uint32_t k, uint64_t* out_ids, float* out_dists,
-                         uint32_t* out_counts, hipStream_t s) {
+                         const uint32_t* orig_bits, const uint64_t* ids, const uint32_t* cand_pos,
+                         const uint32_t* cand_cnt, uint32_t fetch_k, uint32_t k, uint64_t* out_ids,
+                         float* out_dists, uint32_t* out_counts, hipStream_t s) {
 #define FDB_RR(R)                                                                             \
   hipLaunchKernelGGL(rerank_kernel<R>, dim3((unsigned)nq), dim3(64), 0, s, queries, dim,      \
-                     originals, ids, cand_pos, cand_cnt, fetch_k, k, out_ids, out_dists,     \
-                     out_counts);                                                             \
+                     originals, orig_bits, ids, cand_pos, cand_cnt, fetch_k, k, out_ids,     \
+                     out_dists, out_counts);                                                  \
   break;
   switch (regs_for(k)) {
     case 1: FDB_RR(1)
@@ -229,7 +235,10 @@ std::vector<float> kmeans_gpu(const float* h_points, uint64_t n, int dim, int k,
 }
 
 IvfPqIndex::IvfPqIndex(IvfPqArtifacts&& art) : host_(std::move(art)) {
-  nprobe_.store(std::min<uint64_t>(host_.nprobe, host_.nlist), std::memory_order_relaxed);
+  // from_serializable keeps the stored value (ivf_pq.rs:1937); every search
+  // clamps it to nlist
+  nprobe_.store(host_.nprobe, std::memory_order_relaxed);
+  if (host_.has_originals && host_.orig_ok.size() != host_.ids.size()) host_.orig_ok.assign(host_.ids.size(), 1);
   FDB_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   for (auto& e : ev_) FDB_HIP(hipEventCreate(&e));
   const uint64_t N = host_.ids.size();
@@ -257,11 +266,32 @@ void IvfPqIndex::upload_lists() {
     FDB_HIP(hipMemcpyAsync(codes_.p, host_.codes.data(), host_.codes.size(), hipMemcpyHostToDevice,
                            stream_));
   ids_.upload(host_.ids.data(), std::max<size_t>(host_.ids.size(), 1), stream_);
-  if (host_.has_originals && !host_.originals.empty())
-    originals_.upload(host_.originals.data(), host_.originals.size(), stream_);
+  upload_originals();
   live_dirty_ = true;
   pq16_dirty_ = true;
   FDB_HIP(hipStreamSynchronize(stream_));
+}
+
+void IvfPqIndex::upload_originals() {
+  orig_all_ = true;
+  if (!host_.has_originals) return;
+  const uint64_t N = host_.ids.size();
+  if (!host_.originals.empty()) originals_.upload(host_.originals.data(), host_.originals.size(), stream_);
+  std::vector<uint32_t> bits((N + 31) / 32, 0);
+  for (uint64_t i = 0; i < N; ++i)
+    if (host_.orig_ok[i]) bits[i >> 5] |= 1u << (i & 31);
+    else orig_all_ = false;
+  if (!orig_all_) orig_bits_.upload(bits.data(), bits.size(), stream_);
+  FDB_HIP(hipStreamSynchronize(stream_));
+}
+
+void IvfPqIndex::set_original(uint64_t id, const float* v) {
+  const uint64_t N = host_.ids.size(), dim = host_.dim;
+  for (uint64_t p = 0; p < N; ++p)
+    if (host_.ids[p] == id) {
+      if (v) std::memcpy(&host_.originals[p * dim], v, 4 * dim);
+      host_.orig_ok[p] = v ? 1 : 0;
+    }
 }
 
 const uint32_t* IvfPqIndex::live_bitmap() {
@@ -283,6 +313,7 @@ const uint32_t* IvfPqIndex::live_bitmap() {
 
 void IvfPqIndex::last_screen_stats(uint64_t& fallbacks, uint64_t& candidates, hipStream_t s) {
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, s ? s : stream_);
   fallbacks = candidates = 0;
   if (path_ != 2) return;
   FDB_HIP(hipStreamSynchronize(s ? s : stream_));
@@ -301,6 +332,7 @@ void IvfPqIndex::throw_if_nan() {
 
 bool IvfPqIndex::remove(uint64_t id) {
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, stream_);
   for (uint32_t l = 0; l < host_.nlist; ++l) {
     if (tomb_[l].count(id)) continue;
     for (uint64_t p = host_.offsets[l]; p < host_.offsets[l + 1]; ++p)
@@ -308,6 +340,12 @@ bool IvfPqIndex::remove(uint64_t id) {
         tomb_[l].insert(id);
         ++n_tomb_;
         live_dirty_ = true;
+        // the id leaves original_vectors (ivf_pq.rs:1793-1797): every entry
+        // holding it is left out of reranking from now on
+        if (host_.has_originals) {
+          set_original(id, nullptr);
+          upload_originals();
+        }
         return true;
       }
   }
@@ -316,10 +354,11 @@ bool IvfPqIndex::remove(uint64_t id) {
 
 void IvfPqIndex::compact() {
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, stream_);
   if (n_tomb_ == 0) return;
   const uint32_t M = host_.M, dim = host_.dim;
   std::vector<uint64_t> offs(host_.nlist + 1, 0), ids;
-  std::vector<uint8_t> codes;
+  std::vector<uint8_t> codes, ok;
   std::vector<float> orig;
   ids.reserve(host_.ids.size());
   codes.reserve(host_.codes.size());
@@ -328,8 +367,10 @@ void IvfPqIndex::compact() {
       if (tomb_[l].count(host_.ids[p])) continue;
       ids.push_back(host_.ids[p]);
       codes.insert(codes.end(), &host_.codes[p * M], &host_.codes[p * M] + M);
-      if (host_.has_originals)
+      if (host_.has_originals) {
         orig.insert(orig.end(), &host_.originals[p * dim], &host_.originals[p * dim] + dim);
+        ok.push_back(host_.orig_ok[p]);
+      }
     }
     offs[l + 1] = ids.size();
     tomb_[l].clear();
@@ -337,7 +378,10 @@ void IvfPqIndex::compact() {
   host_.offsets.swap(offs);
   host_.ids.swap(ids);
   host_.codes.swap(codes);
-  if (host_.has_originals) host_.originals.swap(orig);
+  if (host_.has_originals) {
+    host_.originals.swap(orig);
+    host_.orig_ok.swap(ok);
+  }
   n_tomb_ = 0;
   upload_lists();
 }
@@ -345,6 +389,7 @@ void IvfPqIndex::compact() {
 void IvfPqIndex::insert(const float* vectors, const uint64_t* ids, uint64_t n) {
   if (n == 0) return;
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, stream_);
   const uint32_t M = host_.M, dim = host_.dim;
   for (uint64_t i = 0; i < n * dim; ++i)
     if (std::isnan(vectors[i])) throw Error(FDB_ERR_NAN, "NaN in the vectors to insert");
@@ -371,8 +416,9 @@ void IvfPqIndex::insert(const float* vectors, const uint64_t* ids, uint64_t n) {
   // each list: its old entries, then the new ones in input order
   std::vector<uint32_t> off, members;
   group_members(assign, (int)host_.nlist, off, members);
+  const uint64_t n_old = host_.ids.size();
   std::vector<uint64_t> offs(host_.nlist + 1, 0), nids;
-  std::vector<uint8_t> codes;
+  std::vector<uint8_t> codes, ok;
   std::vector<float> orig;
   nids.reserve(host_.ids.size() + n);
   codes.reserve(host_.codes.size() + n * M);
@@ -380,14 +426,19 @@ void IvfPqIndex::insert(const float* vectors, const uint64_t* ids, uint64_t n) {
     const uint64_t s = host_.offsets[l], e = host_.offsets[l + 1];
     nids.insert(nids.end(), host_.ids.begin() + s, host_.ids.begin() + e);
     codes.insert(codes.end(), host_.codes.begin() + s * M, host_.codes.begin() + e * M);
-    if (host_.has_originals)
+    if (host_.has_originals) {
       orig.insert(orig.end(), host_.originals.begin() + s * dim, host_.originals.begin() + e * dim);
+      ok.insert(ok.end(), host_.orig_ok.begin() + s, host_.orig_ok.begin() + e);
+    }
     for (uint32_t t = off[l]; t < off[l + 1]; ++t) {
       const uint64_t i = members[t];
-      const uint64_t id = ids ? ids[i] : host_.ids.size() + i;
+      const uint64_t id = ids ? ids[i] : n_old + i;
       nids.push_back(id);
       codes.insert(codes.end(), &newc[i * M], &newc[i * M] + M);
-      if (host_.has_originals) orig.insert(orig.end(), vectors + i * dim, vectors + (i + 1) * dim);
+      if (host_.has_originals) {
+        orig.insert(orig.end(), vectors + i * dim, vectors + (i + 1) * dim);
+        ok.push_back(1);
+      }
       n_tomb_ -= tomb_[l].erase(id);
     }
     offs[l + 1] = nids.size();
@@ -395,7 +446,20 @@ void IvfPqIndex::insert(const float* vectors, const uint64_t* ids, uint64_t n) {
   host_.offsets.swap(offs);
   host_.ids.swap(nids);
   host_.codes.swap(codes);
-  if (host_.has_originals) host_.originals.swap(orig);
+  if (host_.has_originals) {
+    host_.originals.swap(orig);
+    host_.orig_ok.swap(ok);
+    // original_vectors.insert(id, vector) in input order (ivf_pq.rs:1769-1773):
+    // the last vector given for an id becomes every entry's original for it
+    std::unordered_map<uint64_t, uint64_t> last;
+    for (uint64_t i = 0; i < n; ++i) last[ids ? ids[i] : n_old + i] = i;
+    for (uint64_t p = 0; p < host_.ids.size(); ++p) {
+      auto it = last.find(host_.ids[p]);
+      if (it == last.end()) continue;
+      std::memcpy(&host_.originals[p * dim], vectors + it->second * dim, 4 * (size_t)dim);
+      host_.orig_ok[p] = 1;
+    }
+  }
   upload_lists();
 }
 
@@ -403,6 +467,7 @@ void IvfPqIndex::search_filtered(const float* qs, uint64_t nq, uint32_t k, const
                                  uint64_t n_allowed, uint64_t* ids, float* dists, uint32_t* counts) {
   if (nq == 0) return;
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, stream_);
   const uint32_t kk = std::max<uint32_t>(k, 1);
   out_ids_.reserve(nq * kk);
   out_d_.reserve(nq * kk);
@@ -449,11 +514,30 @@ bool IvfPqIndex::set_lut_mode(int mode) {
 
 void IvfPqIndex::enable_reranking(const float* v, uint64_t factor) {
   std::lock_guard<std::mutex> g(mu_);
-  host_.originals.assign(v, v + host_.ids.size() * (uint64_t)host_.dim);
+  OrderedOn on(order_, stream_);
+  const uint64_t N = host_.ids.size(), dim = host_.dim;
+  host_.originals.assign(v, v + N * dim);
+  host_.orig_ok.assign(N, 1);
+  // the vectors are collected into a map by id (ivf_pq.rs:513-514): with
+  // duplicate ids the last one in list order is every such entry's original
+  std::unordered_map<uint64_t, uint64_t> last;
+  last.reserve(N);
+  bool dup = false;
+  for (uint64_t p = 0; p < N; ++p) {
+    auto r = last.emplace(host_.ids[p], p);
+    if (!r.second) {
+      r.first->second = p;
+      dup = true;
+    }
+  }
+  if (dup)
+    for (uint64_t p = 0; p < N; ++p) {
+      const uint64_t src = last[host_.ids[p]];
+      if (src != p) std::memcpy(&host_.originals[p * dim], v + src * dim, 4 * (size_t)dim);
+    }
   host_.has_originals = true;
   host_.rerank_factor = std::max<uint64_t>(factor, 1);
-  originals_.upload(host_.originals.data(), host_.originals.size(), stream_);
-  FDB_HIP(hipStreamSynchronize(stream_));
+  upload_originals();
 }
 
 void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, int order,
@@ -469,8 +553,20 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
     return;
   }
   const bool rerank = host_.has_originals;
-  const uint64_t fetch = (rerank ? (uint64_t)k * host_.rerank_factor : k) * fetch_mult;
+  const uint64_t factor = rerank ? host_.rerank_factor : 1;
+  if (factor > 1024) throw Error(FDB_ERR_UNSUPPORTED, "candidates per query (k * rerank factor) above 1024");
+  const uint64_t fetch = (uint64_t)k * factor * fetch_mult;
   if (fetch > 1024) throw Error(FDB_ERR_UNSUPPORTED, "candidates per query (k * rerank factor) above 1024");
+  if (fetch == 0) {
+    // a stored rerank_factor of 0 (from_serializable keeps it, ivf_pq.rs:1940)
+    // keeps no candidate: every result is empty, as in the reference
+    hipLaunchKernelGGL(fill_empty_kernel, dim3(blocks_for(nq * k, 256)), dim3(256), 0, s, nq, k, d_ids, d_dists,
+                       d_counts);
+    FDB_HIP(hipGetLastError());
+    if (coarse_ms) *coarse_ms = 0.0f;
+    if (scan_ms) *scan_ms = 0.0f;
+    return;
+  }
   // without reranking the kept candidates are truncated to k below
   const bool trunc = !rerank && fetch > k;
   if (np > 1024 && np < host_.nlist) throw Error(FDB_ERR_UNSUPPORTED, "nprobe above 1024");
@@ -576,8 +672,8 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
     FDB_HIP(launch_ivfpq_scan(a, s));
   }
   if (rerank)
-    FDB_HIP(launch_rerank(d_qs, nq, (int)host_.dim, originals_.p, ids_.p, cand_pos_.p, cand_cnt_.p,
-                          (uint32_t)fetch, k, d_ids, d_dists, d_counts, s));
+    FDB_HIP(launch_rerank(d_qs, nq, (int)host_.dim, originals_.p, orig_all_ ? nullptr : orig_bits_.p, ids_.p,
+                          cand_pos_.p, cand_cnt_.p, (uint32_t)fetch, k, d_ids, d_dists, d_counts, s));
   else if (trunc)
     FDB_HIP(launch_truncate(cand_ids_.p, cand_d_.p, cand_cnt_.p, nq, (uint32_t)fetch, k, d_ids, d_dists,
                             d_counts, s));
@@ -591,6 +687,7 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
 
 uint32_t IvfPqIndex::search(const float* q, uint32_t k, uint64_t* ids, float* dists) {
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, stream_);
   const uint32_t np = (uint32_t)std::min<uint64_t>(nprobe(), host_.nlist);  // 0 probes 0 lists
   q_.upload(q, host_.dim, stream_);
   const uint32_t kk = std::max<uint32_t>(k, 1);
@@ -620,6 +717,7 @@ void IvfPqIndex::batch_search(const float* qs, uint64_t nq, uint32_t k, uint64_t
                               float* dists, uint32_t* counts) {
   if (nq == 0) return;
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, stream_);
   // batch_search probes [..=nth]: at least one list (ivf_pq.rs:877-881)
   const uint32_t np = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(nprobe(), host_.nlist));
   q_.upload(qs, nq * host_.dim, stream_);
@@ -648,6 +746,7 @@ void IvfPqIndex::batch_search_device(const float* d_qs, uint64_t nq, uint32_t k,
                                      float* d_dists, uint32_t* d_counts, hipStream_t s,
                                      float* coarse_ms, float* scan_ms) {
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, s ? s : stream_);
   const uint32_t np = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(nprobe(), host_.nlist));
   run(d_qs, nq, k, np, kAdcLanes8, d_ids, d_dists, d_counts, s ? s : stream_, coarse_ms, scan_ms,
       live_bitmap());
@@ -669,6 +768,7 @@ void IvfPqIndex::probe(const float* qs, uint64_t nq, uint32_t nprobe, int32_t* l
                        float* dists) {
   if (nq == 0 || nprobe == 0) return;
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, stream_);
   if (nprobe > host_.nlist) throw Error(FDB_ERR_INVALID_ARGUMENT, "nprobe above nlist");
   if (nprobe > 1024) throw Error(FDB_ERR_UNSUPPORTED, "nprobe above 1024");
   q_.upload(qs, nq * host_.dim, stream_);
@@ -684,6 +784,7 @@ void IvfPqIndex::probe(const float* qs, uint64_t nq, uint32_t nprobe, int32_t* l
 void IvfPqIndex::encode(const float* residuals, uint64_t nq, uint8_t* codes) {
   if (nq == 0) return;
   std::lock_guard<std::mutex> g(mu_);
+  OrderedOn on(order_, stream_);
   // encode residuals directly: vectors = residuals, centroid rows = a zero row
   DevBuf<float> zero;
   std::vector<float> z(host_.dim, 0.0f);

@@ -112,6 +112,10 @@ class IvfPqIndex {
   const uint32_t* live_bitmap();
   // re-uploads ids, codes, offsets and originals after the lists changed
   void upload_lists();
+  // uploads the originals and, when some entry has none, their bitmap
+  void upload_originals();
+  // every entry holding id gets original v (null: none)
+  void set_original(uint64_t id, const float* v);
   void throw_if_nan();
 
   IvfPqArtifacts host_;
@@ -122,8 +126,13 @@ class IvfPqIndex {
   static constexpr uint64_t kPq16MinWork = 1ull << 26;
   hipStream_t stream_ = nullptr;
   std::mutex mu_;
+  StreamOrder order_;  // calls on different streams share the scratch below
 
   DevBuf<float> centroids_, centT_, codebooks_, cbnorm_, originals_;
+  // one bit per list entry: it has an original vector (uploaded only when
+  // some entry has none)
+  DevBuf<uint32_t> orig_bits_;
+  bool orig_all_ = true;
   CoarseQuantizer coarse_;
   DevBuf<uint32_t> off_;
   DevBuf<uint8_t> codes_;

@@ -7,9 +7,10 @@
 // pq16_plan_kernel     each query's first lists and their buffer offsets
 // pq16_count/offsets/scatter_kernel
 //                      the probed (query, probe) pairs grouped by list
-// pq16_screen_kernel   fp16 products of residuals and codes: every value of
-//                      the first lists kept (dense), or the threshold test
-//                      and candidate append
+// pq16_dense_kernel    fp16 products of residuals and codes: every value of
+//                      each query's first lists kept (stage A)
+// pq16_thresh_kernel   the same products against each query's bound, the
+//                      candidates appended (stage B)
 // pq16_select_kernel   the bound d_k from the kept values
 // pq16_classify_kernel the queries' flags and rescoring order
 // pq16_rescore_kernel  exact table distances of the candidates in the
@@ -34,15 +35,11 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // 8 halves as a native vector
 
 constexpr int kT = 256;
-// (query, probe) pairs per screening workgroup, 32 per wave: 4 waves for the
-// first lists (few pairs per list); for every probe, 8 waves up to 96
-// dimensions (KC <= 6), else 4 (measured: 8 waves took the screen of 10M x 96
-// codes at nprobe 64 from 2.4 to 2.1-2.3 ms, and that of 1M x 128 codes at
-// nprobe 16 from 0.23 to 0.26 ms)
-constexpr int kWavesA = 4;
-constexpr int waves_b(int KC) { return KC <= 6 ? 8 : 4; }
+// (query, probe) pairs per screening tile: 32 per wave, 4 waves
+constexpr int kTilePairs = 128;
 
 uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
 
 // The wave's index in its workgroup as a wave-uniform value (scalar
 // branches on it).
@@ -171,7 +168,9 @@ __global__ __launch_bounds__(kT) void pq16_norms_kernel(const float* __restrict_
     }
     atomicMax(&xmax2[p], __float_as_uint(s));
   }
-  xnb[slot] = s;
+  // slots past the list's end hold +inf: their screened value
+  // fma(c, 0, +inf) never passes a finite threshold
+  xnb[slot] = row < len ? s : f_inf();
 }
 
 // ---- (query, probe) pairs by list ------------------------------------------
@@ -188,8 +187,7 @@ constexpr int kSortWG = 32;          // workgroups of the counting sort (at most
 constexpr uint32_t kCB = 64;         // blocks of 32 codes per screening tile
 constexpr uint32_t kXcd = 8;         // L2 domains (XCDs); workgroup b runs on XCD b % 8
 constexpr uint32_t kXcdRun = 4;      // consecutive tiles given to one XCD
-constexpr int kSlots = 8;            // candidate slots per lane in LDS
-constexpr int kNS = 4;               // one-block stages in the screening kernel's LDS ring
+constexpr int kNS = 4;               // one-block stages in stage A's LDS ring
 constexpr uint32_t kLight = 256;     // candidate entries rescored by one wave (more: in parts)
 constexpr uint32_t kPart = 256;      // entries of one part of a heavy query (a workgroup)
 constexpr uint32_t kRound = 64;      // entries of one rescoring round
@@ -429,151 +427,228 @@ __device__ __forceinline__ float add_up(float a, float b) {
 
 // Tiles: list p owns toff[p] .. toff[p+1]: ceil(pairs_p / 128) pair tiles
 // (fastest) times ceil(min(blocks_p, blim) / kCB) block chunks; workgroups
-// stride over the tiles.  In a tile, wave w takes pairs [32w, 32w+32): lane
-// l holds pair l%32's residual on dimensions 16kc + 8(l/32) .. +7 as the B
-// operand.  The chunk's blocks go through an LDS stage of SB blocks shared
-// by the four waves, the next stage's loads issued before the current one
-// is multiplied; D[r] is code 8(r/4) + 4(l/32) + r%4 of a block against
-// pair l%32.
-//   Threshold mode: s' = fma(-2^(1-er-xexp), acc, |x^|^2) against
-//   T' = dkA + eps - |r|^2 rounded up: a code left out has s' > T', so its
-//   screened distance exceeds dkA + eps by more than the FMA's rounding,
-//   which eps covers.
-//   Dense mode: s = fma(.., acc, |r|^2 + |x^|^2) of every code is written
-//   to the pair's 32-aligned range of the query's buffer (+inf past the
-//   list's end, nothing past capA), four rows per 16-byte store.
-template <int KC, bool DENSE, int NW>
-__global__ __launch_bounds__(64 * NW) void pq16_screen_kernel(ScreenArgs a) {
-  // NW: waves per workgroup
-  constexpr uint32_t TQ = 32 * NW;               // pairs per tile
-  constexpr int kUW = (KC + NW - 1) / NW;         // k-chunk loads per wave per block
-  // s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
-  // at their maxima): all but the newest (kNS - 2) blocks' loads, and all
-  constexpr int kRingLoads = (kNS - 2) * (kUW + 1);
-  constexpr int kWaitRing = (kRingLoads & 15) | ((kRingLoads >> 4) << 14) | 0x70 | 0xF00;
-  constexpr int kWaitAll = 0x70 | 0xF00;
-  __shared__ v4u ring[kNS][KC * 64];
-  __shared__ float rxn[kNS][64];  // |x^|^2 of the block (32 values, twice)
-  __shared__ v4u dummy[64];
-  __shared__ float dxn[64];
-  // threshold mode: lane-private candidate slots, moved to the query's list
-  // when full and at the end of each tile (one reservation per move)
-  __shared__ uint2 slots[DENSE ? 1 : 64 * NW * kSlots];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = wave_index();
-  const int col = lane & 31;
-  const int half = lane >> 5;
-  const uint32_t ntiles = a.toff[a.nlist];
-  // Tiles of one list chunk (its pair tiles are consecutive) read the same
-  // blocks: runs of kXcdRun consecutive tiles go to workgroups b, b + 8,
-  // b + 16, ... of one XCD, dispatched together, so the repeat reads hit
-  // that XCD's L2.  A bijection on each round of gridDim.x tiles (a
-  // multiple of kXcd * kXcdRun).
+// of four waves stride over the tiles.  In a tile, wave w takes pairs
+// [32w, 32w+32); with fewer than four groups of 32 pairs, each group has
+// split waves, which take every split-th block of the chunk.  Tiles of one
+// list chunk (its pair tiles are consecutive) read the same blocks: runs of
+// kXcdRun consecutive tiles go to workgroups b, b + 8, b + 16, ... of one
+// XCD, dispatched together, so the repeat reads hit that XCD's L2 (a
+// bijection on each round of gridDim.x tiles, a multiple of kXcd * kXcdRun).
+struct TileWork {
+  uint32_t p, chunk, q0, qend;
+  int split, phase;
+  bool busy;  // wave-uniform: the wave has pairs
+};
+
+__device__ __forceinline__ uint32_t tile_slot() {
   const uint32_t xcd = blockIdx.x % kXcd, y = blockIdx.x / kXcd;
-  const uint32_t slot = ((y / kXcdRun) * kXcd + xcd) * kXcdRun + y % kXcdRun;
-  for (uint32_t t = slot; t < ntiles; t += gridDim.x) {
-    const uint32_t p = a.tl[t];
-    const uint32_t qb = a.qoff[p], qend = a.qoff[p + 1];
-    const uint32_t nqt = (qend - qb + TQ - 1) / TQ;
-    const uint32_t local = t - a.toff[p];
-    const uint32_t chunk = local / nqt;
-    // groups of 32 pairs in the tile; with fewer than NW, each group has
-    // split waves, which take every split-th block of the chunk
-    const uint32_t tq0 = qb + (local - chunk * nqt) * TQ;
-    const uint32_t ng = min((qend - tq0 + 31) / 32, (uint32_t)NW);
-    const int split = NW / (ng == 1 ? 1 : (ng == 2 ? 2 : (ng <= 4 ? 4 : 8)));
-    const int phase = wave % split;
-    const uint32_t q0 = tq0 + (uint32_t)(wave / split) * 32;
-    const bool busy = q0 < qend;  // wave-uniform: the wave has pairs
-    const bool qv = busy && q0 + (uint32_t)col < qend;
-    // lanes past the tile's pairs repeat its last pair, so that every load
-    // below is in bounds without a branch per load (qv keeps them inactive)
-    const uint2 e = a.qlist[min(q0 + (uint32_t)col, qend - 1)];
-    const uint32_t q = e.x, j = e.y;
-    const float* __restrict__ qp = a.queries + (uint64_t)q * a.D;
-    const float* __restrict__ cp = a.centroids + (uint64_t)p * a.D;
-    float r[KC][8];
-    float mx = 0.0f, rn = 0.0f;
-    if (a.vec) {  // whole k-chunks, 16-byte aligned rows: 16-byte loads
+  return ((y / kXcdRun) * kXcd + xcd) * kXcdRun + y % kXcdRun;
+}
+
+__device__ __forceinline__ TileWork tile_work(const ScreenArgs& a, uint32_t t, int wave) {
+  constexpr uint32_t TQ = kTilePairs;
+  TileWork w;
+  w.p = a.tl[t];
+  const uint32_t qb = a.qoff[w.p];
+  w.qend = a.qoff[w.p + 1];
+  const uint32_t nqt = (w.qend - qb + TQ - 1) / TQ;
+  const uint32_t local = t - a.toff[w.p];
+  w.chunk = local / nqt;
+  const uint32_t tq0 = qb + (local - w.chunk * nqt) * TQ;
+  const uint32_t ng = min((w.qend - tq0 + 31) / 32, 4u);
+  w.split = 4 / (ng == 1 ? 1 : (ng == 2 ? 2 : 4));
+  w.phase = wave % w.split;
+  w.q0 = tq0 + (uint32_t)(wave / w.split) * 32;
+  w.busy = w.q0 < w.qend;
+  return w;
+}
+
+// The B operand of the lane's (query, probe) pair: lane l holds the
+// residual r = q - c_p of pair l%32 (the reference's residual, fp32) on
+// dimensions 16kc + 8(l/32) .. +7, scaled by 2^er so that its largest
+// component lies in [2^12, 2^13), as halves; rn = |r|^2 in fp32.  bad when
+// the residual does not fit fp16 (non-finite norm, er beyond +-100).
+template <int KC>
+struct PairOperand {
+  v8h bq[KC];
+  float rn;
+  int er;
+  bool bad;
+};
+
+template <int KC>
+__device__ __forceinline__ void pair_operand(const ScreenArgs& a, uint32_t q, uint32_t p, int half,
+                                             PairOperand<KC>& o) {
+  const float* __restrict__ qp = a.queries + (uint64_t)q * a.D;
+  const float* __restrict__ cp = a.centroids + (uint64_t)p * a.D;
+  float r[KC][8];
+  if (a.vec) {  // whole k-chunks, 16-byte aligned rows: 16-byte loads
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc)
+    for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
-        for (int h4 = 0; h4 < 2; ++h4) {
-          const int d = kc * 16 + 8 * half + 4 * h4;
-          const float4 x = *reinterpret_cast<const float4*>(qp + d);
-          const float4 c = *reinterpret_cast<const float4*>(cp + d);
-          r[kc][4 * h4] = x.x - c.x;  // the reference's residual
-          r[kc][4 * h4 + 1] = x.y - c.y;
-          r[kc][4 * h4 + 2] = x.z - c.z;
-          r[kc][4 * h4 + 3] = x.w - c.w;
-        }
-    } else {
-#pragma unroll
-      for (int kc = 0; kc < KC; ++kc)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int d = kc * 16 + 8 * half + i;
-          r[kc][i] = d < a.D ? qp[d] - cp[d] : 0.0f;
-        }
-    }
+      for (int h4 = 0; h4 < 2; ++h4) {
+        const int d = kc * 16 + 8 * half + 4 * h4;
+        const float4 x = *reinterpret_cast<const float4*>(qp + d);
+        const float4 c = *reinterpret_cast<const float4*>(cp + d);
+        r[kc][4 * h4] = x.x - c.x;
+        r[kc][4 * h4 + 1] = x.y - c.y;
+        r[kc][4 * h4 + 2] = x.z - c.z;
+        r[kc][4 * h4 + 3] = x.w - c.w;
+      }
+  } else {
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        mx = fmaxf(mx, __builtin_fabsf(r[kc][i]));
-        rn = __builtin_fmaf(r[kc][i], r[kc][i], rn);
+        const int d = kc * 16 + 8 * half + i;
+        r[kc][i] = d < a.D ? qp[d] - cp[d] : 0.0f;
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    rn = rn + __shfl_xor(rn, 32);
-    int er = 0;
-    if (mx > 0.0f) {
-      int E;
-      (void)frexpf(mx, &E);
-      er = 13 - E;  // mx * 2^er in [2^12, 2^13)
+  }
+  float mx = 0.0f, rn = 0.0f;
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      mx = fmaxf(mx, __builtin_fabsf(r[kc][i]));
+      rn = __builtin_fmaf(r[kc][i], r[kc][i], rn);
     }
-    const bool bad = !(rn <= 3.0e38f) || er > 100 || er < -100;
-    const bool act = qv && !bad;
-    if (qv && bad && half == 0) atomicOr(&a.force[q], 1);
-    float Tp = -f_inf();  // threshold mode: no append
-    uint32_t o = 0;       // dense mode: buffer offset of the pair
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  rn = rn + __shfl_xor(rn, 32);
+  int er = 0;
+  if (mx > 0.0f) {
+    int E;
+    (void)frexpf(mx, &E);
+    er = 13 - E;  // mx * 2^er in [2^12, 2^13)
+  }
+  const float sc = ldexpf(1.0f, er);
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o.bq[kc][i] = (_Float16)(r[kc][i] * sc);
+  o.rn = rn;
+  o.er = er;
+  o.bad = !(rn <= 3.0e38f) || er > 100 || er < -100;
+}
+
+// The 16 |x^|^2 values of a lane's rows in a block (rows 8(i/4) + 4(l/32) +
+// i%4) from the block's 32 norms in LDS.
+__device__ __forceinline__ void block_norms(const float* __restrict__ sx, int half, float* xs) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float4 x4 = *reinterpret_cast<const float4*>(sx + 8 * g + 4 * half);
+    xs[4 * g] = x4.x;
+    xs[4 * g + 1] = x4.y;
+    xs[4 * g + 2] = x4.z;
+    xs[4 * g + 3] = x4.w;
+  }
+}
+
+// The LDS ring of one workgroup: NS one-block stages, each the block's KC
+// A-operand chunks and its 32 norms.
+template <int KC, int NS>
+struct Ring {
+  v4u blk[NS][KC * 64];
+  float xn[NS][64];
+  v4u dummy[(KC + 3) / 4 * 4 > KC ? 64 : 1];
+  float dxn[64];
+};
+
+// Streams blocks bb .. be-1 of a list (A operands at A, norms at XN)
+// through the ring by direct global-to-LDS loads; block bb + s lands in
+// stage s % NS.  Every wave issues kUW + 1 loads per block (k-chunks w,
+// w + 4, ...; wave 0 also the block's norms; spare loads re-read into a
+// dummy buffer), so waiting for all but the newest NS - 2 blocks' loads is
+// one immediate count, and a workgroup barrier then frees the previous
+// stage.  Blocks past the end re-read the last block.  step(stage, norms,
+// b) runs on the waves whose pairs take block b.  All waves call this.
+template <int KC, int NS, class Step>
+__device__ __forceinline__ void stream_blocks(Ring<KC, NS>& ring, const v4u* __restrict__ A,
+                                              const float* __restrict__ XN, uint32_t bb, uint32_t be, int wave,
+                                              int lane, const TileWork& w, Step&& step) {
+  constexpr int kUW = (KC + 3) / 4;
+  // s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
+  // at their maxima): all but the newest NS - 2 blocks' loads, and all
+  constexpr int kRingLoads = (NS - 2) * (kUW + 1);
+  constexpr int kWaitRing = (kRingLoads & 15) | ((kRingLoads >> 4) << 14) | 0x70 | 0xF00;
+  constexpr int kWaitAll = 0x70 | 0xF00;
+  const uint32_t nst = be - bb;
+  const char* __restrict__ Ab = reinterpret_cast<const char*>(A);
+  const char* __restrict__ Xb = reinterpret_cast<const char*>(XN);
+  const uint32_t lo16 = (uint32_t)lane * 16, lo4 = (uint32_t)(lane & 31) * 4;
+  auto issue = [&](int buf, uint32_t sblk) {
+    const uint32_t bl = bb + min(sblk, nst - 1);
+#pragma unroll
+    for (int i = 0; i < kUW; ++i) {
+      const int u = wave + 4 * i;
+      if (u < KC)
+        lds_load16(Ab + ((uint64_t)bl * KC + u) * 1024 + lo16, &ring.blk[buf][u * 64]);
+      else
+        lds_load16(Ab + (uint64_t)bl * KC * 1024 + lo16, &ring.dummy[0]);
+    }
+    if (wave == 0)
+      lds_load4(Xb + (uint64_t)bl * 128 + lo4, &ring.xn[buf][0]);
+    else
+      lds_load4(Xb + (uint64_t)bl * 128 + lo4, &ring.dxn[0]);
+  };
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i) issue(i, (uint32_t)i);
+  for (uint32_t s = 0; s < nst;) {
+#pragma unroll
+    for (int buf = 0; buf < NS; ++buf) {
+      if (s < nst) {
+        wait_imm<kWaitRing>();  // this wave's loads of block s have landed
+        bare_barrier();         // everyone's have; stage (s-1) % NS is free
+        issue((buf + NS - 1) % NS, s + NS - 1);
+        if (w.busy && (int)(s % w.split) == w.phase) step(ring.blk[buf], ring.xn[buf], bb + s);
+        ++s;
+      }
+    }
+  }
+  wait_imm<kWaitAll>();  // spare loads of the ring's tail
+  bare_barrier();        // the ring is free for the next tile
+}
+
+// Stage A: every screened value s = fma(-2^(1-er-xexp), acc, |r|^2 + |x^|^2)
+// of the pair's first lists goes to the pair's 32-aligned range of the
+// query's buffer (+inf past the list's end, nothing past capA), four rows
+// per 16-byte store, and the pair's bound to epsA.  D[r] of a product is
+// code 8(r/4) + 4(l/32) + r%4 of the block against pair l%32.
+template <int KC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void pq16_dense_kernel(ScreenArgs a) {
+  __shared__ Ring<KC, kNS> ring;
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_index();
+  const int col = lane & 31;
+  const int half = lane >> 5;
+  const uint32_t ntiles = a.toff[a.nlist];
+  for (uint32_t t = tile_slot(); t < ntiles; t += gridDim.x) {
+    const TileWork w = tile_work(a, t, wave);
+    const uint32_t p = w.p;
+    const bool qv = w.busy && w.q0 + (uint32_t)col < w.qend;
+    // lanes past the tile's pairs repeat its last pair, so that every load
+    // is in bounds without a branch per load (qv keeps them inactive)
+    const uint2 e = a.qlist[min(w.q0 + (uint32_t)col, w.qend - 1)];
+    const uint32_t q = e.x, j = e.y;
+    PairOperand<KC> op;
+    pair_operand<KC>(a, q, p, half, op);
+    const bool act = qv && !op.bad;
+    if (qv && op.bad && half == 0) atomicOr(&a.force[q], 1);
+    uint32_t o = 0;  // buffer offset of the pair
     if (act) {
-      const float rnorm = sqrtf(rn) * (1.0f + 0x1p-16f);
+      const float rnorm = sqrtf(op.rn) * (1.0f + 0x1p-16f);
       const float X = sqrtf(__uint_as_float(a.xmax2[p])) * (1.0f + 0x1p-16f);
-      const float eps = pq16_eps(rnorm, X, a);
-      if constexpr (DENSE) {
-        o = a.offA[(uint64_t)q * a.np + j];
-        if (half == 0 && chunk == 0) a.epsA[(uint64_t)q * a.np + j] = eps;
-      } else {
-        const float f = add_up(a.dkA[q], eps) - rn;
-        Tp = f + __builtin_fabsf(f) * 0x1p-22f;
-      }
+      o = a.offA[(uint64_t)q * a.np + j];
+      if (half == 0 && w.chunk == 0) a.epsA[(uint64_t)q * a.np + j] = pq16_eps(rnorm, X, a);
     }
-    const float sc = ldexpf(1.0f, er);
-    v8h bq[KC];
-#pragma unroll
-    for (int kc = 0; kc < KC; ++kc)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) bq[kc][i] = (_Float16)(r[kc][i] * sc);
-    const float cneg = -ldexpf(1.0f, 1 - er - a.xexp);
+    const float cneg = -ldexpf(1.0f, 1 - op.er - a.xexp);
+    const float rn = op.rn;
     const uint32_t b0 = a.bo[p];
     const uint32_t nb = min(a.bo[p + 1] - b0, a.blim);
-    const uint32_t bb = chunk * kCB;
-    const uint32_t be = min(nb, bb + kCB);
-    const uint32_t start = a.list_off[p];
-    const uint32_t len = a.list_off[p + 1] - start;
+    const uint32_t bb = w.chunk * kCB;
+    const uint32_t len = a.list_off[p + 1] - a.list_off[p];
     const v4u* __restrict__ A = reinterpret_cast<const v4u*>(a.data) + (uint64_t)b0 * KC * 64;
-    const float* __restrict__ XN = a.xnb + (uint64_t)b0 * 32;
-    int nslot = 0;
-    auto move = [&](int n) {
-      const uint32_t pos = atomicAdd(&a.ccnt[q], (uint32_t)n);
-      uint2* __restrict__ out = a.cand + (uint64_t)q * a.cap;
-#pragma unroll 1
-      for (int i = 0; i < n; ++i)
-        if (pos + (uint32_t)i < a.cap) out[pos + i] = slots[tid * kSlots + i];
-    };
-    // one block from the ring: KC products, then the mode's epilogue
-    auto block_step = [&](const v4u* __restrict__ sa, const float* __restrict__ sx, uint32_t b) {
+    stream_blocks<KC, kNS>(ring, A, a.xnb + (uint64_t)b0 * 32, bb, min(nb, bb + kCB), wave, lane, w,
+                           [&](const v4u* __restrict__ sa, const float* __restrict__ sx, uint32_t b) {
       // every k-chunk read from LDS before the first product: one LDS
       // round trip per block instead of one per pair of products
       v4u av[KC];
@@ -582,104 +657,161 @@ __global__ __launch_bounds__(64 * NW) void pq16_screen_kernel(ScreenArgs a) {
       v16f acc = {};
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, av[kc]), bq[kc], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, av[kc]), op.bq[kc], acc, 0, 0, 0);
       sched_reads_then_mfma<KC>();
-      const uint32_t rowb = b * 32 + 4 * half;
       float xs[16];
+      block_norms(sx, half, xs);
+      if (act) {
+        const uint32_t rowb = b * 32 + 4 * half;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float4 x4 = *reinterpret_cast<const float4*>(sx + 8 * g + 4 * half);
-        xs[4 * g] = x4.x;
-        xs[4 * g + 1] = x4.y;
-        xs[4 * g + 2] = x4.z;
-        xs[4 * g + 3] = x4.w;
-      }
-      if constexpr (DENSE) {
-        if (act) {
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const uint32_t row = rowb + 8 * g;
-            if (o + row < a.capA) {
-              float4 v;
-              v.x = row + 0 < len ? __builtin_fmaf(cneg, acc[4 * g + 0], rn + xs[4 * g + 0]) : f_inf();
-              v.y = row + 1 < len ? __builtin_fmaf(cneg, acc[4 * g + 1], rn + xs[4 * g + 1]) : f_inf();
-              v.z = row + 2 < len ? __builtin_fmaf(cneg, acc[4 * g + 2], rn + xs[4 * g + 2]) : f_inf();
-              v.w = row + 3 < len ? __builtin_fmaf(cneg, acc[4 * g + 3], rn + xs[4 * g + 3]) : f_inf();
-              *reinterpret_cast<float4*>(a.bufA + (uint64_t)q * a.capA + o + row) = v;
-            }
+        for (int g = 0; g < 4; ++g) {
+          const uint32_t row = rowb + 8 * g;
+          if (o + row < a.capA) {
+            float4 v;
+            v.x = row + 0 < len ? __builtin_fmaf(cneg, acc[4 * g + 0], rn + xs[4 * g + 0]) : f_inf();
+            v.y = row + 1 < len ? __builtin_fmaf(cneg, acc[4 * g + 1], rn + xs[4 * g + 1]) : f_inf();
+            v.z = row + 2 < len ? __builtin_fmaf(cneg, acc[4 * g + 2], rn + xs[4 * g + 2]) : f_inf();
+            v.w = row + 3 < len ? __builtin_fmaf(cneg, acc[4 * g + 3], rn + xs[4 * g + 3]) : f_inf();
+            *reinterpret_cast<float4*>(a.bufA + (uint64_t)q * a.capA + o + row) = v;
           }
         }
-      } else {
-        uint32_t passm = 0;
+      }
+    });
+  }
+}
+
+// Stage B: every probed list against the query's bound.  Tiles and the
+// ring as in stage A.
+//   Test: s'_r = fma(-2^(1-er-xexp), acc_r, |x^_r|^2) <= T' with
+//   T' = dkA + eps - |r|^2 rounded up: a code left out has s' > T', so its
+//   screened distance exceeds dkA + eps by more than the FMA's rounding,
+//   which eps covers.  The 16 values of a lane are reduced to their minimum
+//   first; only lanes whose minimum passes form the row mask.  Rows past
+//   the list's end have |x^|^2 = +inf, so s' = +inf; they are masked
+//   explicitly only where T' is +inf.
+//   Candidates: a lane with a passing row appends one 32-bit entry (row
+//   mask | block in the chunk << 16 | lane << 22) to its wave's LDS queue
+//   at the rank ballot and mbcnt give it: no atomics while blocks stream,
+//   so the ring's loads stay in flight (an atomic with return waits for
+//   every outstanding load).  At the end of the tile (or when the queue is
+//   nearly full) each lane reserves its count in its query's candidate list
+//   with one atomic, and the entries are written out.
+// NS: stages of the ring; W: waves per SIMD the registers are sized for
+// (measured at 1M x 128 codes, nprobe 16: NS 3 at 4 waves per SIMD 0.179 ms;
+// NS 4 at 3 waves 0.186 ms; NS 6 and 8 at 2 waves 0.248 ms).
+template <int KC, int NS, int W>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W))) void pq16_thresh_kernel(ScreenArgs a) {
+  constexpr uint32_t kQ = 256;  // queue entries per wave
+  __shared__ Ring<KC, NS> ring;
+  __shared__ uint32_t wq[4][kQ];
+  __shared__ uint32_t wbase[4][64];  // each lane's next position while flushing
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_index();
+  const int col = lane & 31;
+  const int half = lane >> 5;
+  const uint32_t ntiles = a.toff[a.nlist];
+  for (uint32_t t = tile_slot(); t < ntiles; t += gridDim.x) {
+    const TileWork w = tile_work(a, t, wave);
+    const uint32_t p = w.p;
+    const bool qv = w.busy && w.q0 + (uint32_t)col < w.qend;
+    const uint2 e = a.qlist[min(w.q0 + (uint32_t)col, w.qend - 1)];
+    const uint32_t q = e.x, j = e.y;
+    PairOperand<KC> op;
+    pair_operand<KC>(a, q, p, half, op);
+    if (qv && op.bad && half == 0) atomicOr(&a.force[q], 1);
+    float Tp = -f_inf();  // no append
+    if (qv && !op.bad) {
+      const float rnorm = sqrtf(op.rn) * (1.0f + 0x1p-16f);
+      const float X = sqrtf(__uint_as_float(a.xmax2[p])) * (1.0f + 0x1p-16f);
+      const float f = add_up(a.dkA[q], pq16_eps(rnorm, X, a)) - op.rn;
+      Tp = f + __builtin_fabsf(f) * 0x1p-22f;
+    }
+    const float cneg = -ldexpf(1.0f, 1 - op.er - a.xexp);
+    const uint32_t b0 = a.bo[p];
+    const uint32_t nb = min(a.bo[p + 1] - b0, a.blim);
+    const uint32_t bb = w.chunk * kCB;
+    const uint32_t start = a.list_off[p];
+    const uint32_t len = a.list_off[p + 1] - start;
+    uint32_t* __restrict__ myq = wq[wave];
+    uint32_t qn = 0;   // wave-uniform queue length
+    uint32_t cnt = 0;  // this lane's entries in the queue
+    // Queue to candidate list: one atomic per lane with entries reserves its
+    // range; then 64 entries at a time, each lane takes one, gets its slot
+    // from the owner's running position (an LDS atomic) and writes (list
+    // position of the row base, probe index << 16 | mask).  All lanes call
+    // this (the shuffles take every lane).
+    auto flush = [&]() {
+      wbase[wave][lane] = cnt ? atomicAdd(&a.ccnt[q], cnt) : 0u;
+      cnt = 0;
+      __builtin_amdgcn_wave_barrier();
+      for (uint32_t i0 = 0; i0 < qn; i0 += 64) {
+        const uint32_t i = i0 + (uint32_t)lane;
+        const uint32_t ent = i < qn ? myq[i] : 0u;
+        const int owner = (int)((ent >> 22) & 63);
+        const uint32_t oq = (uint32_t)__shfl((int)q, owner), oj = (uint32_t)__shfl((int)j, owner);
+        if (i < qn) {
+          const uint32_t pos = atomicAdd(&wbase[wave][owner], 1u);
+          if (pos < a.cap) {
+            const uint32_t rowb = (bb + ((ent >> 16) & 63)) * 32 + 4 * (uint32_t)(owner >> 5);
+            a.cand[(uint64_t)oq * a.cap + pos] = make_uint2(start + rowb, (oj << 16) | (ent & 0xFFFFu));
+          }
+        }
+      }
+      qn = 0;
+      __builtin_amdgcn_wave_barrier();
+    };
+    const v4u* __restrict__ A = reinterpret_cast<const v4u*>(a.data) + (uint64_t)b0 * KC * 64;
+    stream_blocks<KC, NS>(ring, A, a.xnb + (uint64_t)b0 * 32, bb, min(nb, bb + kCB), wave, lane, w,
+                          [&](const v4u* __restrict__ sa, const float* __restrict__ sx, uint32_t b) {
+      v16f acc = {};
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr)
-          passm |= (__builtin_fmaf(cneg, acc[rr], xs[rr]) <= Tp ? 1u : 0u) << rr;
-        // rows past the list's end (the last block's padding) never pass
+      for (int kc = 0; kc < KC; ++kc)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, sa[kc * 64 + lane]), op.bq[kc], acc, 0,
+                                                     0, 0);
+      float xs[16];
+      block_norms(sx, half, xs);
+      float s[16];
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) s[rr] = __builtin_fmaf(cneg, acc[rr], xs[rr]);
+      const float m0 = fminf(fminf(s[0], s[1]), s[2]);
+      const float m1 = fminf(fminf(s[3], s[4]), s[5]);
+      const float m2 = fminf(fminf(s[6], s[7]), s[8]);
+      const float m3 = fminf(fminf(s[9], s[10]), s[11]);
+      const float m4 = fminf(fminf(s[12], s[13]), s[14]);
+      const bool pass = fminf(fminf(fminf(m0, m1), fminf(m2, m3)), fminf(m4, s[15])) <= Tp;
+      if (__ballot(pass) == 0) return;
+      const uint32_t rowb = b * 32 + 4 * half;
+      uint32_t passm = 0;
+      if (pass) {
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) passm |= (s[rr] <= Tp ? 1u : 0u) << rr;
+        // rows past the list's end pass only a threshold of +inf
         if (rowb + 28 > len)
 #pragma unroll
           for (int rr = 0; rr < 16; ++rr)
             if (rowb + 8 * (rr >> 2) + (rr & 3) >= len) passm &= ~(1u << rr);
-        // one entry per lane and block with a passing row: the list
-        // position of the lane's row base, the probe index and the 16-row
-        // mask (rows 8(i/4) + i%4 from the base), expanded by the rescoring
-        if (__ballot(passm != 0) != 0) {
-          if (passm != 0) {
-            slots[tid * kSlots + nslot] = make_uint2(start + rowb, (j << 16) | passm);
-            if (++nslot == kSlots) {
-              move(kSlots);
-              nslot = 0;
-            }
-          }
-        }
       }
-    };
-    // The chunk's blocks stream through a ring of kNS one-block LDS buffers
-    // by direct global-to-LDS loads; block bb + s lands in ring[s % kNS].
-    // Every wave issues kUW + 1 loads per block (k-chunks w, w+NW, ...;
-    // wave 0 also the block's |x^|^2; spare loads re-read into a dummy
-    // buffer), so waiting for all but the last (kNS-2) blocks' loads is one
-    // immediate count.  Blocks past the chunk's end re-read its last block.
-    const uint32_t nst = be - bb;
-#define FDB_ISSUE(BUF, S)                                                                               \
-    {                                                                                                   \
-      const uint32_t bl = bb + min((uint32_t)(S), nst - 1);                                             \
-      _Pragma("unroll") for (int i = 0; i < kUW; ++i) {                                                 \
-        const int u = wave + NW * i;                                                                    \
-        if (u < KC)                                                                                     \
-          lds_load16(A + ((uint64_t)bl * KC + u) * 64 + lane, &ring[BUF][u * 64]);                     \
-        else                                                                                            \
-          lds_load16(A + (uint64_t)bl * KC * 64 + lane, &dummy[0]);                                     \
-      }                                                                                                 \
-      if (wave == 0)                                                                                    \
-        lds_load4(XN + (uint64_t)bl * 32 + (lane & 31), &rxn[BUF][0]);                                 \
-      else                                                                                              \
-        lds_load4(XN + (uint64_t)bl * 32 + (lane & 31), &dxn[0]);                                       \
-    }
-    FDB_ISSUE(0, 0)
-    FDB_ISSUE(1, 1)
-    FDB_ISSUE(2, 2)
-#define FDB_STEP(BUF)                                                                                   \
-    if (s < nst) {                                                                                      \
-      wait_imm<kWaitRing>();  /* this wave's loads of block s have landed */                            \
-      bare_barrier();         /* everyone's have; ring[(s-1) % kNS] is free */                          \
-      FDB_ISSUE((BUF + kNS - 1) % kNS, s + kNS - 1)                                                     \
-      if (busy && (int)(s % split) == phase) block_step(ring[BUF], rxn[BUF], bb + s);                   \
-      ++s;                                                                                              \
-    }
-    for (uint32_t s = 0; s < nst;) {
-      FDB_STEP(0)
-      FDB_STEP(1)
-      FDB_STEP(2)
-      FDB_STEP(3)
-    }
-#undef FDB_STEP
-#undef FDB_ISSUE
-    wait_imm<kWaitAll>();  // spare loads of the ring's tail
-    bare_barrier();        // the ring is free for the next tile
-    if constexpr (!DENSE) {
-      if (nslot > 0) move(nslot);
-    }
+      // one entry per lane and block with a passing row: its 16-row mask
+      // (rows 8(i/4) + i%4 from the lane's row base)
+      const uint64_t bal = __ballot(passm != 0);
+      if (bal == 0) return;
+      if (passm != 0) {
+        const uint32_t rank =
+            __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        myq[qn + rank] = passm | ((b - bb) << 16) | ((uint32_t)lane << 22);
+        ++cnt;
+      }
+      qn += (uint32_t)__popcll(bal);
+      if (qn > kQ - 64) flush();
+    });
+    if (qn > 0) flush();
   }
+}
+
+// Stage B's registers: the B operand takes 4 * KC of them
+template <int KC>
+void (*thresh_kernel())(ScreenArgs) {
+  return pq16_thresh_kernel<KC, 3, (KC <= 8 ? 4 : (KC <= 12 ? 3 : 2))>;
 }
 
 // One wave per query: dkA = (k-th smallest kept screened value) + the
@@ -1544,7 +1676,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   const uint64_t chunk = cdiv(npr, G);
   // tiles of a stage: at most (pairs / 128 + lists) pair tiles per chunk
   auto tile_bound = [&](uint32_t blim) {
-    return (cdiv(npr, 32 * kWavesA) + nlist) * cdiv(std::min<uint64_t>(L.max_blocks, blim), kCB);
+    return (cdiv(npr, kTilePairs) + nlist) * cdiv(std::min<uint64_t>(L.max_blocks, blim), kCB);
   };
   const uint64_t tbA = tile_bound(capA / 32), tbB = tile_bound(0xFFFFFFFFu);
   tl_.reserve(std::max<uint64_t>(tbA + tbB, 1));
@@ -1554,8 +1686,8 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   pst.s1 = PairSet{a.probes, nq, np, nullptr, nlist, chunk};
   pst.blim0 = capA / 32;
   pst.blim1 = 0xFFFFFFFFu;
-  pst.tq0 = 32 * kWavesA;
-  pst.tq1 = 32 * waves_b(L.KC);
+  pst.tq0 = kTilePairs;
+  pst.tq1 = kTilePairs;
   pst.G = G;
   pst.H = H_.p;
   pst.qoff = qoff_.p;
@@ -1600,8 +1732,8 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   switch (L.KC) {
 #define FDB_KC(n)                                  \
   case n:                                          \
-    dense = pq16_screen_kernel<n, true, kWavesA>;   \
-    thresh = pq16_screen_kernel<n, false, waves_b(n)>; \
+    dense = pq16_dense_kernel<n>;                  \
+    thresh = thresh_kernel<n>();                   \
     break;
     FDB_KC(1) FDB_KC(2) FDB_KC(3) FDB_KC(4) FDB_KC(5) FDB_KC(6) FDB_KC(7) FDB_KC(8)
     FDB_KC(9) FDB_KC(10) FDB_KC(11) FDB_KC(12) FDB_KC(13) FDB_KC(14) FDB_KC(15) FDB_KC(16)
@@ -1617,7 +1749,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   sa.tl = tl_.p;
   sa.qlist = qlist_.p;
   sa.blim = capA / 32;
-  hipLaunchKernelGGL(dense, dim3(grid), dim3(64 * kWavesA), 0, s, sa);
+  hipLaunchKernelGGL(dense, dim3(grid), dim3(256), 0, s, sa);
   FDB_HIP(hipGetLastError());
   const int R = list_regs(a.k);
   switch (R) {
@@ -1640,7 +1772,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   sa.qlist = qlist_.p + std::max<uint64_t>(npr, 1);
   sa.blim = 0xFFFFFFFFu;
   if (timing_) FDB_HIP(hipEventRecord(tev_[0], s));
-  hipLaunchKernelGGL(thresh, dim3(grid), dim3(64 * waves_b(L.KC)), 0, s, sa);
+  hipLaunchKernelGGL(thresh, dim3(grid), dim3(256), 0, s, sa);
   FDB_HIP(hipGetLastError());
   if (timing_) {
     FDB_HIP(hipEventRecord(tev_[1], s));

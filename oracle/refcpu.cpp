@@ -15,6 +15,7 @@
 #include <map>
 #include <queue>
 #include <thread>
+#include <unordered_map>
 #include <unordered_set>
 #include <vector>
 
@@ -544,7 +545,9 @@ struct fdbo_ivfpq {
   std::vector<uint64_t> ids;     // [N], list order
   std::vector<uint8_t> codes;    // [N][M], list order
   std::atomic<uint64_t> nprobe{1};
-  std::vector<float> originals;  // [N][dim] list order, when reranking is on
+  // original_vectors: Option<RwLock<HashMap<u64, Vector>>> (ivf_pq.rs:356)
+  bool reranking = false;
+  std::unordered_map<uint64_t, std::vector<float>> originals;
   uint64_t rerank_factor = 1;
   // PartitionData::tombstones (ivf_pq.rs:190): ids per list; sized on first use
   std::vector<std::unordered_set<uint64_t>> tomb;
@@ -672,8 +675,24 @@ void fdbo_ivfpq_set_nprobe(fdbo_ivfpq* h, uint64_t nprobe) {
 uint64_t fdbo_ivfpq_nprobe(const fdbo_ivfpq* h) { return h->nprobe.load(std::memory_order_relaxed); }
 
 void fdbo_ivfpq_enable_reranking(fdbo_ivfpq* h, const float* v, uint64_t factor) {
-  h->originals.assign(v, v + h->offsets.back() * (uint64_t)h->dim);
+  // enable_reranking (:513-517): the vectors collected into a map by id (a
+  // later vector of an id replaces an earlier one), factor at least 1
+  h->originals.clear();
+  for (uint64_t p = 0; p < h->offsets.back(); ++p)
+    h->originals[h->ids[p]].assign(v + p * h->dim, v + (p + 1) * h->dim);
+  h->reranking = true;
   h->rerank_factor = std::max<uint64_t>(factor, 1);
+}
+
+// from_serializable (ivf_pq.rs:1918-1925, 1940): original_vectors from
+// (id, vector) records, a later record of an id replacing an earlier one;
+// the rerank factor as stored
+void fdbo_ivfpq_set_originals(fdbo_ivfpq* h, const uint64_t* ids, const float* v, uint64_t n,
+                              uint64_t factor) {
+  h->originals.clear();
+  for (uint64_t i = 0; i < n; ++i) h->originals[ids[i]].assign(v + i * h->dim, v + (i + 1) * h->dim);
+  h->reranking = true;
+  h->rerank_factor = factor;
 }
 
 namespace {
@@ -698,11 +717,13 @@ int select_probes(const fdbo_ivfpq* h, const float* q, uint64_t count, int32_t* 
 // then a stable ascending sort and truncation.  Originals are addressed by
 // list position here; the reference looks them up by id.
 int rerank(const fdbo_ivfpq* h, const float* q, std::vector<std::pair<uint64_t, float>>& cand,
-           const std::vector<uint64_t>& pos, int k, uint64_t* out_ids, float* out_d) {
+           int k, uint64_t* out_ids, float* out_d) {
   std::vector<std::pair<uint64_t, float>> rr;
-  for (size_t i = 0; i < cand.size(); ++i)
-    rr.push_back({cand[i].first,
-                  std::sqrt(l2sq_avx2(q, &h->originals[pos[i] * h->dim], (size_t)h->dim))});
+  for (size_t i = 0; i < cand.size(); ++i) {
+    auto it = h->originals.find(cand[i].first);  // filter_map: no vector, no result
+    if (it == h->originals.end()) continue;
+    rr.push_back({cand[i].first, std::sqrt(l2sq_avx2(q, it->second.data(), (size_t)h->dim))});
+  }
   std::stable_sort(rr.begin(), rr.end(), [](auto& a, auto& b) { return a.second < b.second; });
   int cnt = std::min<int>((int)rr.size(), k);
   for (int i = 0; i < cnt; ++i) {
@@ -743,14 +764,10 @@ int finish(const fdbo_ivfpq* h, const float* q, PosHeap& heap, int k, uint64_t* 
   }
   std::reverse(v.begin(), v.end());
   std::stable_sort(v.begin(), v.end(), [](const PosItem& a, const PosItem& b) { return a.d < b.d; });
-  if (!h->originals.empty()) {
+  if (h->reranking) {
     std::vector<std::pair<uint64_t, float>> cand;
-    std::vector<uint64_t> pos;
-    for (auto& it : v) {
-      cand.push_back({h->ids[it.pos], it.d});
-      pos.push_back(it.pos);
-    }
-    return rerank(h, q, cand, pos, k, out_ids, out_d);
+    for (auto& it : v) cand.push_back({h->ids[it.pos], it.d});
+    return rerank(h, q, cand, k, out_ids, out_d);
   }
   int cnt = std::min<int>((int)v.size(), k);
   for (int i = 0; i < cnt; ++i) {
@@ -769,7 +786,7 @@ int fdbo_ivfpq_probes(const fdbo_ivfpq* h, const float* q, uint64_t nprobe, int3
 // IVFPQIndex::search, ivf_pq.rs:590-677
 int fdbo_ivfpq_search(const fdbo_ivfpq* h, const float* q, int k, uint64_t* out_ids,
                       float* out_dists) {
-  const uint64_t fetch_k = h->originals.empty() ? (uint64_t)k : (uint64_t)k * h->rerank_factor;
+  const uint64_t fetch_k = !h->reranking ? (uint64_t)k : (uint64_t)k * h->rerank_factor;
   uint64_t nprobe = h->nprobe.load(std::memory_order_relaxed);
   std::vector<int32_t> lists(h->nlist);
   int np = select_probes(h, q, nprobe, lists.data(), nullptr);
@@ -799,7 +816,7 @@ int fdbo_ivfpq_search(const fdbo_ivfpq* h, const float* q, int k, uint64_t* out_
 void fdbo_ivfpq_batch_search(const fdbo_ivfpq* h, const float* queries, uint64_t nq, int k,
                              uint64_t* out_ids, float* out_dists, int32_t* out_counts) {
   if (nq == 0) return;
-  const uint64_t fetch_k = h->originals.empty() ? (uint64_t)k : (uint64_t)k * h->rerank_factor;
+  const uint64_t fetch_k = !h->reranking ? (uint64_t)k : (uint64_t)k * h->rerank_factor;
   const int dim = h->dim, M = h->M;
   uint64_t nprobe = h->nprobe.load(std::memory_order_relaxed);
   // [..=nth] with nth = min(nprobe, nlist).saturating_sub(1): nprobe 0 probes 1 list (:877-881)
@@ -857,7 +874,7 @@ int fdbo_ivfpq_search_filtered(const fdbo_ivfpq* h, const float* q, int k, const
                                uint64_t n_allowed, uint64_t* out_ids, float* out_dists) {
   if (n_allowed == 0) return 0;  // :700-703
   std::unordered_set<uint64_t> allow(allowed, allowed + n_allowed);
-  const uint64_t fetch_k = h->originals.empty() ? (uint64_t)k : (uint64_t)k * h->rerank_factor;
+  const uint64_t fetch_k = !h->reranking ? (uint64_t)k : (uint64_t)k * h->rerank_factor;
   const uint64_t filter_fetch_k = fetch_k * 4;  // :712
   uint64_t nprobe = h->nprobe.load(std::memory_order_relaxed);
   std::vector<int32_t> lists(h->nlist);
@@ -890,6 +907,7 @@ int fdbo_ivfpq_delete(fdbo_ivfpq* h, uint64_t id) {
     for (uint64_t j = h->offsets[l]; j < h->offsets[l + 1]; ++j)
       if (h->ids[j] == id) {
         h->tomb[l].insert(id);
+        if (h->reranking) h->originals.erase(id);  // :1793-1797
         return 1;
       }
   }
@@ -917,8 +935,7 @@ void fdbo_ivfpq_insert(fdbo_ivfpq* h, const float* vectors, const uint64_t* ids,
     const uint64_t at = h->offsets[l + 1];
     h->ids.insert(h->ids.begin() + at, ids[i]);
     h->codes.insert(h->codes.begin() + at * M, code.begin(), code.end());
-    if (!h->originals.empty())
-      h->originals.insert(h->originals.begin() + at * dim, v, v + dim);
+    if (h->reranking) h->originals[ids[i]].assign(v, v + dim);  // :1769-1773
     for (int t = l + 1; t <= h->nlist; ++t) h->offsets[t]++;
     h->tomb[l].erase(ids[i]);
   }
@@ -927,17 +944,14 @@ void fdbo_ivfpq_insert(fdbo_ivfpq* h, const float* vectors, const uint64_t* ids,
 // compact, ivf_pq.rs:1828-1851
 void fdbo_ivfpq_compact(fdbo_ivfpq* h) {
   if (h->tomb.empty()) return;
-  const int dim = h->dim, M = h->M;
+  const int M = h->M;
   std::vector<uint64_t> offs(h->nlist + 1, 0), ids;
   std::vector<uint8_t> codes;
-  std::vector<float> orig;
   for (int l = 0; l < h->nlist; ++l) {
     for (uint64_t j = h->offsets[l]; j < h->offsets[l + 1]; ++j) {
       if (h->tomb[l].count(h->ids[j])) continue;
       ids.push_back(h->ids[j]);
       codes.insert(codes.end(), &h->codes[j * M], &h->codes[j * M] + M);
-      if (!h->originals.empty())
-        orig.insert(orig.end(), &h->originals[j * dim], &h->originals[j * dim] + dim);
     }
     offs[l + 1] = ids.size();
     h->tomb[l].clear();
@@ -945,7 +959,6 @@ void fdbo_ivfpq_compact(fdbo_ivfpq* h) {
   h->offsets.swap(offs);
   h->ids.swap(ids);
   h->codes.swap(codes);
-  if (!h->originals.empty()) h->originals.swap(orig);
 }
 
 // batch_search_parallel, ivf_pq.rs:1060-1084

@@ -93,9 +93,13 @@ void fdbo_ivfpq_export(const fdbo_ivfpq* h, float* centroids, float* codebooks,
                        uint64_t* list_offsets, uint64_t* ids, uint8_t* codes);
 void fdbo_ivfpq_set_nprobe(fdbo_ivfpq* h, uint64_t nprobe);          /* :524-527 */
 uint64_t fdbo_ivfpq_nprobe(const fdbo_ivfpq* h);
-/* rerank: original vectors in list order (same positions as codes) */
+/* rerank: original vectors in list order (same positions as codes), kept
+   as a map id -> vector like original_vectors */
 void fdbo_ivfpq_enable_reranking(fdbo_ivfpq* h, const float* vectors_list_order,
                                  uint64_t rerank_factor);            /* :513-517 */
+/* original_vectors from (id, vector) records, rerank factor as stored */
+void fdbo_ivfpq_set_originals(fdbo_ivfpq* h, const uint64_t* ids, const float* vectors,
+                              uint64_t n, uint64_t rerank_factor);   /* :1918-1940 */
 /* coarse selection as search() does it (:538-553); out sorted by (dist, idx) */
 int fdbo_ivfpq_probes(const fdbo_ivfpq* h, const float* q, uint64_t nprobe,
                       int32_t* out_lists, float* out_dists);

@@ -67,6 +67,8 @@ def lib() -> C.CDLL:
     L.fdbo_ivfpq_nprobe.restype = u64
     L.fdbo_ivfpq_enable_reranking.argtypes = [_P, _P, u64]
     L.fdbo_ivfpq_enable_reranking.restype = None
+    L.fdbo_ivfpq_set_originals.argtypes = [_P, _P, _P, u64, u64]
+    L.fdbo_ivfpq_set_originals.restype = None
     L.fdbo_ivfpq_probes.argtypes = [_P, _P, u64, _P, _P]
     L.fdbo_ivfpq_probes.restype = i32
     L.fdbo_ivfpq_search.argtypes = [_P, _P, i32, _P, _P]
@@ -227,6 +229,12 @@ class IvfPq:
     def enable_reranking(self, vectors_list_order, factor: int):
         v = _f(vectors_list_order)
         lib().fdbo_ivfpq_enable_reranking(self.h, _p(v), factor)
+
+    def set_originals(self, ids, vectors, factor: int):
+        """original_vectors as a loaded file holds them: (id, vector) records."""
+        idv = np.ascontiguousarray(ids, np.uint64)
+        v = _f(np.asarray(vectors, np.float32).reshape(len(idv), self.dim))
+        lib().fdbo_ivfpq_set_originals(self.h, _p(idv), _p(v), len(idv), factor)
 
     def probes(self, q, nprobe: int):
         q = _f(q)

@@ -653,3 +653,55 @@ def test_assignment_takes_the_first_of_twin_centroids():
     ix.insert(v, np.arange(40, dtype=np.uint64))
     off = ix.export()["list_offsets"].astype(np.int64)
     assert off[2] - off[1] == 40 and off[4] - off[3] == 0
+
+
+def test_rerank_follows_original_vectors_by_id():
+    """original_vectors is a map id -> vector (ivf_pq.rs:356): delete removes
+    the id's vector (:1793-1797), insert_batch replaces it (:1769-1773), a
+    loaded file holds whatever records were saved (:1918-1925); rerank_results
+    drops candidates without one (filter_map, :562-571).  Duplicate ids make
+    one map entry serve several list entries."""
+    from forgedb import datagen
+    base, queries = datagen.workload("ivfpq_int", n=3000, nq=8)
+    base[2000:2100] = base[0:100]  # ids 2000..2099 duplicate the rows of 0..99
+    ix = refcpu.IvfPq.build(base, nlist=8, M=16, seed=5)
+    art = ix.export()
+    # duplicate ids: list entries 0..99 of id 500..599 too
+    ids = art["ids"].copy()
+    ids[ids < 100] += 500
+    plain = refcpu.IvfPq.create(art["centroids"], art["codebooks"], art["list_offsets"], ids, art["codes"])
+    rr = refcpu.IvfPq.create(art["centroids"], art["codebooks"], art["list_offsets"], ids, art["codes"])
+    rr.enable_reranking(base[art["ids"].astype(np.int64)], 3)
+    for h in (plain, rr):
+        h.set_nprobe(8)
+    # the map after enable_reranking: the last vector of each id in list order
+    orig = {}
+    for p, i in enumerate(ids):
+        orig[int(i)] = base[int(art["ids"][p])]
+    k = 10
+
+    def check(tag):
+        for q in np.concatenate([queries, base[500:503], base[50:53]]):
+            pool, _ = plain.search(q, k * 3)
+            want = _rerank_model(q, pool, orig, k)
+            gi, gd = rr.search(q, k)
+            assert [int(i) for i in gi] == [i for i, _ in want], tag
+            assert np.array_equal(gd, np.array([d for _, d in want], np.float32)), tag
+
+    check("enable")
+    # delete: one list entry tombstoned, the id's vector gone for all entries
+    victim = int(ids[np.where(ids == 510)[0][0]])
+    assert rr.delete(victim) and plain.delete(victim)
+    del orig[victim]
+    check("delete")
+    # insert of an existing id: every entry of it reranks with the new vector
+    newv = (base[520] + 3.0).astype(np.float32)
+    rr.insert(newv[None], np.array([520], np.uint64))
+    plain.insert(newv[None], np.array([520], np.uint64))
+    orig[520] = newv
+    check("insert")
+    # a loaded file's records: only some ids have vectors
+    keep = [i for i in sorted(orig) if i % 3]
+    rr.set_originals(np.array(keep, np.uint64), np.stack([orig[i] for i in keep]), 3)
+    orig = {i: orig[i] for i in keep}
+    check("records")
