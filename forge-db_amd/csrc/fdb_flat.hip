@@ -715,16 +715,6 @@ unsigned nblocks(uint64_t n, unsigned t) { return (unsigned)((n + t - 1) / t); }
 
 __global__ void clear_u32(uint32_t* p) { *p = 0; }
 
-__global__ void nan_flag_kernel(const float* __restrict__ q, uint64_t n, int* err) {
-  const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e < n && q[e] != q[e]) atomicOr(err, 1);
-}
-
-__global__ void keys_to_lists_kernel(const uint64_t* __restrict__ keys, uint64_t n, int32_t* __restrict__ out) {
-  const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e < n) out[e] = keys[e] == ~0ull ? -1 : (int32_t)keys[e];
-}
-
 __global__ void fill_empty(uint64_t n, uint32_t k, uint64_t* ids, float* d, uint32_t* c) {
   const uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e < n * k) {
@@ -1039,61 +1029,36 @@ void FlatSearcher::screen(const FlatRows& x, int metric, const float* d_qs, cons
   exact(x, metric, d_qs, q_norm, nq, k, d_ids, d_dists, d_counts, s, flags_.p);
 }
 
-hipError_t launch_keys_to_lists(const uint64_t* keys, uint64_t n, int32_t* out, hipStream_t s) {
-  if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(keys_to_lists_kernel, dim3(nblocks(n, 256)), dim3(256), 0, s, keys, n, out);
-  return hipGetLastError();
-}
-
 void CoarseQuantizer::init(const float* centroids, const float* centT, uint32_t nlist, uint32_t dim,
                            hipStream_t s) {
   cent_ = centroids;
   centT_ = centT;
   nlist_ = nlist;
   dim_ = dim;
-  cnorm_.reserve(nlist);
-  FDB_HIP(launch_row_norms(centroids, nlist, (int)dim, cnorm_.p, s));
-  std::vector<float> rn(nlist);
-  FDB_HIP(hipMemcpyAsync(rn.data(), cnorm_.p, 4 * (size_t)nlist, hipMemcpyDeviceToHost, s));
-  FDB_HIP(hipStreamSynchronize(s));
-  rnmax_ = 0.0f;
-  for (float v : rn) rnmax_ = std::max(rnmax_, v);
+  c16_.build(centroids, nlist, dim, s);
 }
 
-// Automatic mode takes the exact kernel: at nlist 1024-4096 (10,000 queries,
-// nprobe 16-64) it measured 0.15-0.48 ms against 0.28-1.07 ms screened, the
-// screen's fixed cost per workgroup dominating so few centroids.
+// Screening (fdb_coarse16.hpp) where it applies, then the exact kernel on the
+// queries it flagged; else the exact kernel, in parts for batches too small
+// to fill the GPU.
 void CoarseQuantizer::select(const float* d_qs, uint64_t nq, uint32_t np, int32_t* probes, float* dists,
                              int* err, hipStream_t s) {
   if (nq == 0 || np == 0) return;
-  const bool screen =
-      mode_ == 2 && FlatSearcher::screenable(FDB_METRIC_EUCLIDEAN_SQUARED, (int)dim_, np) && nlist_ > 64;
-  if (!screen) {
-    const uint64_t parts = (uint64_t)coarse_parts(nq, (int)nlist_, (int)np);
-    const uint64_t cap = parts > 1 ? nq * parts * np : 0;
-    if (cap) {
-      part_d_.reserve(cap);
-      part_k_.reserve(cap);
-    }
-    FDB_HIP(launch_coarse_select(d_qs, nq, (int)dim_, centT_, (int)nlist_, (int)np, probes, dists, err, s,
-                                 part_d_.p, part_k_.p, cap));
+  if (mode_ != 1 && nlist_ >= 256 && c16_.serves(np)) {
+    flags_.reserve(nq);
+    c16_.select(d_qs, nq, np, cent_, probes, dists, flags_.p, s);
+    FDB_HIP(launch_coarse_select(d_qs, nq, (int)dim_, centT_, (int)nlist_, (int)np, probes, dists, err, s, nullptr,
+                                 nullptr, 0, flags_.p));
     return;
   }
-  // the exact kernel reports NaN distances; here a NaN query is looked for
-  hipLaunchKernelGGL(nan_flag_kernel, dim3(nblocks(nq * dim_, 256)), dim3(256), 0, s, d_qs, nq * dim_, err);
-  FDB_HIP(hipGetLastError());
-  qn_.reserve(nq);
-  FDB_HIP(launch_row_norms(d_qs, nq, (int)dim_, qn_.p, s));
-  keys_.reserve(nq * np);
-  cnt_.reserve(nq);
-  float* d = dists;
-  if (!d) {
-    dtmp_.reserve(nq * np);
-    d = dtmp_.p;
+  const uint64_t parts = (uint64_t)coarse_parts(nq, (int)nlist_, (int)np);
+  const uint64_t cap = parts > 1 ? nq * parts * np : 0;
+  if (cap) {
+    part_d_.reserve(cap);
+    part_k_.reserve(cap);
   }
-  const FlatRows x{centT_, (uint64_t)centT_ld((int)nlist_), nlist_, (int)dim_, cent_, cnorm_.p, rnmax_, nullptr};
-  srch_.screen(x, FDB_METRIC_EUCLIDEAN_SQUARED, d_qs, qn_.p, nq, np, keys_.p, d, cnt_.p, s);
-  FDB_HIP(launch_keys_to_lists(keys_.p, nq * np, probes, s));
+  FDB_HIP(launch_coarse_select(d_qs, nq, (int)dim_, centT_, (int)nlist_, (int)np, probes, dists, err, s,
+                               part_d_.p, part_k_.p, cap));
 }
 
 // Automatic mode screens when there are at least 2^26 (query, row) pairs;

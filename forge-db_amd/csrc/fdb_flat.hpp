@@ -6,6 +6,7 @@
 #include <mutex>
 #include <vector>
 
+#include "fdb_coarse16.hpp"
 #include "fdb_host.hpp"
 
 namespace fdb {
@@ -223,22 +224,19 @@ class FlatSearcher {
   DevBuf<uint2> buf_;
 };
 
-// Keys [n] as written by FlatSearcher with ids == nullptr (~0 = none) -> int32
-// list ids (-1 = none).
-hipError_t launch_keys_to_lists(const uint64_t* keys, uint64_t n, int32_t* out, hipStream_t s);
-
 // ---- coarse quantizer ---------------------------------------------------------
 
 // Selection of the nprobe nearest of nlist centroids (squared L2 in the
 // reference's order, ascending by (distance, list id)): the exact VALU kernel
-// (launch_coarse_select) or MFMA screening + exact rescoring, which returns
-// the same lists and distances.
+// (launch_coarse_select) or fp16 matrix-core screening with exact rescoring
+// (Coarse16, fdb_coarse16.hpp), which returns the same lists and distances.
 class CoarseQuantizer {
  public:
   // centroids [nlist][dim] and their transposed copy (launch_transpose_centroids),
-  // both device-resident and owned by the caller; computes the norms
+  // both device-resident and owned by the caller; builds the fp16 blocks
   void init(const float* centroids, const float* centT, uint32_t nlist, uint32_t dim, hipStream_t s);
-  // 0 = automatic, 1 = exact kernel only, 2 = screening where it applies
+  // 0 = automatic (screening where it applies: nprobe <= 64 and nlist >=
+  // 256), 1 = exact kernel only, 2 = screening where it applies
   void set_mode(int m) { mode_ = m; }
   // probes [nq][np] (np <= nlist, <= 1024); dists [nq][np] nullable; a NaN
   // distance ORs 1 into *err
@@ -250,11 +248,10 @@ class CoarseQuantizer {
   const float* centT_ = nullptr;
   uint32_t nlist_ = 0, dim_ = 0;
   int mode_ = 0;
-  float rnmax_ = 0.0f;
-  FlatSearcher srch_;
-  DevBuf<float> cnorm_, qn_, dtmp_, part_d_;
-  DevBuf<uint64_t> keys_;
-  DevBuf<uint32_t> cnt_, part_k_;
+  Coarse16 c16_;
+  DevBuf<int> flags_;
+  DevBuf<float> part_d_;
+  DevBuf<uint32_t> part_k_;
 };
 
 // ---- BruteForceIndex ------------------------------------------------------

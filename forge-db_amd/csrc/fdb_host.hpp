@@ -102,6 +102,35 @@ struct OrderedOn {
   OrderedOn& operator=(const OrderedOn&) = delete;
 };
 
+// Coefficients of the fp16 screening bound |s - d| <= c_dot |r| X' +
+// c_sq (|r| + X')^2, X' = X + cabs, for s = |r|^2 + |x|^2 - 2<r^, x^> with
+// r^, x^ the operands scaled into [2^12, 2^13) and rounded to fp16, the
+// product accumulated in fp32 on the matrix cores, against a reference
+// value d that is a sum of non-negative terms each rounded at most n_ref
+// times.  With u = 2^-24, uh = 2^-11 and D16 the padded dimension:
+//   each converted component is within uh relative plus 2^-26 of the
+//   operand's largest component (flushed fp16 subnormals included), so
+//   <r^, x^> (unscaled) is within h' |r| X' of <r, x>, where
+//   h' = 2uh + uh^2 + 2.002 * 2^-26 sqrt(D16) + 1.002 g2,
+//   g2 = 2u D16 / (1 - 2u D16) covering fp32 accumulation in any order
+//   (rounded or truncated), and X' = X + 2^-26 sqrt(D16) cmax for rows of
+//   norm <= X and largest component cmax;
+//   |r|^2 and |x|^2 in fp32 are within gamma_D16 (|r| + X)^2 together, the
+//   final add and FMA within 3u (|r| + X')^2, and the reference's rounding
+//   within gamma_(n_ref) d <= gamma_(n_ref) (|r| + X)^2.
+// Everything gets a 1.1 slack factor.
+inline void screen_eps_coeffs(int D16, int n_ref, float cmax, float& c_dot, float& c_sq, float& cabs) {
+  const double u = std::ldexp(1.0, -24), uh = std::ldexp(1.0, -11);
+  const double g2 = 2.0 * u * D16 / (1.0 - 2.0 * u * D16);
+  const double hp = 2.0 * uh + uh * uh + 2.002 * std::ldexp(1.0, -26) * std::sqrt((double)D16) + 1.002 * g2 +
+                    D16 * std::ldexp(1.0, -52);
+  const double gD = D16 * u / (1.0 - D16 * u);
+  const double ga = n_ref * u / (1.0 - n_ref * u);
+  c_dot = (float)(1.1 * 2.0 * hp);
+  c_sq = (float)(1.1 * (gD + 3.0 * u + ga));
+  cabs = (float)(1.0001 * std::ldexp(1.0, -26) * std::sqrt((double)D16) * cmax);
+}
+
 // Squared L2 in the reference's AVX2 order (src/distance/simd.rs:335-366),
 // scalar: 8 FMA lanes, lanes summed from -0.0 left to right, scalar tail.
 inline float host_l2sq_ref(const float* a, const float* b, int n) {

@@ -1497,30 +1497,12 @@ __global__ __launch_bounds__(1024) void pq16_stats_kernel(const int* __restrict_
   }
 }
 
-// Bound coefficients.  With u = 2^-24, uh = 2^-11 and D16 the padded
-// dimension, on components scaled into [2^12, 2^13) (rows: the codebooks'
-// largest component; a query: its residual's):
-//   each converted component is within uh relative plus 2^-26 of that
-//   largest component (flushed fp16 subnormals included), so the scaled
-//   product <r^, x^> is within h' |r| X' of <r, x^>, where
-//   h' = 2uh + uh^2 + 2.002 * 2^-26 sqrt(D16) + 1.002 g2, g2 = 2u D16/(1 - 2u D16)
-//   covers fp32 accumulation in any order (rounded or truncated), and
-//   X' = X + 2^-26 sqrt(D16) cmax for codes of norm <= X;
-//   |r|^2 and |x^|^2 in fp32 are within gamma_D16 (|r| + X)^2 together, the
-//   final add and FMA within 3u (|r| + X')^2, and the reference's own table
-//   distance within gamma_(dsub + M + 2) of the exact value (sums of
-//   non-negative terms).  Everything gets a 1.1 slack factor.
+// Bound coefficients (screen_eps_coeffs): the reference's table distance is
+// a sum of M table entries, each a sum of dsub squares of differences, so a
+// term is rounded at most dsub + M + 2 times (the residual's and the
+// difference's subtractions included).
 void pq16_eps_coeffs(int D16, int M, int dsub, float cmax, float& c_dot, float& c_sq, float& cabs) {
-  const double u = std::ldexp(1.0, -24), uh = std::ldexp(1.0, -11);
-  const double g2 = 2.0 * u * D16 / (1.0 - 2.0 * u * D16);
-  const double hp = 2.0 * uh + uh * uh + 2.002 * std::ldexp(1.0, -26) * std::sqrt((double)D16) + 1.002 * g2 +
-                    D16 * std::ldexp(1.0, -52);
-  const double gD = D16 * u / (1.0 - D16 * u);
-  const int na = dsub + M + 2;
-  const double ga = na * u / (1.0 - na * u);
-  c_dot = (float)(1.1 * 2.0 * hp);
-  c_sq = (float)(1.1 * (gD + 3.0 * u + ga));
-  cabs = (float)(1.0001 * std::ldexp(1.0, -26) * std::sqrt((double)D16) * cmax);
+  screen_eps_coeffs(D16, dsub + M + 2, cmax, c_dot, c_sq, cabs);
 }
 
 }  // namespace

@@ -55,7 +55,7 @@ __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
     const float* __restrict__ queries, uint64_t nq, int dim, const float* __restrict__ centT,
     int ldc, int nlist, int nsel, int32_t* __restrict__ out_lists, float* __restrict__ out_dists,
     int* __restrict__ err_flag, int part_len, float* __restrict__ part_d,
-    uint32_t* __restrict__ part_k) {
+    uint32_t* __restrict__ part_k, const int* __restrict__ only) {
   extern __shared__ float qsT[];  // [dim][QB], rows permuted
   __shared__ uint2 s_queue[kThreads / 64][kCoarseTQ][64];
   const int tid = threadIdx.x;
@@ -63,6 +63,13 @@ __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
   const int wave = tid >> 6;
   const uint64_t q0 = (uint64_t)blockIdx.x * kCoarseQB;
   const int d8 = D8T ? D8T : dim / 8;
+  if (only) {
+    // only the workgroups holding a flagged query run; the others' lists
+    // are already written (and would be the same)
+    bool any = false;
+    for (int i = 0; i < kCoarseQB; ++i) any = any || (q0 + i < nq && only[q0 + i] != 0);
+    if (!any) return;
+  }
 
   for (int e = tid; e < kCoarseQB * dim; e += kThreads) {
     const int qq = e / dim;
@@ -218,10 +225,10 @@ __global__ __launch_bounds__(kThreads) void coarse_merge_kernel(
 template <int R>
 hipError_t launch_coarse_t(const float* queries, uint64_t nq, int dim, const float* centT, int ldc,
                            int nlist, int nsel, int32_t* out_lists, float* out_dists, int* err_flag,
-                           int parts, float* part_d, uint32_t* part_k, hipStream_t stream) {
+                           int parts, float* part_d, uint32_t* part_k, const int* only, hipStream_t stream) {
   const size_t lds = sizeof(float) * (size_t)kCoarseQB * dim;
   void (*fn)(const float*, uint64_t, int, const float*, int, int, int, int32_t*, float*, int*, int,
-             float*, uint32_t*) =
+             float*, uint32_t*, const int*) =
       dim / 8 == 16 ? coarse_select_kernel<R, 16>
                     : (dim / 8 == 12 ? coarse_select_kernel<R, 12> : coarse_select_kernel<R, 0>);
   if (lds > 64 * 1024) {
@@ -233,7 +240,7 @@ hipError_t launch_coarse_t(const float* queries, uint64_t nq, int dim, const flo
   const int part_len = (ldc / 256 + parts - 1) / parts * 256;
   hipLaunchKernelGGL(fn, dim3((unsigned)blocks, (unsigned)parts), dim3(kThreads), lds, stream,
                      queries, nq, dim, centT, ldc, nlist, nsel, out_lists, out_dists, err_flag,
-                     part_len, part_d, part_k);
+                     part_len, part_d, part_k, only);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || parts == 1) return e;
   hipLaunchKernelGGL(coarse_merge_kernel<R>, dim3((unsigned)((nq + 3) / 4)), dim3(kThreads), 0,
@@ -718,15 +725,15 @@ int coarse_parts(uint64_t nq, int nlist, int nsel) {
 hipError_t launch_coarse_select(const float* queries, uint64_t nq, int dim, const float* centT,
                                 int nlist, int nsel, int32_t* out_lists, float* out_dists,
                                 int* err_flag, hipStream_t stream, float* part_d,
-                                uint32_t* part_k, uint64_t part_cap) {
+                                uint32_t* part_k, uint64_t part_cap, const int* only) {
   if (nq == 0) return hipSuccess;
   if (nsel <= 0 || nsel > 1024 || nlist <= 0 || dim <= 0 || dim > 2048) return hipErrorInvalidValue;
-  int parts = (part_d && part_k) ? coarse_parts(nq, nlist, nsel) : 1;
+  int parts = (part_d && part_k && !only) ? coarse_parts(nq, nlist, nsel) : 1;
   if (parts > 1 && nq * (uint64_t)parts * nsel > part_cap) return hipErrorInvalidValue;
   const int ld = centT_ld(nlist);
 #define FDB_CS(R)                                                                                  \
   return launch_coarse_t<R>(queries, nq, dim, centT, ld, nlist, nsel, out_lists, out_dists, err_flag, \
-                            parts, part_d, part_k, stream);
+                            parts, part_d, part_k, only, stream);
   switch (topk_regs(nsel)) {
     case 1: FDB_CS(1)
     case 2: FDB_CS(2)

@@ -16,11 +16,14 @@ namespace fdb {
 // With a workspace part_d / part_k of part_cap entries (>= nq *
 // coarse_parts(nq, nlist, nsel) * nsel), a batch too small to fill the GPU
 // splits the centroids into coarse_parts(...) parts, each selecting its own
-// list, and a second kernel merges them; the result is the same.
+// list, and a second kernel merges them; the result is the same.  With
+// only (nullable, [nq]), just the workgroups holding a query whose flag is
+// set run (one part).
 hipError_t launch_coarse_select(const float* queries, uint64_t nq, int dim, const float* centT,
                                 int nlist, int nsel, int32_t* out_lists, float* out_dists,
                                 int* err_flag, hipStream_t stream, float* part_d = nullptr,
-                                uint32_t* part_k = nullptr, uint64_t part_cap = 0);
+                                uint32_t* part_k = nullptr, uint64_t part_cap = 0,
+                                const int* only = nullptr);
 // Number of centroid parts launch_coarse_select uses for this batch (1 = none).
 int coarse_parts(uint64_t nq, int nlist, int nsel);
 

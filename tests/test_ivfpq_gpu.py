@@ -80,6 +80,39 @@ def test_probe_parity_centroid_parts(nlist, dim, nq):
             assert np.array_equal(lists[q], ol), (nprobe, q)
 
 
+@pytest.mark.parametrize("nlist,dim,nq,nprobes", [(2048, 37, 100, (17, 32, 33, 64)), (1024, 128, 65, (2, 16)),
+                                                  (4096, 96, 300, (64,)), (512, 12, 50, (8, 16)),
+                                                  (640, 20, 97, (1, 20))])
+def test_probe_parity_screened_shapes(nlist, dim, nq, nprobes):
+    """Coarse selection at list counts the matrix-core screening serves
+    (nprobe <= 64 and at most one probe per 32 lists): dimensions off the
+    8- and 4-float grids, a last tile of fewer than 32 queries, twins, and
+    rows the screening hands to the exact kernel (values past fp16's reach
+    once scaled, and zero)."""
+    print(f"screened probe parity: nlist {nlist}, dim {dim}, {nq} queries, nprobe {nprobes}", flush=True)
+    rng = np.random.default_rng(nlist * 7 + dim)
+    M = 1
+    cen = (rng.standard_normal((nlist, dim)) * 3.0).astype(np.float32)
+    cen[nlist // 2:nlist // 2 + 16] = cen[:16]  # twins
+    cb = rng.standard_normal((M, 256, dim)).astype(np.float32)
+    offsets = np.arange(nlist + 1, dtype=np.uint64)
+    ids = np.arange(nlist, dtype=np.uint64)
+    codes = rng.integers(0, 256, (nlist, M), dtype=np.uint8)
+    gx = gpu_index(dict(centroids=cen, codebooks=cb, list_offsets=offsets, ids=ids, codes=codes))
+    ox = refcpu.IvfPq.create(cen, cb, offsets, ids, codes)
+    queries = (cen[rng.integers(0, nlist, nq)] + 0.5 * rng.standard_normal((nq, dim))).astype(np.float32)
+    queries[3] = cen[5]                # on a twin
+    queries[4] *= np.float32(1e19)     # |q|^2 past fp32
+    queries[5] *= np.float32(1e-33)    # scale exponent out of range
+    queries[6] = 0.0
+    for nprobe in nprobes:
+        lists, d = gx.probe(queries, nprobe)
+        for q in range(nq):
+            ol, od = ox.probes(queries[q], nprobe)
+            assert np.array_equal(d[q], od), (nprobe, q)
+            assert np.array_equal(lists[q], ol), (nprobe, q)
+
+
 @pytest.mark.parametrize("nprobe,k", [(1, 10), (8, 10), (16, 1), (16, 64), (16, 65), (16, 100),
                                       (64, 10), (5, 256), (3, 1000)])
 def test_batch_search_parity(small_ivfpq, nprobe, k):
