@@ -302,6 +302,18 @@ fdb_status fdb_ivfpq_batch_search_device_timed(fdb_ivfpq* h, const float* d_quer
   });
 }
 
+fdb_status fdb_ivfpq_batch_search_device_noalloc(fdb_ivfpq* h, const float* d_queries, uint64_t nq,
+                                                 uint32_t k, uint64_t* d_out_ids, float* d_out_dists,
+                                                 uint32_t* d_out_counts, void* stream) {
+  return guarded([&] {
+    IvfPqIndex* ix = H(h);
+    uint64_t cap = 0;
+    int32_t* probes = noalloc_scratch(cap);
+    ix->batch_search_device_noalloc(d_queries, nq, k, d_out_ids, d_out_dists, d_out_counts, (hipStream_t)stream,
+                                    probes, cap);
+  });
+}
+
 fdb_status fdb_ivfpq_sync(fdb_ivfpq* h, void* stream) {
   return guarded([&] {
     if (H(h)->sync((hipStream_t)stream)) throw Error(FDB_ERR_NAN, "NaN centroid distance (a query contains NaN)");

@@ -1061,6 +1061,13 @@ void CoarseQuantizer::select(const float* d_qs, uint64_t nq, uint32_t np, int32_
                                part_d_.p, part_k_.p, cap));
 }
 
+void CoarseQuantizer::select_one_part(const float* d_qs, uint64_t nq, uint32_t np, int32_t* probes, int* err,
+                                      hipStream_t s) const {
+  if (nq == 0 || np == 0) return;
+  FDB_HIP(launch_coarse_select(d_qs, nq, (int)dim_, centT_, (int)nlist_, (int)np, probes, nullptr, err, s, nullptr,
+                               nullptr, 0));
+}
+
 // Automatic mode screens when there are at least 2^26 (query, row) pairs;
 // below that the launch sequence costs more than the exact scan.
 bool BruteForceIndex::screen_applies(uint64_t nq, uint32_t k) const {

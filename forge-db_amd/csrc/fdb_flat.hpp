@@ -242,6 +242,10 @@ class CoarseQuantizer {
   // distance ORs 1 into *err
   void select(const float* d_qs, uint64_t nq, uint32_t np, int32_t* probes, float* dists, int* err,
               hipStream_t s);
+  // The exact kernel in one part (the same probes): uses no device memory
+  // beyond probes and err.
+  void select_one_part(const float* d_qs, uint64_t nq, uint32_t np, int32_t* probes, int* err,
+                       hipStream_t s) const;
 
  private:
   const float* cent_ = nullptr;

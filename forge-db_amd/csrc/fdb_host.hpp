@@ -72,6 +72,11 @@ struct StreamOrder {
   ~StreamOrder() {
     if (ev) (void)hipEventDestroy(ev);
   }
+  // creates the event (a handle's constructor calls this, so that calls
+  // need not)
+  void init() {
+    if (!ev) FDB_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  }
   void begin(hipStream_t s) {
     if (pending && last != s) FDB_HIP(hipStreamWaitEvent(s, ev, 0));
   }

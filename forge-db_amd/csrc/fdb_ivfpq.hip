@@ -87,6 +87,13 @@ __global__ __launch_bounds__(64) void rerank_kernel(const float* __restrict__ qu
   if (lane == 0) out_counts[q] = count;
 }
 
+// Device scratch of fdb_ivfpq_batch_search_device_noalloc: the probe lists,
+// one copy per device, held until the process ends.  Host code uses the
+// address hipGetSymbolAddress returns for the current device
+// (noalloc_scratch), never the array's name.
+constexpr uint64_t kNoAllocProbes = 1ull << 21;  // int32 entries (8 MiB)
+__device__ __align__(256) int32_t scratch[kNoAllocProbes];
+
 int regs_for(uint32_t k) {
   int r = (int)((k + 63) / 64), p = 1;
   while (p < r) p <<= 1;
@@ -140,6 +147,24 @@ hipError_t launch_truncate(const uint64_t* cid, const float* cd, const uint32_t*
 }
 
 }  // namespace
+
+// The current device's copy of the no-allocation scratch: its address is
+// looked up once per device (with that device current) and kept.
+int32_t* noalloc_scratch(uint64_t& cap) {
+  static std::mutex mu;
+  static int32_t* addr[64] = {};
+  int dev = 0;
+  FDB_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) throw Error(FDB_ERR_UNSUPPORTED, "device ordinal above 63");
+  std::lock_guard<std::mutex> g(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    FDB_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    addr[dev] = static_cast<int32_t*>(p);
+  }
+  cap = kNoAllocProbes;
+  return addr[dev];
+}
 
 // Members of each cluster in ascending point order (a stable counting sort).
 void group_members(const std::vector<int32_t>& assign, int k, std::vector<uint32_t>& off,
@@ -238,6 +263,7 @@ IvfPqIndex::IvfPqIndex(IvfPqArtifacts&& art) : host_(std::move(art)) {
   // from_serializable keeps the stored value (ivf_pq.rs:1937); every search
   // clamps it to nlist
   nprobe_.store(host_.nprobe, std::memory_order_relaxed);
+  order_.init();
   if (host_.has_originals && host_.orig_ok.size() != host_.ids.size()) host_.orig_ok.assign(host_.ids.size(), 1);
   FDB_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
   for (auto& e : ev_) FDB_HIP(hipEventCreate(&e));
@@ -750,6 +776,66 @@ void IvfPqIndex::batch_search_device(const float* d_qs, uint64_t nq, uint32_t k,
   const uint32_t np = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(nprobe(), host_.nlist));
   run(d_qs, nq, k, np, kAdcLanes8, d_ids, d_dists, d_counts, s ? s : stream_, coarse_ms, scan_ms,
       live_bitmap());
+}
+
+void IvfPqIndex::batch_search_device_noalloc(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids,
+                                             float* d_dists, uint32_t* d_counts, hipStream_t s, int32_t* probes,
+                                             uint64_t cap) {
+  std::lock_guard<std::mutex> g(mu_);
+  const hipStream_t st = s ? s : stream_;
+  OrderedOn on(order_, st);
+  if (host_.has_originals)
+    throw Error(FDB_ERR_UNSUPPORTED, "the no-allocation batch search serves indexes without reranking");
+  if (n_tomb_ != 0)
+    throw Error(FDB_ERR_UNSUPPORTED, "the no-allocation batch search serves indexes without tombstones");
+  // batch_search probes [..=nth]: at least one list (ivf_pq.rs:877-881)
+  const uint32_t np = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(nprobe(), host_.nlist));
+  if (k > 1024) throw Error(FDB_ERR_UNSUPPORTED, "k above 1024");
+  if (np > 1024 && np < host_.nlist) throw Error(FDB_ERR_UNSUPPORTED, "nprobe above 1024");
+  if (nq * (uint64_t)np > cap)
+    throw Error(FDB_ERR_UNSUPPORTED,
+                "nq * nprobe above the no-allocation scratch (" + std::to_string(cap) + " probe entries)");
+  if (nq == 0) return;
+  if (k == 0) {
+    hipLaunchKernelGGL(fill_empty_kernel, dim3(blocks_for(nq, 256)), dim3(256), 0, st, nq, k, d_ids, d_dists,
+                       d_counts);
+    FDB_HIP(hipGetLastError());
+    return;
+  }
+  if (np >= host_.nlist) {
+    hipLaunchKernelGGL(iota_probes_kernel, dim3(blocks_for(nq * np, 256)), dim3(256), 0, st, nq, np, probes);
+    FDB_HIP(hipGetLastError());
+    hipLaunchKernelGGL(nan_check_kernel, dim3(blocks_for(nq * host_.dim, 256)), dim3(256), 0, st, d_qs,
+                       nq * host_.dim, err_.p);
+    FDB_HIP(hipGetLastError());
+  } else {
+    coarse_.select_one_part(d_qs, nq, np, probes, err_.p, st);
+  }
+  IvfPqScanArgs a{};
+  a.queries = d_qs;
+  a.nq = nq;
+  a.dim = (int)host_.dim;
+  a.M = (int)host_.M;
+  a.dsub = (int)host_.dsub;
+  a.probes = probes;
+  a.np = (int)np;
+  a.nlist = (int)host_.nlist;
+  a.centroids = centroids_.p;
+  a.codebooks = codebooks_.p;
+  a.list_off = off_.p;
+  a.codes = codes_.p;
+  a.ids = ids_.p;
+  a.k = (int)k;
+  a.order = kAdcLanes8;
+  a.lut_mode = lut_mode();
+  a.cbnorm = cbnorm_.p;
+  a.live = nullptr;
+  a.out_ids = d_ids;
+  a.out_dists = d_dists;
+  a.out_pos = nullptr;
+  a.out_counts = d_counts;
+  FDB_HIP(launch_ivfpq_scan(a, st));
+  path_ = 0;
 }
 
 bool IvfPqIndex::sync(hipStream_t s) {

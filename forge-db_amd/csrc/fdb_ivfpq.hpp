@@ -77,6 +77,11 @@ class IvfPqIndex {
                            float* coarse_ms = nullptr, float* scan_ms = nullptr);
   // returns true when a NaN was seen since the last call
   bool sync(hipStream_t stream);
+  // batch_search_device without device allocation: the table scan, with
+  // the [nq][nprobe] probe lists in `probes` (cap entries; the caller's
+  // static scratch).  Plain indexes only (no reranking, no tombstones).
+  void batch_search_device_noalloc(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_ids, float* d_dists,
+                                   uint32_t* d_counts, hipStream_t stream, int32_t* probes, uint64_t cap);
   void probe(const float* qs, uint64_t nq, uint32_t nprobe, int32_t* lists, float* dists);
   void encode(const float* residuals, uint64_t nq, uint8_t* codes);
 
@@ -163,6 +168,9 @@ class IvfPqIndex {
   int path_ = 0;
   float screen_kernel_ms_ = 0.0f;
 };
+
+// The current device's no-allocation scratch (probe lists; cap entries).
+int32_t* noalloc_scratch(uint64_t& cap);
 
 // Seeded k-means over n host rows [n][dim] (KMeans::fit_raw, kmeans.rs:87-193):
 // k centroids [k][dim] after at most max_iters Lloyd steps on the GPU.

@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "fdb_ivfpq_destroy", "fdb_ivfpq_set_nprobe", "fdb_ivfpq_nprobe",
     "fdb_ivfpq_describe", "fdb_ivfpq_export", "fdb_ivfpq_enable_reranking",
     "fdb_ivfpq_search", "fdb_ivfpq_batch_search", "fdb_ivfpq_batch_search_device",
+    "fdb_ivfpq_batch_search_device_noalloc",
     "fdb_ivfpq_sync", "fdb_ivfpq_probe", "fdb_ivfpq_encode",
     "fdb_ivfpq_batch_search_device_timed", "fdb_ivfpq_set_lut_mode", "fdb_ivfpq_lut_mode",
     "fdb_ivfpq_search_filtered", "fdb_ivfpq_delete", "fdb_ivfpq_insert", "fdb_ivfpq_compact",
@@ -127,6 +128,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fdb_ivfpq_search": [_P, _P, C.c_uint32, C.c_uint32, _P, _P, _P],
         "fdb_ivfpq_batch_search": [_P, _P, C.c_uint64, C.c_uint32, C.c_uint32, _P, _P, _P],
         "fdb_ivfpq_batch_search_device": [_P, _P, C.c_uint64, C.c_uint32, _P, _P, _P, _P],
+        "fdb_ivfpq_batch_search_device_noalloc": [_P, _P, C.c_uint64, C.c_uint32, _P, _P, _P, _P],
         "fdb_ivfpq_batch_search_device_timed": [_P, _P, C.c_uint64, C.c_uint32, _P, _P, _P, _P,
                                                 _P, _P],
         "fdb_ivfpq_sync": [_P, _P],
@@ -456,6 +458,14 @@ class IVFPQIndex:
             self._h, C.c_void_p(d_queries), nq, k, C.c_void_p(d_ids), C.c_void_p(d_dists),
             C.c_void_p(d_counts), C.c_void_p(stream)))
         return None
+
+    def batch_search_device_noalloc(self, d_queries: int, nq: int, k: int, d_ids: int, d_dists: int,
+                                    d_counts: int, stream: int = 0) -> None:
+        """batch_search_device without device allocation (its probe lists in
+        a static device array; plain indexes, nq * nprobe <= 2^21)."""
+        _check(self._lib, self._lib.fdb_ivfpq_batch_search_device_noalloc(
+            self._h, C.c_void_p(d_queries), nq, k, C.c_void_p(d_ids), C.c_void_p(d_dists),
+            C.c_void_p(d_counts), C.c_void_p(stream)))
 
     def sync(self, stream: int = 0) -> None:
         _check(self._lib, self._lib.fdb_ivfpq_sync(self._h, C.c_void_p(stream)))

@@ -200,6 +200,20 @@ FDB_API fdb_status fdb_ivfpq_batch_search_device(fdb_ivfpq* index, const float* 
                                                  uint64_t nq, uint32_t k, uint64_t* d_out_ids,
                                                  float* d_out_dists, uint32_t* d_out_counts,
                                                  void* hip_stream);
+/* No counterpart in the reference: fdb_ivfpq_batch_search_device for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  It allocates nothing:
+ * the [nq][nprobe] probe lists go to a static device array of 2^21 int32
+ * entries (8 MiB per device, held until the process ends), and the table
+ * scan writes straight to the caller's outputs; the results equal
+ * fdb_ivfpq_batch_search_device's.  FDB_ERR_UNSUPPORTED when nq * nprobe
+ * exceeds 2^21, or the index has reranking on or tombstones.  Every call on
+ * one device shares that array: calls that overlap on one device (other
+ * handles or other streams included) race. */
+FDB_API fdb_status fdb_ivfpq_batch_search_device_noalloc(fdb_ivfpq* index, const float* d_queries,
+                                                         uint64_t nq, uint32_t k, uint64_t* d_out_ids,
+                                                         float* d_out_dists, uint32_t* d_out_counts,
+                                                         void* hip_stream);
 /* Waits for the handle's work on `hip_stream` (NULL = own stream) and
  * returns FDB_ERR_NAN if a device search since the last sync saw a NaN. */
 FDB_API fdb_status fdb_ivfpq_sync(fdb_ivfpq* index, void* hip_stream);
