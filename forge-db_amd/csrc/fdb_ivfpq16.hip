@@ -37,6 +37,14 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));  // 8 halves as a nati
 constexpr int kT = 256;
 // (query, probe) pairs per screening tile: 32 per wave, 4 waves
 constexpr int kTilePairs = 128;
+// Stage B: groups of 32 pairs per wave (tiles of 128 per group), and the
+// waves per SIMD its registers are sized for.  Two groups where they fit
+// three waves per SIMD (measured at 10M x 96, KC 6: 1.80 ms against 1.92
+// with one group at four waves); at 1M x 128 (KC 8) two groups need the
+// registers of two waves per SIMD and take 0.24 ms against 0.185 with one
+// group at four.
+constexpr int stage_b_groups(int KC) { return KC <= 6 ? 2 : 1; }
+constexpr int stage_b_waves(int KC) { return KC <= 6 ? 3 : (KC <= 8 ? 4 : (KC <= 12 ? 3 : 2)); }
 
 uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
@@ -437,7 +445,9 @@ __device__ __forceinline__ float add_up(float a, float b) {
 struct TileWork {
   uint32_t p, chunk, q0, qend;
   int split, phase;
-  bool busy;  // wave-uniform: the wave has pairs
+  bool busy;   // wave-uniform: the wave has pairs
+  uint32_t q1;  // a second group of 32 pairs (tiles of 256 pairs)
+  bool busy1;  // wave-uniform: the wave has the second group
 };
 
 __device__ __forceinline__ uint32_t tile_slot() {
@@ -445,8 +455,11 @@ __device__ __forceinline__ uint32_t tile_slot() {
   return ((y / kXcdRun) * kXcd + xcd) * kXcdRun + y % kXcdRun;
 }
 
+// TQ pairs per tile: 128, or 256 (then with five to eight groups of 32,
+// wave w also takes group w + 4).
+template <uint32_t TQ>
 __device__ __forceinline__ TileWork tile_work(const ScreenArgs& a, uint32_t t, int wave) {
-  constexpr uint32_t TQ = kTilePairs;
+  static_assert(TQ == 128 || TQ == 256, "tiles of 128 or 256 pairs");
   TileWork w;
   w.p = a.tl[t];
   const uint32_t qb = a.qoff[w.p];
@@ -455,11 +468,14 @@ __device__ __forceinline__ TileWork tile_work(const ScreenArgs& a, uint32_t t, i
   const uint32_t local = t - a.toff[w.p];
   w.chunk = local / nqt;
   const uint32_t tq0 = qb + (local - w.chunk * nqt) * TQ;
-  const uint32_t ng = min((w.qend - tq0 + 31) / 32, 4u);
+  const uint32_t ngr = min((w.qend - tq0 + 31) / 32, TQ / 32);
+  const uint32_t ng = min(ngr, 4u);
   w.split = 4 / (ng == 1 ? 1 : (ng == 2 ? 2 : 4));
   w.phase = wave % w.split;
   w.q0 = tq0 + (uint32_t)(wave / w.split) * 32;
   w.busy = w.q0 < w.qend;
+  w.q1 = tq0 + (uint32_t)(wave + 4) * 32;
+  w.busy1 = ngr > 4 && w.q1 < w.qend;  // split is 1 then
   return w;
 }
 
@@ -622,7 +638,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
   const int half = lane >> 5;
   const uint32_t ntiles = a.toff[a.nlist];
   for (uint32_t t = tile_slot(); t < ntiles; t += gridDim.x) {
-    const TileWork w = tile_work(a, t, wave);
+    const TileWork w = tile_work<kTilePairs>(a, t, wave);
     const uint32_t p = w.p;
     const bool qv = w.busy && w.q0 + (uint32_t)col < w.qend;
     // lanes past the tile's pairs repeat its last pair, so that every load
@@ -698,59 +714,84 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
 //   with one atomic, and the entries are written out.
 // NS: stages of the ring; W: waves per SIMD the registers are sized for
 // (measured at 1M x 128 codes, nprobe 16: NS 3 at 4 waves per SIMD 0.179 ms;
-// NS 4 at 3 waves 0.186 ms; NS 6 and 8 at 2 waves 0.248 ms).
-template <int KC, int NS, int W>
+// NS 4 at 3 waves 0.186 ms; NS 6 and 8 at 2 waves 0.248 ms).  PG: groups
+// of 32 pairs per wave (tiles of 128 PG pairs): with PG 2 a list chunk of up
+// to 256 pairs is streamed through the ring once, each block multiplied
+// against both groups' operands.
+template <int KC, int NS, int W, int PG>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W))) void pq16_thresh_kernel(ScreenArgs a) {
+  static_assert(PG == 1 || PG == 2, "one or two groups of pairs per wave");
   constexpr uint32_t kQ = 256;  // queue entries per wave
   __shared__ Ring<KC, NS> ring;
   __shared__ uint32_t wq[4][kQ];
-  __shared__ uint32_t wbase[4][64];  // each lane's next position while flushing
+  __shared__ uint32_t wbase[4][PG][64];  // each (group, lane)'s next position while flushing
   const int lane = threadIdx.x & 63;
   const int wave = wave_index();
   const int col = lane & 31;
   const int half = lane >> 5;
   const uint32_t ntiles = a.toff[a.nlist];
   for (uint32_t t = tile_slot(); t < ntiles; t += gridDim.x) {
-    const TileWork w = tile_work(a, t, wave);
+    const TileWork w = tile_work<kTilePairs * PG>(a, t, wave);
     const uint32_t p = w.p;
-    const bool qv = w.busy && w.q0 + (uint32_t)col < w.qend;
-    const uint2 e = a.qlist[min(w.q0 + (uint32_t)col, w.qend - 1)];
-    const uint32_t q = e.x, j = e.y;
-    PairOperand<KC> op;
-    pair_operand<KC>(a, q, p, half, op);
-    if (qv && op.bad && half == 0) atomicOr(&a.force[q], 1);
-    float Tp = -f_inf();  // no append
-    if (qv && !op.bad) {
-      const float rnorm = sqrtf(op.rn) * (1.0f + 0x1p-16f);
-      const float X = sqrtf(__uint_as_float(a.xmax2[p])) * (1.0f + 0x1p-16f);
-      const float f = add_up(a.dkA[q], pq16_eps(rnorm, X, a)) - op.rn;
-      Tp = f + __builtin_fabsf(f) * 0x1p-22f;
+    const float X = sqrtf(__uint_as_float(a.xmax2[p])) * (1.0f + 0x1p-16f);
+    uint32_t q[PG], j[PG];
+    PairOperand<KC> op[PG];
+    float Tp[PG], cneg[PG];
+#pragma unroll
+    for (int g = 0; g < PG; ++g) {
+      const uint32_t qg = g == 0 ? w.q0 : w.q1;
+      const bool gbusy = g == 0 ? w.busy : w.busy1;
+      const bool qv = gbusy && qg + (uint32_t)col < w.qend;
+      const uint2 e = a.qlist[min(qg + (uint32_t)col, w.qend - 1)];
+      q[g] = e.x;
+      j[g] = e.y;
+      Tp[g] = -f_inf();  // no append
+      cneg[g] = 0.0f;
+      if (g > 0 && !gbusy) continue;  // wave-uniform
+      pair_operand<KC>(a, q[g], p, half, op[g]);
+      if (qv && op[g].bad && half == 0) atomicOr(&a.force[q[g]], 1);
+      if (qv && !op[g].bad) {
+        const float rnorm = sqrtf(op[g].rn) * (1.0f + 0x1p-16f);
+        const float f = add_up(a.dkA[q[g]], pq16_eps(rnorm, X, a)) - op[g].rn;
+        Tp[g] = f + __builtin_fabsf(f) * 0x1p-22f;
+      }
+      cneg[g] = -ldexpf(1.0f, 1 - op[g].er - a.xexp);
     }
-    const float cneg = -ldexpf(1.0f, 1 - op.er - a.xexp);
     const uint32_t b0 = a.bo[p];
     const uint32_t nb = min(a.bo[p + 1] - b0, a.blim);
     const uint32_t bb = w.chunk * kCB;
     const uint32_t start = a.list_off[p];
     const uint32_t len = a.list_off[p + 1] - start;
     uint32_t* __restrict__ myq = wq[wave];
-    uint32_t qn = 0;   // wave-uniform queue length
-    uint32_t cnt = 0;  // this lane's entries in the queue
-    // Queue to candidate list: one atomic per lane with entries reserves its
-    // range; then 64 entries at a time, each lane takes one, gets its slot
-    // from the owner's running position (an LDS atomic) and writes (list
-    // position of the row base, probe index << 16 | mask).  All lanes call
-    // this (the shuffles take every lane).
+    uint32_t qn = 0;       // wave-uniform queue length
+    uint32_t cnt[PG];      // this lane's entries in the queue, per group
+#pragma unroll
+    for (int g = 0; g < PG; ++g) cnt[g] = 0;
+    // Queue to candidate list: one atomic per (lane, group) with entries
+    // reserves its range; then 64 entries at a time, each lane takes one,
+    // gets its slot from the owner's running position (an LDS atomic) and
+    // writes (list position of the row base, probe index << 16 | mask).  All
+    // lanes call this (the shuffles take every lane).
     auto flush = [&]() {
-      wbase[wave][lane] = cnt ? atomicAdd(&a.ccnt[q], cnt) : 0u;
-      cnt = 0;
+#pragma unroll
+      for (int g = 0; g < PG; ++g) {
+        wbase[wave][g][lane] = cnt[g] ? atomicAdd(&a.ccnt[q[g]], cnt[g]) : 0u;
+        cnt[g] = 0;
+      }
       __builtin_amdgcn_wave_barrier();
       for (uint32_t i0 = 0; i0 < qn; i0 += 64) {
         const uint32_t i = i0 + (uint32_t)lane;
         const uint32_t ent = i < qn ? myq[i] : 0u;
         const int owner = (int)((ent >> 22) & 63);
-        const uint32_t oq = (uint32_t)__shfl((int)q, owner), oj = (uint32_t)__shfl((int)j, owner);
+        const int g = PG > 1 ? (int)((ent >> 28) & 1) : 0;
+        uint32_t oq = (uint32_t)__shfl((int)q[0], owner), oj = (uint32_t)__shfl((int)j[0], owner);
+        if constexpr (PG > 1) {
+          const uint32_t oq1 = (uint32_t)__shfl((int)q[PG - 1], owner), oj1 = (uint32_t)__shfl((int)j[PG - 1], owner);
+          oq = g ? oq1 : oq;
+          oj = g ? oj1 : oj;
+        }
         if (i < qn) {
-          const uint32_t pos = atomicAdd(&wbase[wave][owner], 1u);
+          const uint32_t pos = atomicAdd(&wbase[wave][g][owner], 1u);
           if (pos < a.cap) {
             const uint32_t rowb = (bb + ((ent >> 16) & 63)) * 32 + 4 * (uint32_t)(owner >> 5);
             a.cand[(uint64_t)oq * a.cap + pos] = make_uint2(start + rowb, (oj << 16) | (ent & 0xFFFFu));
@@ -763,55 +804,59 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W))) void p
     const v4u* __restrict__ A = reinterpret_cast<const v4u*>(a.data) + (uint64_t)b0 * KC * 64;
     stream_blocks<KC, NS>(ring, A, a.xnb + (uint64_t)b0 * 32, bb, min(nb, bb + kCB), wave, lane, w,
                           [&](const v4u* __restrict__ sa, const float* __restrict__ sx, uint32_t b) {
-      v16f acc = {};
-#pragma unroll
-      for (int kc = 0; kc < KC; ++kc)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, sa[kc * 64 + lane]), op.bq[kc], acc, 0,
-                                                     0, 0);
       float xs[16];
       block_norms(sx, half, xs);
-      float s[16];
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) s[rr] = __builtin_fmaf(cneg, acc[rr], xs[rr]);
-      const float m0 = fminf(fminf(s[0], s[1]), s[2]);
-      const float m1 = fminf(fminf(s[3], s[4]), s[5]);
-      const float m2 = fminf(fminf(s[6], s[7]), s[8]);
-      const float m3 = fminf(fminf(s[9], s[10]), s[11]);
-      const float m4 = fminf(fminf(s[12], s[13]), s[14]);
-      const bool pass = fminf(fminf(fminf(m0, m1), fminf(m2, m3)), fminf(m4, s[15])) <= Tp;
-      if (__ballot(pass) == 0) return;
       const uint32_t rowb = b * 32 + 4 * half;
-      uint32_t passm = 0;
-      if (pass) {
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr) passm |= (s[rr] <= Tp ? 1u : 0u) << rr;
-        // rows past the list's end pass only a threshold of +inf
-        if (rowb + 28 > len)
+      for (int g = 0; g < PG; ++g) {
+        if (g > 0 && !w.busy1) break;  // wave-uniform
+        v16f acc = {};
 #pragma unroll
-          for (int rr = 0; rr < 16; ++rr)
-            if (rowb + 8 * (rr >> 2) + (rr & 3) >= len) passm &= ~(1u << rr);
+        for (int kc = 0; kc < KC; ++kc)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, sa[kc * 64 + lane]), op[g].bq[kc],
+                                                       acc, 0, 0, 0);
+        float s[16];
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) s[rr] = __builtin_fmaf(cneg[g], acc[rr], xs[rr]);
+        const float m0 = fminf(fminf(s[0], s[1]), s[2]);
+        const float m1 = fminf(fminf(s[3], s[4]), s[5]);
+        const float m2 = fminf(fminf(s[6], s[7]), s[8]);
+        const float m3 = fminf(fminf(s[9], s[10]), s[11]);
+        const float m4 = fminf(fminf(s[12], s[13]), s[14]);
+        const bool pass = fminf(fminf(fminf(m0, m1), fminf(m2, m3)), fminf(m4, s[15])) <= Tp[g];
+        if (__ballot(pass) == 0) continue;
+        uint32_t passm = 0;
+        if (pass) {
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr) passm |= (s[rr] <= Tp[g] ? 1u : 0u) << rr;
+          // rows past the list's end pass only a threshold of +inf
+          if (rowb + 28 > len)
+#pragma unroll
+            for (int rr = 0; rr < 16; ++rr)
+              if (rowb + 8 * (rr >> 2) + (rr & 3) >= len) passm &= ~(1u << rr);
+        }
+        // one entry per lane, group and block with a passing row: its
+        // 16-row mask (rows 8(i/4) + i%4 from the lane's row base)
+        const uint64_t bal = __ballot(passm != 0);
+        if (bal == 0) continue;
+        if (passm != 0) {
+          const uint32_t rank =
+              __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+          myq[qn + rank] = passm | ((b - bb) << 16) | ((uint32_t)lane << 22) | ((uint32_t)g << 28);
+          ++cnt[g];
+        }
+        qn += (uint32_t)__popcll(bal);
+        if (qn > kQ - 64) flush();
       }
-      // one entry per lane and block with a passing row: its 16-row mask
-      // (rows 8(i/4) + i%4 from the lane's row base)
-      const uint64_t bal = __ballot(passm != 0);
-      if (bal == 0) return;
-      if (passm != 0) {
-        const uint32_t rank =
-            __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-        myq[qn + rank] = passm | ((b - bb) << 16) | ((uint32_t)lane << 22);
-        ++cnt;
-      }
-      qn += (uint32_t)__popcll(bal);
-      if (qn > kQ - 64) flush();
     });
     if (qn > 0) flush();
   }
 }
 
-// Stage B's registers: the B operand takes 4 * KC of them
+// Stage B's kernel for KC k-chunks
 template <int KC>
 void (*thresh_kernel())(ScreenArgs) {
-  return pq16_thresh_kernel<KC, 3, (KC <= 8 ? 4 : (KC <= 12 ? 3 : 2))>;
+  return pq16_thresh_kernel<KC, 3, stage_b_waves(KC), stage_b_groups(KC)>;
 }
 
 // One wave per query: dkA = (k-th smallest kept screened value) + the
@@ -836,9 +881,12 @@ __global__ __launch_bounds__(64) void pq16_select_kernel(const float* __restrict
   WaveTopK<R> tk;
   tk.init(k);
   int qn = 0;
-  const float4* __restrict__ v = reinterpret_cast<const float4*>(bufA + q * capA);
+  // (a plain vector type: loop-carried HIP float4 values can end up in
+  // scratch memory)
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const f4* __restrict__ v = reinterpret_cast<const f4*>(bufA + q * capA);
   const uint32_t n4 = (n + 3) / 4;  // n is a multiple of 32 or capA
-  const float4 none = make_float4(f_inf(), f_inf(), f_inf(), f_inf());
+  const f4 none = {f_inf(), f_inf(), f_inf(), f_inf()};
   // k <= 64: each lane's smallest value goes in first; the k-th smallest of
   // those bounds the k-th overall, so that few of the others get past the
   // list's threshold (one merge instead of one per 64 early values).  Every
@@ -849,7 +897,7 @@ __global__ __launch_bounds__(64) void pq16_select_kernel(const float* __restrict
 #pragma unroll 1
     for (uint32_t i0 = 0; i0 < n4; i0 += 64) {
       const uint32_t il = i0 + (uint32_t)lane;
-      const float4 w = il < n4 ? v[il] : none;
+      const f4 w = il < n4 ? v[il] : none;
       const uint32_t i = 4 * il;
       if (w.x < mn) { mn = w.x; skip = i; }
       if (w.y < mn) { mn = w.y; skip = i + 1; }
@@ -859,11 +907,11 @@ __global__ __launch_bounds__(64) void pq16_select_kernel(const float* __restrict
     tk.offer_queued(mn, skip, mn < f_inf(), queue, qn);
     tk.flush(queue, qn);
   }
-  float4 w = (uint32_t)lane < n4 ? v[lane] : none;
+  f4 w = (uint32_t)lane < n4 ? v[lane] : none;
 #pragma unroll 1
   for (uint32_t i0 = 0; i0 < n4; i0 += 64) {
     const uint32_t inext = i0 + 64 + (uint32_t)lane;
-    const float4 wn = inext < n4 ? v[inext] : none;  // the next values in flight
+    const f4 wn = inext < n4 ? v[inext] : none;  // the next values in flight
     const uint32_t i = 4 * (i0 + (uint32_t)lane);
     tk.offer_queued(w.x, i, w.x < f_inf() && i != skip, queue, qn);
     tk.offer_queued(w.y, i + 1, w.y < f_inf() && i + 1 != skip, queue, qn);
@@ -1403,7 +1451,7 @@ __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q, 
 // Workgroups [0, nh) take the heavy list, one query at a time; the others
 // four queries of order each, the longer lists (front) dispatched first.
 template <int R, int DS, int MM>
-__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(4))) void pq16_rescore_kernel(RescoreArgs16 a,
+__global__ __launch_bounds__(kT) __attribute__((amdgpu_waves_per_eu(3))) void pq16_rescore_kernel(RescoreArgs16 a,
                                                                                                    uint64_t nq,
                                                                                                    uint32_t nh) {
   if (blockIdx.x < nh) {
@@ -1669,7 +1717,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   pst.blim0 = capA / 32;
   pst.blim1 = 0xFFFFFFFFu;
   pst.tq0 = kTilePairs;
-  pst.tq1 = kTilePairs;
+  pst.tq1 = kTilePairs * stage_b_groups(L.KC);
   pst.G = G;
   pst.H = H_.p;
   pst.qoff = qoff_.p;
