@@ -155,13 +155,15 @@ __device__ __forceinline__ void merge_low(const float (&a)[L], const float (&b)[
 // Workgroup of kW waves per tile of 32 queries.  Lane l of a wave serves
 // query l % 32 with the half-lane l / 32; wave w screens the blocks w, w +
 // kW, ...  M: block minima kept per (wave, half-lane), 2 kW M >= np.
-// LDS: the tile's queries (fp32, rows of 16 KC), then per query cap
-// candidate slots (centroid index, distance bits); before the candidate
-// pass the slots hold the kept minima, [32][16 M].
+// LDS: the tile's queries (fp32, rows of 16 KC, stride 16 KC + 4), then
+// per query cap candidate slots (centroid index, distance bits); before the
+// candidate pass the slots hold the kept minima, [32][2 kW M + 4].
 template <int KC, int M>
 __global__ __launch_bounds__(kCT) __attribute__((amdgpu_waves_per_eu(2))) void coarse16_kernel(C16Args a) {
-  constexpr int LDQ = 16 * KC;
+  constexpr int LDQ = 16 * KC;      // floats of a query row
+  constexpr int LQS = LDQ + 4;      // their LDS stride: 4 banks apart (no conflicts across rows)
   constexpr int U = 2 * kW * M;  // kept minima per query
+  constexpr int US = U + 4;      // their LDS stride (4 banks apart)
   static_assert(U % 64 == 0, "kept minima fill whole waves");
   extern __shared__ __align__(16) uint32_t lds[];
   __shared__ float s_qn[32], s_T[32];
@@ -169,7 +171,7 @@ __global__ __launch_bounds__(kCT) __attribute__((amdgpu_waves_per_eu(2))) void c
   __shared__ uint32_t s_cnt[32], s_pre[33];
   __shared__ uint8_t s_pair[32 * kMaxCap];  // query of each rescored pair
   float* __restrict__ qs = reinterpret_cast<float*>(lds);
-  uint2* __restrict__ cand = reinterpret_cast<uint2*>(lds + 32 * LDQ);
+  uint2* __restrict__ cand = reinterpret_cast<uint2*>(lds + 32 * LQS);
   float* __restrict__ mins = reinterpret_cast<float*>(cand);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -194,7 +196,11 @@ __global__ __launch_bounds__(kCT) __attribute__((amdgpu_waves_per_eu(2))) void c
       v[r] = (qi < nqt && d < a.dim) ? a.queries[(q0 + qi) * (uint64_t)a.dim + d] : 0.0f;
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r) qs[tid + r * kCT] = v[r];
+    for (int r = 0; r < R; ++r) {
+      const int e = tid + r * kCT;
+      const int qi = e / LDQ;
+      qs[qi * LQS + (e - qi * LDQ)] = v[r];
+    }
   }
   if (tid < 32) s_cnt[tid] = 0;
   __syncthreads();
@@ -207,7 +213,7 @@ __global__ __launch_bounds__(kCT) __attribute__((amdgpu_waves_per_eu(2))) void c
     int nan = 0;
 #pragma unroll
     for (int i = 0; i < LDQ / TPQ; ++i) {
-      const float v = qs[qi * LDQ + sub + i * TPQ];
+      const float v = qs[qi * LQS + sub + i * TPQ];
       nan |= v != v;
       mx = fmaxf(mx, __builtin_fabsf(v));
       qn = __builtin_fmaf(v, v, qn);
@@ -240,8 +246,8 @@ __global__ __launch_bounds__(kCT) __attribute__((amdgpu_waves_per_eu(2))) void c
   v8h bq[KC];
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc) {
-    const float4 x0 = *reinterpret_cast<const float4*>(qs + col * LDQ + kc * 16 + 8 * half);
-    const float4 x1 = *reinterpret_cast<const float4*>(qs + col * LDQ + kc * 16 + 8 * half + 4);
+    const float4 x0 = *reinterpret_cast<const float4*>(qs + col * LQS + kc * 16 + 8 * half);
+    const float4 x1 = *reinterpret_cast<const float4*>(qs + col * LQS + kc * 16 + 8 * half + 4);
     bq[kc][0] = (_Float16)(x0.x * sc);
     bq[kc][1] = (_Float16)(x0.y * sc);
     bq[kc][2] = (_Float16)(x0.z * sc);
@@ -336,7 +342,7 @@ __global__ __launch_bounds__(kCT) __attribute__((amdgpu_waves_per_eu(2))) void c
     if (__ballot(m < top[M - 1]) != 0) keep_smallest<M>(top, m);
   });
 #pragma unroll
-  for (int i = 0; i < M; ++i) mins[col * U + (wave * 2 + half) * M + i] = top[i];
+  for (int i = 0; i < M; ++i) mins[col * US + (wave * 2 + half) * M + i] = top[i];
   __syncthreads();
 
   // S = the np-th smallest kept minimum (they belong to distinct
@@ -346,7 +352,7 @@ __global__ __launch_bounds__(kCT) __attribute__((amdgpu_waves_per_eu(2))) void c
   // exchanged and merged once more (np <= 4M).
   static_assert(kW == 4, "eight kept lists per query: four per half-wave");
   if (wave == 0) {
-    const float* __restrict__ mq = mins + col * U + 4 * half * M;
+    const float* __restrict__ mq = mins + col * US + 4 * half * M;
     float l0[M], l1[M], l2[M], l3[M];
 #pragma unroll
     for (int i = 0; i < M; i += 4) {
@@ -444,7 +450,7 @@ __global__ __launch_bounds__(kCT) __attribute__((amdgpu_waves_per_eu(2))) void c
     const int qi = s_pair[i];
     const uint32_t slot = i - s_pre[qi];
     const float* __restrict__ cr = a.centroids + (uint64_t)cand[qi * cap + slot].x * a.dim;
-    const float* __restrict__ qr = qs + qi * LDQ;
+    const float* __restrict__ qr = qs + qi * LQS;
     float l0 = 0.0f, l1 = 0.0f, l2 = 0.0f, l3 = 0.0f;
     // the row's chunks loaded 16 at a time (d8 <= 2 KC), then the lanes
     constexpr int G = 2 * KC < 16 ? 2 * KC : 16;
@@ -594,8 +600,10 @@ void Coarse16::select(const float* d_qs, uint64_t nq, uint32_t np, const float* 
   a.probes = probes;
   a.dists = dists;
   a.flags = flags;
-  const size_t lds = (size_t)32 * 16 * KC_ * 4 + (size_t)32 * a.cap * 8;
+  const size_t lds = (size_t)32 * (16 * KC_ + 4) * 4 + (size_t)32 * a.cap * 8;
   const bool m16 = np > 32;  // 8 M >= np kept minima per query
+  // the kept minima ([32][8 M + 4] floats) are held in the candidate slots
+  if ((8 * (m16 ? 16 : 8) + 4) * 4 > a.cap * 8) throw Error(FDB_ERR_HIP, "coarse screening: minima exceed the slots");
   void (*fn)(C16Args) = nullptr;
 #define FDB_C16(K)                                          \
   case K:                                                   \
