@@ -191,9 +191,11 @@ def cpu_leg(run, nq, args, gpu_ids, k, threads, how):
 
 
 def thresh_kernel_name(dim):
-    """The threshold screening kernel (stage B) an IVF-PQ shape runs."""
+    """The threshold screening kernel (stage B) an IVF-PQ shape runs:
+    <k-chunks, ring stages, waves per SIMD, groups of 32 pairs per wave>."""
     kc = (dim + 15) // 16
-    return f"pq16_thresh_kernel<{kc}, 3, {4 if kc <= 8 else (3 if kc <= 12 else 2)}>"
+    waves = 3 if kc <= 6 else (4 if kc <= 8 else (3 if kc <= 12 else 2))
+    return f"pq16_thresh_kernel<{kc}, 3, {waves}, {2 if kc <= 6 else 1}>"
 
 
 def latency_leg(index, oracle, queries, k, reps):
