@@ -190,6 +190,11 @@ def cpu_leg(run, nq, args, gpu_ids, k, threads, how):
             "cpu_model": cpu_model(), "gpu_id_agreement": round(agree, 6)}
 
 
+def w_name(w):
+    """The WORKLOADS key of a workload."""
+    return next(name for name, v in WORKLOADS.items() if v is w)
+
+
 def thresh_kernel_name(dim):
     """The threshold screening kernel (stage B) an IVF-PQ shape runs:
     <k-chunks, ring stages, waves per SIMD, groups of 32 pairs per wave>."""
@@ -433,7 +438,10 @@ def bench_ivf(args, w, base, queries):
 
     ms_per_step = r.timed_loop(step, lambda: index.sync(r.sptr))
     log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step, {nq / ms_per_step * 1e3:,.0f} QPS")
-    times = [index.batch_search_device(*r.ptrs(), timed=True) for _ in range(args.timing_reps)]
+    times, screen_ms = [], []
+    for _ in range(args.timing_reps):
+        times.append(index.batch_search_device(*r.ptrs(), timed=True))
+        screen_ms.append(index.last_screen_kernel_ms())
     coarse_ms = float(np.mean([c for c, _ in times]))
     scan_ms = float(np.mean([s for _, s in times]))
     path = index.last_search_path()
@@ -443,7 +451,26 @@ def bench_ivf(args, w, base, queries):
     scanned = int(sizes[lists].sum())
     dim = base.shape[1]
     fp32_bytes = scanned * dim * 4
-    if path == 2:
+    if path == 3:
+        # list screening on the matrix cores: stage B's products, 2 x D16
+        # flops per (query, probed row), against the fp16 matrix peak
+        kernel_ms = float(np.mean(screen_ms))
+        kc = (dim + 15) // 16
+        flops = 2 * 16 * kc * scanned
+        tflops = flops / (kernel_ms / 1e3) / 1e12
+        tag = {"ivf_1m_l2": "1Mx96_l2"}.get(w_name(w))
+        traffic = read_traffic(f"ivf_lists_{tag}_traffic.txt") if tag else None
+        log(f"[bench] coarse {coarse_ms:.3f} ms, scan {scan_ms:.3f} ms; {scanned / nq:,.0f} rows per query; "
+            f"path 3 (list screening; {fallbacks} of {nq} queries rescanned exactly); threshold kernel "
+            f"{kernel_ms:.3f} ms: {flops / 1e9:.1f} GFLOP -> {tflops:,.1f} TFLOP/s"
+            + (f"; {traffic / 1e9:.2f} GB past L2 from the committed counters" if traffic else ""))
+        roof = {"bound": "mfma", "achieved": round(tflops, 1), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / FP16_PEAK_TFLOPS, 4), "traffic": traffic,
+                "kernel": thresh_kernel_name(dim), "kernel_ms": round(kernel_ms, 4), "algorithmic_flops": flops,
+                "hbm_gbs": round(traffic / (kernel_ms / 1e3) / 1e9, 1) if traffic else None,
+                "scan_stage_ms": round(scan_ms, 4), "f32_row_bytes": fp32_bytes, "coarse_ms": round(coarse_ms, 4),
+                "fallbacks": fallbacks}
+    elif path == 2:
         # half-precision rows of the probed lists + the K' candidates' rows
         kp = 64 if k + 16 <= 64 else 128
         row_bytes = scanned * ((dim + 1) // 2) * 4 + nq * kp * dim * 4
@@ -451,17 +478,18 @@ def bench_ivf(args, w, base, queries):
     else:
         row_bytes = fp32_bytes
         kernel = "ivf_flat_scan_kernel"
-    achieved = row_bytes / (scan_ms / 1e3) / 1e9
-    log(f"[bench] coarse {coarse_ms:.3f} ms, scan {scan_ms:.3f} ms; {scanned / nq:,.0f} rows per "
-        f"query; path {path} ({fallbacks} of {nq} queries rescanned exactly); {row_bytes / 1e9:.2f} GB "
-        f"read -> {achieved:,.0f} GB/s ({fp32_bytes / 1e9:.2f} GB of f32 rows in the probed lists)")
-    traffic = read_traffic("ivf16_screen_1Mx96_l2_traffic.txt") if (path == 2 and w is WORKLOADS["ivf_1m_l2"]) \
-        else None
-    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": kernel, "kernel_ms": round(scan_ms, 4),
-            "algorithmic_bytes": row_bytes, "f32_row_bytes": fp32_bytes, "coarse_ms": round(coarse_ms, 4),
-            "fallbacks": fallbacks}
+    if path != 3:
+        achieved = row_bytes / (scan_ms / 1e3) / 1e9
+        log(f"[bench] coarse {coarse_ms:.3f} ms, scan {scan_ms:.3f} ms; {scanned / nq:,.0f} rows per "
+            f"query; path {path} ({fallbacks} of {nq} queries rescanned exactly); {row_bytes / 1e9:.2f} GB "
+            f"read -> {achieved:,.0f} GB/s ({fp32_bytes / 1e9:.2f} GB of f32 rows in the probed lists)")
+        traffic = read_traffic("ivf16_screen_1Mx96_l2_traffic.txt") \
+            if (path == 2 and w is WORKLOADS["ivf_1m_l2"]) else None
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": kernel, "kernel_ms": round(scan_ms, 4),
+                "algorithmic_bytes": row_bytes, "f32_row_bytes": fp32_bytes, "coarse_ms": round(coarse_ms, 4),
+                "fallbacks": fallbacks}
     gpu_ids = r.ids().copy()
     cpu = None
     if not args.no_cpu:

@@ -569,8 +569,15 @@ fdb_status fdb_ivf_set_coarse_mode(fdb_ivf* h, uint32_t mode) {
 }
 fdb_status fdb_ivf_set_search_mode(fdb_ivf* h, uint32_t mode) {
   return guarded([&] {
-    if (mode > 1) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown search mode");
+    if (mode > 2) throw Error(FDB_ERR_INVALID_ARGUMENT, "unknown search mode");
     impl_of(h)->set_search_mode((int)mode);
+  });
+}
+
+fdb_status fdb_ivf_last_screen_kernel_ms(fdb_ivf* h, float* out) {
+  return guarded([&] {
+    if (!out) throw Error(FDB_ERR_INVALID_ARGUMENT, "null argument");
+    *out = impl_of(h)->last_screen_kernel_ms();
   });
 }
 

@@ -1306,74 +1306,122 @@ void IvfFlatIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_i
   }
   if (timed) FDB_HIP(hipEventRecord(ev_[1], s));
   const bool l1 = metric_ == FDB_METRIC_MANHATTAN;
+  const bool l2 = metric_ == FDB_METRIC_EUCLIDEAN || metric_ == FDB_METRIC_EUCLIDEAN_SQUARED;
+  // the exact scan of queries [q0, q0 + m), those flagged only when flags
+  auto exact_scan = [&](uint64_t q0, uint64_t m, const int* flags) {
+    IvfFlatScanArgs a{};
+    a.queries = d_qs + q0 * dim_;
+    a.nq = m;
+    a.dim = (int)dim_;
+    a.probes = probes_.p + q0 * np;
+    a.np = (int)np;
+    a.nlist = (int)nlist_;
+    a.data = data_.p;
+    a.boff = boff_.p;
+    a.row_off = row_off_.p;
+    a.row_norm = row_norm_.p;
+    a.q_norm = qn_.p ? qn_.p + q0 : nullptr;
+    a.ids = ids_.p;
+    a.metric = (int)metric_;
+    a.k = (int)k;
+    a.out_ids = d_ids + q0 * k;
+    a.out_d = d_dists + q0 * k;
+    a.out_counts = d_counts + q0;
+    a.flags = flags;
+    FDB_HIP(launch_ivf_flat_scan(a, s));
+  };
+  // list screening on the matrix cores (fdb_ivfpq16.hpp over the rows):
+  // pairs grouped by list, each list's blocks multiplied against up to 256
+  // queries at a time
+  const uint64_t scanned = nlist_ ? h_ids_.size() * np / nlist_ : 0;
+  bool lists = search_mode_ != 1 && l2 && np >= 2 && dim_ <= 256 && nlist_ <= 8192 &&
+               (search_mode_ == 2 || nq * scanned >= kListScreenMinWork);
+  if (lists && !p16_tried_) {
+    p16_.build_rows(rowsl_.p, row_off_.p, h_offsets_, nlist_, (int)dim_, s);
+    p16_tried_ = true;
+  }
+  lists = lists && p16_.ok;
   // (the exact rescoring reads rows as float4: dim a multiple of 4, <= 512)
-  const bool screen = search_mode_ != 1 && l16_.ok && k + 16 <= 128 && dim_ % 4 == 0 && dim_ <= 512 &&
-                      (l1 || metric_ == FDB_METRIC_EUCLIDEAN || metric_ == FDB_METRIC_EUCLIDEAN_SQUARED);
+  const bool screen = !lists && search_mode_ != 1 && l16_.ok && k + 16 <= 128 && dim_ % 4 == 0 && dim_ <= 512 &&
+                      (l1 || l2);
   if (metric_ == FDB_METRIC_COSINE || screen) {
     qn_.reserve(nq);
     FDB_HIP(launch_row_norms(d_qs, nq, dim_, qn_.p, s));
   }
   path_ = 0;
-  if (screen) {
-    // fp16 screening of the probed lists, exact rescoring of K' candidates,
-    // then the exact scan for the queries the bound does not settle
-    const int kp = (k + 16 <= 64) ? 64 : 128;
-    cand_d_.reserve(nq * kp);
-    cand_k_.reserve(nq * kp);
-    cand_c_.reserve(nq);
-    abound_.reserve(nq);
-    flags_.reserve(nq);
-    fallbacks_.reserve(1);
-    hipLaunchKernelGGL(clear_u32, dim3(1), dim3(1), 0, s, fallbacks_.p);
-    FDB_HIP(hipGetLastError());
-    FDB_HIP(l16_.screen(d_qs, nq, probes_.p, np, nlist_, row_off_.p, l1, kp, cand_d_.p, cand_k_.p, cand_c_.p,
-                        abound_.p, s));
-    RescoreArgs r{};
-    r.queries = d_qs;
-    r.dim = (int)dim_;
-    r.rows = rowsl_.p;
-    r.row_norm = row_norm_.p;
-    r.q_norm = qn_.p;
-    r.cand_keys = cand_k_.p;
-    r.cand_d = cand_d_.p;
-    r.cand_counts = cand_c_.p;
-    r.kp = kp;
-    r.metric = (int)metric_;
-    r.k = (int)k;
-    r.ids = ids_.p;
-    r.out_ids = d_ids;
-    r.out_d = d_dists;
-    r.out_counts = d_counts;
-    r.flags = flags_.p;
-    r.fallbacks = fallbacks_.p;
-    r.abound = abound_.p;
-    r.bkind = kBoundIvf16;
-    r.n = h_ids_.size();
-    r.xmag = l1 ? l16_.xnorm1_max : l16_.xnorm2_max;
-    r.xexp = l16_.xexp;
-    FDB_HIP(launch_rescore(r, nq, s));
-    path_ = 2;
+  if (timed) screen_kernel_ms_ = 0.0f;
+  if (lists) {
+    // each slice screened and rescored, then its flagged queries scanned
+    // exactly
+    p16s_.reset_stats(s);
+    p16s_.set_timing(timed);
+    const uint64_t sl = std::min<uint64_t>(nq, Pq16Searcher::slice((int)k));
+    for (uint64_t q0 = 0; q0 < nq; q0 += sl) {
+      const uint64_t m = std::min<uint64_t>(sl, nq - q0);
+      Pq16SearchArgs sa{};
+      sa.queries = d_qs + q0 * dim_;
+      sa.nq = m;
+      sa.probes = probes_.p + q0 * np;
+      sa.np = (int)np;
+      sa.centroids = cent_.p;
+      sa.ids = ids_.p;
+      sa.list_off = row_off_.p;
+      sa.k = (int)k;
+      sa.order = 0;
+      sa.rows = rowsl_.p;
+      sa.sqrt_out = metric_ == FDB_METRIC_EUCLIDEAN ? 1 : 0;
+      sa.out_ids = d_ids + q0 * k;
+      sa.out_d = d_dists + q0 * k;
+      sa.out_counts = d_counts + q0;
+      p16s_.search(p16_, sa, s);
+      exact_scan(q0, m, p16s_.flags());
+    }
+    if (timed) screen_kernel_ms_ = p16s_.screen_ms();
+    p16s_.set_timing(false);
+    path_ = 3;
+  } else {
+    if (screen) {
+      // fp16 screening of the probed lists, exact rescoring of K' candidates,
+      // then the exact scan for the queries the bound does not settle
+      const int kp = (k + 16 <= 64) ? 64 : 128;
+      cand_d_.reserve(nq * kp);
+      cand_k_.reserve(nq * kp);
+      cand_c_.reserve(nq);
+      abound_.reserve(nq);
+      flags_.reserve(nq);
+      fallbacks_.reserve(1);
+      hipLaunchKernelGGL(clear_u32, dim3(1), dim3(1), 0, s, fallbacks_.p);
+      FDB_HIP(hipGetLastError());
+      FDB_HIP(l16_.screen(d_qs, nq, probes_.p, np, nlist_, row_off_.p, l1, kp, cand_d_.p, cand_k_.p, cand_c_.p,
+                          abound_.p, s));
+      RescoreArgs r{};
+      r.queries = d_qs;
+      r.dim = (int)dim_;
+      r.rows = rowsl_.p;
+      r.row_norm = row_norm_.p;
+      r.q_norm = qn_.p;
+      r.cand_keys = cand_k_.p;
+      r.cand_d = cand_d_.p;
+      r.cand_counts = cand_c_.p;
+      r.kp = kp;
+      r.metric = (int)metric_;
+      r.k = (int)k;
+      r.ids = ids_.p;
+      r.out_ids = d_ids;
+      r.out_d = d_dists;
+      r.out_counts = d_counts;
+      r.flags = flags_.p;
+      r.fallbacks = fallbacks_.p;
+      r.abound = abound_.p;
+      r.bkind = kBoundIvf16;
+      r.n = h_ids_.size();
+      r.xmag = l1 ? l16_.xnorm1_max : l16_.xnorm2_max;
+      r.xexp = l16_.xexp;
+      FDB_HIP(launch_rescore(r, nq, s));
+      path_ = 2;
+    }
+    exact_scan(0, nq, screen ? flags_.p : nullptr);
   }
-  IvfFlatScanArgs a{};
-  a.queries = d_qs;
-  a.nq = nq;
-  a.dim = (int)dim_;
-  a.probes = probes_.p;
-  a.np = (int)np;
-  a.nlist = (int)nlist_;
-  a.data = data_.p;
-  a.boff = boff_.p;
-  a.row_off = row_off_.p;
-  a.row_norm = row_norm_.p;
-  a.q_norm = qn_.p;
-  a.ids = ids_.p;
-  a.metric = (int)metric_;
-  a.k = (int)k;
-  a.out_ids = d_ids;
-  a.out_d = d_dists;
-  a.out_counts = d_counts;
-  a.flags = screen ? flags_.p : nullptr;
-  FDB_HIP(launch_ivf_flat_scan(a, s));
   if (timed) {
     FDB_HIP(hipEventRecord(ev_[2], s));
     FDB_HIP(hipEventSynchronize(ev_[2]));
@@ -1385,6 +1433,11 @@ void IvfFlatIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint64_t* d_i
 uint64_t IvfFlatIndex::last_fallbacks(hipStream_t s) {
   std::lock_guard<std::mutex> g(mu_);
   OrderedOn on(order_, s ? s : stream_);
+  if (path_ == 3) {
+    uint64_t fb = 0, cand = 0;
+    p16s_.read_stats(fb, cand, s ? s : stream_);
+    return fb;
+  }
   if (path_ == 0 || !fallbacks_.p) return 0;  // the last search did not screen
   FDB_HIP(hipStreamSynchronize(s ? s : stream_));
   uint32_t v = 0;

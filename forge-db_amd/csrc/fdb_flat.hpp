@@ -8,6 +8,7 @@
 
 #include "fdb_coarse16.hpp"
 #include "fdb_host.hpp"
+#include "fdb_ivfpq16.hpp"
 
 namespace fdb {
 
@@ -350,19 +351,30 @@ class IvfFlatIndex {
     std::lock_guard<std::mutex> g(mu_);
     coarse_.set_mode(m);
   }
-  // scan strategy: 0 = automatic (fp16 screening + exact rescoring for
-  // Euclidean, squared Euclidean and Manhattan when k <= 112 and dim is a
-  // multiple of 4, <= 512), 1 = exact scan only; same results
+  // scan strategy: 0 = automatic (for Euclidean and squared Euclidean,
+  // batches of at least 2^26 (query, row) pairs screen the lists on the
+  // matrix cores, list by list; else fp16 screening per query + exact
+  // rescoring for Euclidean, squared Euclidean and Manhattan when k <= 112
+  // and dim is a multiple of 4, <= 512), 1 = exact scan only, 2 = the
+  // list screening wherever it applies (Euclidean and squared Euclidean,
+  // dim <= 256, nprobe >= 2), else as 0; same results
   void set_search_mode(int m) {
     std::lock_guard<std::mutex> g(mu_);
     search_mode_ = m;
   }
   // queries of the last search rescanned exactly after screening (waits for s)
   uint64_t last_fallbacks(hipStream_t s);
-  // how the last search ran: 0 exact scan, 2 fp16 screening
+  // how the last search ran: 0 exact scan, 2 fp16 screening per query, 3
+  // list screening on the matrix cores
   int last_path() {
     std::lock_guard<std::mutex> g(mu_);
     return path_;
+  }
+  // duration of the list screening's threshold kernel in the last timed
+  // batch (0 when it did not take list screening)
+  float last_screen_kernel_ms() {
+    std::lock_guard<std::mutex> g(mu_);
+    return screen_kernel_ms_;
   }
   uint32_t dim() const { return dim_; }
   uint64_t size() const { return h_ids_.size(); }
@@ -397,6 +409,11 @@ class IvfFlatIndex {
   DevBuf<float> centT_, cent_, data_, row_norm_;
   DevBuf<float> rowsl_;  // [N][dim] row-major, list order (rescoring)
   Ivf16Lists l16_;
+  Pq16Lists p16_;        // the rows as matrix-core blocks (built on first use)
+  bool p16_tried_ = false;
+  Pq16Searcher p16s_;
+  static constexpr uint64_t kListScreenMinWork = 1ull << 26;  // (query, row) pairs
+  float screen_kernel_ms_ = 0.0f;
   int search_mode_ = 0, path_ = 0;
   DevBuf<float> cand_d_, abound_;
   DevBuf<uint64_t> cand_k_;

@@ -181,6 +181,54 @@ __global__ __launch_bounds__(kT) void pq16_norms_kernel(const float* __restrict_
   xnb[slot] = row < len ? s : f_inf();
 }
 
+// Blocks of full rows (Pq16Lists::build_rows): one workgroup (64*KC threads)
+// per block, thread (kc, lane) writes the 8 halves of its lane for k-chunk kc.
+__global__ void pq16_rows_kernel(const float* __restrict__ rows, const uint32_t* __restrict__ list_off,
+                                 const uint32_t* __restrict__ bo, uint32_t nlist, int D, int KC, float scale,
+                                 uint4* __restrict__ out) {
+  const uint32_t B = blockIdx.x;
+  const uint32_t p = owner(bo, nlist, B);
+  const int kc = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const uint32_t row = (B - bo[p]) * 32 + (lane & 31);
+  const bool valid = row < list_off[p + 1] - list_off[p];
+  const float* __restrict__ x = rows + ((uint64_t)list_off[p] + row) * D;
+  _Float16 h[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int d = kc * 16 + 8 * (lane >> 5) + t;
+    h[t] = (_Float16)(valid && d < D ? x[d] * scale : 0.0f);
+  }
+  uint4 w;
+  w.x = (uint32_t)__builtin_bit_cast(uint16_t, h[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[1]) << 16);
+  w.y = (uint32_t)__builtin_bit_cast(uint16_t, h[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[3]) << 16);
+  w.z = (uint32_t)__builtin_bit_cast(uint16_t, h[4]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[5]) << 16);
+  w.w = (uint32_t)__builtin_bit_cast(uint16_t, h[6]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[7]) << 16);
+  out[((uint64_t)B * KC + kc) * 64 + lane] = w;
+}
+
+// Thread per padded row slot: |x|^2 in fp32 (any order is within the bound's
+// gamma_D), the list maximum, +inf past the list's end.
+__global__ __launch_bounds__(kT) void pq16_row_norms_kernel(const float* __restrict__ rows,
+                                                            const uint32_t* __restrict__ list_off,
+                                                            const uint32_t* __restrict__ bo, uint32_t nlist,
+                                                            uint64_t nslots, int D, float* __restrict__ xnb,
+                                                            uint32_t* __restrict__ xmax2) {
+  const uint64_t slot = (uint64_t)blockIdx.x * kT + threadIdx.x;
+  if (slot >= nslots) return;
+  const uint32_t B = (uint32_t)(slot >> 5);
+  const uint32_t p = owner(bo, nlist, B);
+  const uint32_t row = (B - bo[p]) * 32 + (uint32_t)(slot & 31);
+  const bool valid = row < list_off[p + 1] - list_off[p];
+  float s = 0.0f;
+  if (valid) {
+    const float* __restrict__ x = rows + ((uint64_t)list_off[p] + row) * D;
+    for (int d = 0; d < D; ++d) s = __builtin_fmaf(x[d], x[d], s);
+    atomicMax(&xmax2[p], __float_as_uint(s));
+  }
+  xnb[slot] = valid ? s : f_inf();
+}
+
 // ---- (query, probe) pairs by list ------------------------------------------
 //
 // A counting sort without global atomics: workgroup w takes pairs
@@ -496,7 +544,9 @@ template <int KC>
 __device__ __forceinline__ void pair_operand(const ScreenArgs& a, uint32_t q, uint32_t p, int half,
                                              PairOperand<KC>& o) {
   const float* __restrict__ qp = a.queries + (uint64_t)q * a.D;
-  const float* __restrict__ cp = a.centroids + (uint64_t)p * a.D;
+  // full vectors (no centroids): the residual is the query itself
+  const float* __restrict__ cp = a.centroids ? a.centroids + (uint64_t)p * a.D : qp;
+  const float cs = a.centroids ? 1.0f : 0.0f;
   float r[KC][8];
   if (a.vec) {  // whole k-chunks, 16-byte aligned rows: 16-byte loads
 #pragma unroll
@@ -506,10 +556,10 @@ __device__ __forceinline__ void pair_operand(const ScreenArgs& a, uint32_t q, ui
         const int d = kc * 16 + 8 * half + 4 * h4;
         const float4 x = *reinterpret_cast<const float4*>(qp + d);
         const float4 c = *reinterpret_cast<const float4*>(cp + d);
-        r[kc][4 * h4] = x.x - c.x;
-        r[kc][4 * h4 + 1] = x.y - c.y;
-        r[kc][4 * h4 + 2] = x.z - c.z;
-        r[kc][4 * h4 + 3] = x.w - c.w;
+        r[kc][4 * h4] = x.x - cs * c.x;
+        r[kc][4 * h4 + 1] = x.y - cs * c.y;
+        r[kc][4 * h4 + 2] = x.z - cs * c.z;
+        r[kc][4 * h4 + 3] = x.w - cs * c.w;
       }
   } else {
 #pragma unroll
@@ -517,7 +567,7 @@ __device__ __forceinline__ void pair_operand(const ScreenArgs& a, uint32_t q, ui
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int d = kc * 16 + 8 * half + i;
-        r[kc][i] = d < a.D ? qp[d] - cp[d] : 0.0f;
+        r[kc][i] = d < a.D ? qp[d] - cs * cp[d] : 0.0f;
       }
   }
   float mx = 0.0f, rn = 0.0f;
@@ -869,7 +919,7 @@ __global__ __launch_bounds__(64) void pq16_select_kernel(const float* __restrict
                                                          const uint32_t* __restrict__ nreal,
                                                          const uint32_t* __restrict__ jlim,
                                                          const float* __restrict__ epsA, int np, int k,
-                                                         float* __restrict__ dkA) {
+                                                         int margin, float* __restrict__ dkA) {
   __shared__ uint2 queue[64];
   const uint64_t q = blockIdx.x;
   const int lane = threadIdx.x;
@@ -922,7 +972,12 @@ __global__ __launch_bounds__(64) void pq16_select_kernel(const float* __restrict
   tk.flush(queue, qn);
   float em = 0.0f;
   for (uint32_t j = 0; j < jlim[q]; ++j) em = fmaxf(em, epsA[q * np + j]);
-  if (lane == 0) dkA[q] = add_up(tk.tau, em);
+  if (lane == 0) {
+    // margin (the Euclidean metric): rows whose square roots tie with the
+    // k-th's may exceed its squared distance by a few ulps
+    const float dk = add_up(tk.tau, em);
+    dkA[q] = margin ? dk + __builtin_fabsf(dk) * 0x1p-20f : dk;
+  }
 }
 
 // ---- exact rescoring ----------------------------------------------------------
@@ -973,6 +1028,8 @@ struct RescoreArgs16 {
   uint32_t cap;
   const int* force;
   int k, order;
+  const float* rows;  // full vectors in list order (Pq16SearchArgs::rows), or null
+  int sqrt_out;       // with rows: the square root of the squared L2 (Euclidean)
   uint64_t* out_ids;
   float* out_d;
   uint32_t* out_counts;
@@ -1111,6 +1168,62 @@ __device__ __forceinline__ float entry_cached(const float* __restrict__ r, const
     }
     return total;
   }
+}
+
+// The reference's squared L2 (euclidean_distance_squared_avx2,
+// src/distance/simd.rs:335-366: 8 FMA lanes over the 8-float chunks, the
+// lanes summed 0..7, a scalar tail) of a query in LDS and a row in global
+// memory; with a row length a multiple of 4, the row is read 16 bytes at a
+// time, 16 loads in flight.
+__device__ __forceinline__ float row_l2sq(const float* __restrict__ q, const float* __restrict__ x, int n) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const int nb = n / 8;
+  float total = 0.0f;
+  if (nb > 0) {
+    float l[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) l[t] = 0.0f;
+    if ((n & 3) == 0) {
+      const f4* __restrict__ x4 = reinterpret_cast<const f4*>(x);
+      for (int i0 = 0; i0 < nb; i0 += 8) {
+        f4 v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (2 * i0 + j < 2 * nb) v[j] = x4[2 * i0 + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (i0 + j < nb) {
+            const float* __restrict__ qi = q + 8 * (i0 + j);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+              const float d = qi[t] - (t < 4 ? v[2 * j][t] : v[2 * j + 1][t - 4]);
+              l[t] = __builtin_fmaf(d, d, l[t]);
+            }
+          }
+      }
+    } else {
+      for (int i = 0; i < nb; ++i)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const float d = q[8 * i + t] - x[8 * i + t];
+          l[t] = __builtin_fmaf(d, d, l[t]);
+        }
+    }
+    total = l[0];
+#pragma unroll
+    for (int t = 1; t < 8; ++t) total = total + l[t];
+  }
+  for (int i = 8 * nb; i < n; ++i) {
+    const float d = q[i] - x[i];
+    total = total + d * d;
+  }
+  return total;
+}
+
+// The exact distance of a full-vector candidate (list position key).
+__device__ __forceinline__ float row_dist(const RescoreArgs16& a, const float* __restrict__ qs, uint32_t key) {
+  const float t = row_l2sq(qs, a.rows + (uint64_t)key * a.D, a.D);
+  return a.sqrt_out ? __builtin_sqrtf(t) : t;
 }
 
 // The reference's distance of one code: entries v(m) summed in adc_sum order.
@@ -1315,11 +1428,16 @@ __device__ __forceinline__ void pq16_rescore_light(const RescoreArgs16& a, uint6
       float d = f_inf();
       if (has) {
         ++ncand;
-        const CodeRow<MM> code(a.codes + (uint64_t)key * M);
-        const float* __restrict__ cen = a.centroids + (uint64_t)a.probes[q * a.np + jj] * D;
-        d = adc_order(M, a.order, [&](int m) {
-          return entry_direct<DS>(qs + m * dsub, cen + m * dsub, a.cb4 + ((uint64_t)m * 256 + code[m]) * ds4, dsub);
-        });
+        if constexpr (DS < 0) {
+          d = row_dist(a, qs, key);
+        } else {
+          const CodeRow<MM> code(a.codes + (uint64_t)key * M);
+          const float* __restrict__ cen = a.centroids + (uint64_t)a.probes[q * a.np + jj] * D;
+          d = adc_order(M, a.order, [&](int m) {
+            return entry_direct<DS>(qs + m * dsub, cen + m * dsub, a.cb4 + ((uint64_t)m * 256 + code[m]) * ds4,
+                                    dsub);
+          });
+        }
       }
       tk.offer_queued(d, key, has, queue[wave], qn);
     });
@@ -1390,7 +1508,12 @@ __device__ __forceinline__ void pq16_rescore_heavy(RescoreArgs16 a, uint64_t q, 
     const uint2 e = c < cnt ? cq[c] : make_uint2(0u, 0u);
     expand_entries(e, c < cnt, xent[wave], xpre[wave], [&](bool has, uint32_t key, uint32_t jj) {
       float d = f_inf();
-      if (has) {
+      if constexpr (DS < 0) {
+        if (has) {
+          ++ncand;
+          d = row_dist(a, qs, key);
+        }
+      } else if (has) {
         ++ncand;
         const CodeRow<MM> code(a.codes + (uint64_t)key * M);
         if (cached) {
@@ -1545,12 +1668,10 @@ __global__ __launch_bounds__(1024) void pq16_stats_kernel(const int* __restrict_
   }
 }
 
-// Bound coefficients (screen_eps_coeffs): the reference's table distance is
-// a sum of M table entries, each a sum of dsub squares of differences, so a
-// term is rounded at most dsub + M + 2 times (the residual's and the
-// difference's subtractions included).
-void pq16_eps_coeffs(int D16, int M, int dsub, float cmax, float& c_dot, float& c_sq, float& cabs) {
-  screen_eps_coeffs(D16, dsub + M + 2, cmax, c_dot, c_sq, cabs);
+// Bound coefficients (screen_eps_coeffs) for a reference distance whose
+// terms are each rounded at most nref times (Pq16Lists::nref).
+void pq16_eps_coeffs(int D16, int nref, float cmax, float& c_dot, float& c_sq, float& cabs) {
+  screen_eps_coeffs(D16, nref, cmax, c_dot, c_sq, cabs);
 }
 
 }  // namespace
@@ -1563,6 +1684,10 @@ void Pq16Lists::build(const float* d_codebooks, const uint8_t* d_codes, const ui
   D = M * dsub;
   KC = (D + 15) / 16;
   nlist = nl;
+  // the reference's table distance sums M entries, each a sum of dsub
+  // squares of differences: a term is rounded at most dsub + M + 2 times
+  // (the residual's and the difference's subtractions included)
+  nref = dsub + M + 2;
   // B operands beyond 64 registers, or lists beyond the LDS counting sort:
   // the table scan only
   if (KC > 16 || nlist == 0 || nlist > kHistMax) return;
@@ -1617,6 +1742,71 @@ void Pq16Lists::build(const float* d_codebooks, const uint8_t* d_codes, const ui
     FDB_HIP(hipGetLastError());
     hipLaunchKernelGGL(pq16_norms_kernel, dim3((unsigned)cdiv(nblocks * 32, kT)), dim3(kT), 0, s, d_codebooks,
                        d_codes, d_off, bo.p, nlist, nblocks * 32, M, dsub, xnb.p, xmax2.p);
+    FDB_HIP(hipGetLastError());
+  }
+  ok = true;
+}
+
+void Pq16Lists::build_rows(const float* d_rows, const uint32_t* d_off, const std::vector<uint64_t>& offsets,
+                           uint32_t nl, int dim, hipStream_t s) {
+  ok = false;
+  M = 1;
+  dsub = dim;
+  D = dim;
+  KC = (D + 15) / 16;
+  nlist = nl;
+  // the reference's squared L2 (8 FMA lanes, their sum, the tail): a term
+  // is rounded at most dim + 2 times (its subtraction included)
+  nref = dim + 2;
+  if (KC > 16 || nlist == 0 || nlist > kHistMax || dim <= 0) return;
+  std::vector<uint32_t> hbo(nlist + 1, 0);
+  uint64_t nbk = 0;
+  max_blocks = 0;
+  for (uint32_t p = 0; p < nlist; ++p) {
+    hbo[p] = (uint32_t)nbk;
+    const uint64_t nb = cdiv(offsets[p + 1] - offsets[p], 32);
+    nbk += nb;
+    max_blocks = std::max(max_blocks, nb);
+  }
+  if (nbk >= 0xFFFFFFFFull || offsets[nlist] >= 0xFFFFFFFFull) return;
+  hbo[nlist] = (uint32_t)nbk;
+  nblocks = nbk;
+  bo.upload(hbo.data(), hbo.size(), s);
+  stats.reserve(1);
+  hipLaunchKernelGGL(pq16_fill_u32, dim3(1), dim3(kT), 0, s, stats.p, (uint64_t)1, 0u);
+  FDB_HIP(hipGetLastError());
+  const uint64_t n = offsets[nlist] * (uint64_t)dim;
+  if (n > 0) {
+    hipLaunchKernelGGL(pq16_cb_stats_kernel, dim3((unsigned)std::min<uint64_t>(cdiv(n, kT), 1024)), dim3(kT), 0, s,
+                       d_rows, n, stats.p);
+    FDB_HIP(hipGetLastError());
+  }
+  uint32_t mbits = 0;
+  FDB_HIP(hipMemcpyAsync(&mbits, stats.p, 4, hipMemcpyDeviceToHost, s));
+  FDB_HIP(hipStreamSynchronize(s));
+  if (mbits >= 0x7F800000u) return;  // a non-finite component
+  float mxv;
+  std::memcpy(&mxv, &mbits, 4);
+  cmax = mxv;
+  xexp = 0;
+  if (mxv > 0.0f) {
+    int E;
+    (void)std::frexp(mxv, &E);
+    xexp = 13 - E;
+  }
+  if (xexp > 100 || xexp < -100) return;
+  data.reserve(std::max<uint64_t>(nblocks * KC * 64, 1));
+  xnb.reserve(std::max<uint64_t>(nblocks * 32, 1));
+  xmax2.reserve(nlist);
+  hipLaunchKernelGGL(pq16_fill_u32, dim3((unsigned)std::min<uint64_t>(cdiv(nlist, kT), 1024)), dim3(kT), 0, s,
+                     xmax2.p, (uint64_t)nlist, 0u);
+  FDB_HIP(hipGetLastError());
+  if (nblocks > 0) {
+    hipLaunchKernelGGL(pq16_rows_kernel, dim3((unsigned)nblocks), dim3(64 * KC), 0, s, d_rows, d_off, bo.p, nlist, D,
+                       KC, std::ldexp(1.0f, xexp), data.p);
+    FDB_HIP(hipGetLastError());
+    hipLaunchKernelGGL(pq16_row_norms_kernel, dim3((unsigned)cdiv(nblocks * 32, kT)), dim3(kT), 0, s, d_rows, d_off,
+                       bo.p, nlist, nblocks * 32, D, xnb.p, xmax2.p);
     FDB_HIP(hipGetLastError());
   }
   ok = true;
@@ -1737,8 +1927,8 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   sa.queries = a.queries;
   sa.D = L.D;
   sa.vec = L.D == 16 * L.KC && (reinterpret_cast<uintptr_t>(a.queries) & 15) == 0 &&
-           (reinterpret_cast<uintptr_t>(a.centroids) & 15) == 0;
-  sa.centroids = a.centroids;
+           (a.rows || (reinterpret_cast<uintptr_t>(a.centroids) & 15) == 0);
+  sa.centroids = a.rows ? nullptr : a.centroids;  // full vectors: the query is the residual
   sa.list_off = a.list_off;
   sa.bo = L.bo.p;
   sa.data = L.data.p;
@@ -1756,7 +1946,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   sa.cand = cand_.p;
   sa.cap = cap;
   sa.force = force_.p;
-  pq16_eps_coeffs(16 * L.KC, L.M, L.dsub, L.cmax, sa.c_dot, sa.c_sq, sa.cabs);
+  pq16_eps_coeffs(16 * L.KC, L.nref, L.cmax, sa.c_dot, sa.c_sq, sa.cabs);
   void (*dense)(ScreenArgs) = nullptr;
   void (*thresh)(ScreenArgs) = nullptr;
   switch (L.KC) {
@@ -1786,7 +1976,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
 #define FDB_SEL(n)                                                                                              \
   case n:                                                                                                       \
     hipLaunchKernelGGL(pq16_select_kernel<n>, dim3((unsigned)nq), dim3(64), 0, s, bufA_.p, capA, nA_.p, nreal_.p, jlim_.p, \
-                       epsA_.p, np, a.k, dkA_.p);                                                               \
+                       epsA_.p, np, a.k, a.rows && a.sqrt_out ? 1 : 0, dkA_.p);                                 \
     break;
     FDB_SEL(1) FDB_SEL(2) FDB_SEL(4) FDB_SEL(8) FDB_SEL(16)
 #undef FDB_SEL
@@ -1830,6 +2020,8 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   r.force = force_.p;
   r.k = a.k;
   r.order = a.order;
+  r.rows = a.rows;
+  r.sqrt_out = a.sqrt_out;
   r.out_ids = a.out_ids;
   r.out_d = a.out_d;
   r.out_counts = a.out_counts;
@@ -1850,13 +2042,14 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   r.counters = nheavy_.p;
   r.cb4 = L.cb4.p;
   r.nlist = (int)nlist;
-  r.cached = (uint64_t)np * L.D * sizeof(float) <= 32 * 1024;
+  r.cached = !a.rows && (uint64_t)np * L.D * sizeof(float) <= 32 * 1024;
   const size_t lds = sizeof(float) * ((size_t)L.D + (r.cached ? (size_t)np * L.D : 0));
   const int ds = (L.dsub == 3 || L.dsub == 4 || L.dsub == 8) ? L.dsub : 0;
   void (*rk)(RescoreArgs16, uint64_t, uint32_t) = nullptr;
 #define FDB_RS(n)                                                                       \
   case n:                                                                               \
-    rk = ds == 3 ? (L.M == 32 ? pq16_rescore_kernel<n, 3, 32> : pq16_rescore_kernel<n, 3, 0>)        \
+    rk = a.rows ? pq16_rescore_kernel<n, -1, 0>                                                      \
+         : ds == 3 ? (L.M == 32 ? pq16_rescore_kernel<n, 3, 32> : pq16_rescore_kernel<n, 3, 0>)      \
                  : (ds == 4 ? pq16_rescore_kernel<n, 4, 0>                                           \
                             : (ds == 8 ? (L.M == 16 ? pq16_rescore_kernel<n, 8, 16> : pq16_rescore_kernel<n, 8, 0>) \
                                        : pq16_rescore_kernel<n, 0, 0>));                             \

@@ -41,6 +41,7 @@ namespace fdb {
 struct Pq16Lists {
   bool ok = false;
   int M = 0, dsub = 0, D = 0, KC = 0, xexp = 0;
+  int nref = 0;  // roundings of one term in the reference's distance (the bound's gamma)
   uint32_t nlist = 0;
   uint64_t nblocks = 0, max_blocks = 0;
   float cmax = 0.0f;  // largest |codebook component|
@@ -48,6 +49,10 @@ struct Pq16Lists {
   // offsets on the device
   void build(const float* d_codebooks, const uint8_t* d_codes, const uint32_t* d_off,
              const std::vector<uint64_t>& offsets, uint32_t nlist, int M, int dsub, hipStream_t s);
+  // The same blocks over full vectors: d_rows [N][dim] in list order (the
+  // IVF index's lists); x^ is the row itself (M = 1, dsub = dim).
+  void build_rows(const float* d_rows, const uint32_t* d_off, const std::vector<uint64_t>& offsets, uint32_t nlist,
+                  int dim, hipStream_t s);
   DevBuf<uint4> data;
   DevBuf<float> xnb, cb4;  // cb4: codewords padded to a multiple of 4 floats
   DevBuf<uint32_t> xmax2, bo, stats;
@@ -66,6 +71,12 @@ struct Pq16SearchArgs {
   const uint32_t* list_off;  // [nlist+1]
   int k;
   int order;  // AdcOrder of the exact distances
+  // Full vectors (lists built with build_rows): rows [N][dim] in list order;
+  // the query is the residual (centroids unused) and the exact distance is
+  // the reference's squared L2, or its square root with sqrt_out (the
+  // Euclidean metric); codebooks and codes are unused.
+  const float* rows = nullptr;
+  int sqrt_out = 0;
   uint64_t* out_ids;
   float* out_d;
   uint32_t* out_counts;

@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "fdb_ivfpq_search_filtered", "fdb_ivfpq_delete", "fdb_ivfpq_insert", "fdb_ivfpq_compact",
     "fdb_ivfpq_len", "fdb_ivfpq_num_tombstones", "fdb_ivfpq_set_coarse_mode", "fdb_ivf_set_coarse_mode",
     "fdb_ivf_set_search_mode", "fdb_ivf_last_fallbacks", "fdb_ivf_last_search_path",
+    "fdb_ivf_last_screen_kernel_ms",
     "fdb_ivfpq_set_search_mode", "fdb_ivfpq_last_screen_stats", "fdb_ivfpq_last_search_path",
     "fdb_ivfpq_last_screen_kernel_ms",
     "fdb_bf_create", "fdb_bf_add", "fdb_bf_remove", "fdb_bf_len", "fdb_bf_dimension",
@@ -62,7 +63,7 @@ EXPORTED_SYMBOLS = (
 
 LUT_EXACT, LUT_FAST = 0, 1
 BF_AUTO, BF_EXACT, BF_SCREEN, BF_SCREEN_F32 = 0, 1, 2, 3
-IVF_AUTO, IVF_EXACT = 0, 1
+IVF_AUTO, IVF_EXACT, IVF_SCREEN_LISTS = 0, 1, 2
 IVFPQ_AUTO, IVFPQ_EXACT, IVFPQ_SCREEN = 0, 1, 2
 COARSE_AUTO, COARSE_EXACT, COARSE_SCREEN = 0, 1, 2
 
@@ -149,6 +150,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
         "fdb_ivf_set_search_mode": [_P, C.c_uint32],
         "fdb_ivf_last_fallbacks": [_P, _P, _P],
         "fdb_ivf_last_search_path": [_P, _P],
+        "fdb_ivf_last_screen_kernel_ms": [_P, _P],
         "fdb_bf_create": [C.c_uint32, _P],
         "fdb_bf_add": [_P, _P, _P, C.c_uint64, C.c_uint32],
         "fdb_bf_remove": [_P, C.c_uint64, _P],
@@ -707,8 +709,10 @@ class IVFIndex:
 
     def set_search_mode(self, mode: int) -> None:
         """IVF_AUTO (default: half-precision screening + exact rescoring for
-        Euclidean, squared Euclidean and Manhattan) or IVF_EXACT (exact-order
-        scan only); same results."""
+        Euclidean, squared Euclidean and Manhattan; large Euclidean batches
+        screen list by list on the matrix cores), IVF_EXACT (exact-order scan
+        only) or IVF_SCREEN_LISTS (list screening wherever it applies); same
+        results."""
         _check(self._lib, self._lib.fdb_ivf_set_search_mode(self._h, int(mode)))
 
     def last_fallbacks(self, stream: int = 0) -> int:
@@ -718,10 +722,18 @@ class IVFIndex:
         return int(out.value)
 
     def last_search_path(self) -> int:
-        """How the last search ran: 0 exact scan, 2 fp16 screening."""
+        """How the last search ran: 0 exact scan, 2 fp16 screening per query,
+        3 list screening on the matrix cores."""
         out = C.c_uint32()
         _check(self._lib, self._lib.fdb_ivf_last_search_path(self._h, C.byref(out)))
         return int(out.value)
+
+    def last_screen_kernel_ms(self) -> float:
+        """The list screening's threshold kernel duration in the last timed
+        batch (HIP events on its stream; 0 when it took another path)."""
+        out = C.c_float()
+        _check(self._lib, self._lib.fdb_ivf_last_screen_kernel_ms(self._h, C.byref(out)))
+        return float(out.value)
 
     def __len__(self) -> int:
         return int(self._lib.fdb_ivf_len(self._h))

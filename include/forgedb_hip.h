@@ -164,7 +164,7 @@ FDB_API fdb_status fdb_ivfpq_last_screen_stats(fdb_ivfpq* index, void* hip_strea
 FDB_API fdb_status fdb_ivfpq_last_search_path(fdb_ivfpq* index, uint32_t* out);
 /* Measurement (no counterpart in the reference): the duration in ms of the
  * screening kernel that tests every probed code against its query's bound
- * (pq16_screen_kernel, summed over slices) in the last call of
+ * (pq16_thresh_kernel, summed over slices) in the last call of
  * fdb_ivfpq_batch_search_device_timed, from HIP events on the call's
  * stream; 0 when that call took the table scan. */
 FDB_API fdb_status fdb_ivfpq_last_screen_kernel_ms(fdb_ivfpq* index, float* out);
@@ -362,18 +362,35 @@ FDB_API void fdb_ivf_set_nprobe(fdb_ivf* index, uint64_t nprobe);
 /* Coarse selection strategy, as fdb_ivfpq_set_coarse_mode. */
 FDB_API fdb_status fdb_ivf_set_coarse_mode(fdb_ivf* index, uint32_t mode);
 /* Scan strategy (no counterpart in the reference, whose scan is one loop):
- *   FDB_IVF_AUTO (default): for Euclidean, squared Euclidean and Manhattan
- *     with k <= 112 and dim a multiple of 4 (<= 512), the probed lists are scanned in half precision to pick
- *     K' = 64 or 128 candidates per query, their distances are recomputed
- *     exactly in the reference's order, and a rounding-error bound proves
- *     that no other scanned row can enter the top k; queries where it cannot
- *     be proved are rescanned exactly.  Results are identical to
- *     FDB_IVF_EXACT.
+ *   FDB_IVF_AUTO (default):
+ *     - Euclidean and squared Euclidean batches of at least 2^26 (query,
+ *       row) pairs (dim <= 256, nprobe >= 2): list screening.  The (query,
+ *       list) pairs are grouped by list and each list's rows, in half
+ *       precision, are multiplied against up to 256 queries at a time on the
+ *       matrix cores; a rounding-error bound on the k-th distance keeps
+ *       every row that can enter the top k, whose distances are then
+ *       recomputed exactly in the reference's order.
+ *     - else, for Euclidean, squared Euclidean and Manhattan with k <= 112
+ *       and dim a multiple of 4 (<= 512): per-query screening.  The probed
+ *       lists are scanned in half precision to pick K' = 64 or 128
+ *       candidates per query, their distances are recomputed exactly, and a
+ *       bound proves that no other scanned row can enter the top k.
+ *     Queries where a bound cannot be proved are rescanned exactly.  Results
+ *     are identical to FDB_IVF_EXACT.
  *   FDB_IVF_EXACT: the exact-order scan for every query.
+ *   FDB_IVF_SCREEN_LISTS: list screening wherever it applies, whatever the
+ *     batch size; otherwise as FDB_IVF_AUTO.
  * fdb_ivf_last_fallbacks counts the queries of the last search that were
  * rescanned (waits for hip_stream; NULL = the handle's own stream);
- * fdb_ivf_last_search_path reports 0 (exact scan) or 2 (fp16 screening). */
-enum { FDB_IVF_AUTO = 0, FDB_IVF_EXACT = 1 };
+ * fdb_ivf_last_search_path reports 0 (exact scan), 2 (per-query screening)
+ * or 3 (list screening). */
+enum { FDB_IVF_AUTO = 0, FDB_IVF_EXACT = 1, FDB_IVF_SCREEN_LISTS = 2 };
+/* Measurement (no counterpart in the reference): the duration in ms of the
+ * list screening's threshold kernel (pq16_thresh_kernel, summed over
+ * slices) in the last fdb_ivf_batch_search_device call given coarse_ms or
+ * scan_ms, from HIP events on the call's stream; 0 when that call did not
+ * take list screening. */
+FDB_API fdb_status fdb_ivf_last_screen_kernel_ms(fdb_ivf* index, float* out);
 FDB_API fdb_status fdb_ivf_set_search_mode(fdb_ivf* index, uint32_t mode);
 FDB_API fdb_status fdb_ivf_last_fallbacks(fdb_ivf* index, void* hip_stream, uint64_t* out);
 FDB_API fdb_status fdb_ivf_last_search_path(fdb_ivf* index, uint32_t* out);

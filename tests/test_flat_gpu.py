@@ -16,8 +16,8 @@ import pytest
 
 import refcpu
 
-from forgedb import (BF_EXACT, BF_SCREEN, BF_SCREEN_F32, COARSE_SCREEN, IVF_AUTO, IVF_EXACT, BruteForceIndex,
-                     DistanceMetric, ForgeDbError, IVFIndex, datagen)
+from forgedb import (BF_EXACT, BF_SCREEN, BF_SCREEN_F32, COARSE_SCREEN, IVF_AUTO, IVF_EXACT, IVF_SCREEN_LISTS,
+                     BruteForceIndex, DistanceMetric, ForgeDbError, IVFIndex, datagen)
 
 pytestmark = pytest.mark.gpu
 
@@ -346,6 +346,54 @@ def test_ivf_fp16_screen_edges(ivf_small):
                 g, (gi, gd, gc), (oi, od, oc) = ivf_pair(s2, metric, nprobe, k)
                 check_rows(gi, gd, gc, oi, od, oc, f"dim {dim} {metric.name} nprobe {nprobe}")
                 assert g.last_search_path() == path
+
+
+@pytest.mark.parametrize("metric", [DistanceMetric.Euclidean, DistanceMetric.EuclideanSquared],
+                         ids=["l2", "l2sq"])
+@pytest.mark.parametrize("nprobe,k", [(2, 10), (8, 100), (32, 100), (128, 7), (16, 300)])
+def test_ivf_parity_list_screen(ivf_small, metric, nprobe, k):
+    """List screening on the matrix cores (IVF_SCREEN_LISTS forces it at this
+    size): bit-identical to the oracle, ties by list position."""
+    print(f"ivf list screening, nprobe {nprobe}, k {k}, {metric.name}", flush=True)
+    g, (gi, gd, gc), (oi, od, oc) = ivf_pair(ivf_small, metric, nprobe, k, mode=IVF_SCREEN_LISTS)
+    check_rows(gi, gd, gc, oi, od, oc, f"list screen {metric.name} nprobe {nprobe} k {k}")
+    assert g.last_search_path() == 3
+    fb = g.last_fallbacks()
+    print(f"  {fb} of 64 queries rescanned", flush=True)
+    assert fb <= 2
+
+
+def test_ivf_list_screen_edges(ivf_small):
+    """List screening with near-equal rows (square roots that tie), a query
+    far beyond the rows' scale (rescanned exactly), and dimensions off the
+    16-float grid (44, 37: no 16-byte row loads, 20)."""
+    print("ivf list screening edge cases", flush=True)
+    rng = np.random.default_rng(33)
+    s = dict(ivf_small)
+    rows = s["rows"].copy()
+    n0 = int(s["off"][1])
+    for t in range(3):
+        src = rows[t].copy()
+        pos = rng.choice(np.arange(3, n0), min(200, n0 - 3) // 3, replace=False)
+        rows[pos] = src + rng.uniform(-1e-4, 1e-4, (len(pos), rows.shape[1])).astype(np.float32)
+    rows[n0 + 1] = rows[n0]  # exact duplicates: ties resolve to the lower list position
+    s["rows"] = rows
+    q = np.concatenate([rows[:3] + 1e-3, rows[n0:n0 + 1], s["queries"][:5]]).astype(np.float32)
+    q[5, 7] = 1e30  # beyond fp16 once scaled: rescanned exactly
+    for metric in (DistanceMetric.Euclidean, DistanceMetric.EuclideanSquared):
+        g, (gi, gd, gc), (oi, od, oc) = ivf_pair(s, metric, 4, 100, queries=q, mode=IVF_SCREEN_LISTS)
+        check_rows(gi, gd, gc, oi, od, oc, f"list screen near ties {metric.name}")
+        assert g.last_search_path() == 3 and g.last_fallbacks() >= 1, metric.name
+    for dim in (44, 37, 20):
+        base = rng.standard_normal((3000, dim)).astype(np.float32)
+        cen, off, order = refcpu.ivf_build(base, 64, seed=2)
+        s2 = dict(cen=cen, off=off, ids=order.astype(np.uint64), rows=base[order],
+                  queries=rng.standard_normal((50, dim)).astype(np.float32))
+        for metric in (DistanceMetric.Euclidean, DistanceMetric.EuclideanSquared):
+            for nprobe, k in ((2, 100), (6, 30), (64, 112)):
+                g, (gi, gd, gc), (oi, od, oc) = ivf_pair(s2, metric, nprobe, k, mode=IVF_SCREEN_LISTS)
+                check_rows(gi, gd, gc, oi, od, oc, f"list screen dim {dim} {metric.name} nprobe {nprobe}")
+                assert g.last_search_path() == 3
 
 
 @pytest.mark.parametrize("metric", [DistanceMetric.Euclidean, DistanceMetric.Manhattan])

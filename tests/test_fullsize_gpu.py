@@ -78,7 +78,8 @@ def test_bf_1m_x128(metric):
     g = BruteForceIndex.from_arrays(base, None, metric)
     g.set_search_mode(BF_SCREEN)
     screened = g.batch_search_arrays(queries, 100)
-    assert g.last_search_path() == 2
+    # Euclidean: list screening on the matrix cores; Manhattan: per-query fp16 screening
+    assert g.last_search_path() == (3 if metric == DistanceMetric.Euclidean else 2)
     print(f"  exact rescans: {g.last_fallbacks()} of 2000", flush=True)
     g.set_search_mode(BF_EXACT)
     same(screened, g.batch_search_arrays(queries, 100), f"bf {metric.name} screened vs exact")
@@ -96,7 +97,8 @@ def test_ivf_1m_x96(metric):
     g = IVFIndex.build(base, 4096, metric, seed=1)
     g.set_nprobe(32)
     screened = g.batch_search_arrays(queries, 100)
-    assert g.last_search_path() == 2
+    # Euclidean: list screening on the matrix cores; Manhattan: per-query fp16 screening
+    assert g.last_search_path() == (3 if metric == DistanceMetric.Euclidean else 2)
     print(f"  exact rescans: {g.last_fallbacks()} of 10000", flush=True)
     g.set_search_mode(IVF_EXACT)
     same(screened, g.batch_search_arrays(queries, 100), f"ivf {metric.name} screened vs exact")
