@@ -231,15 +231,23 @@ __global__ __launch_bounds__(kT) void pq16_row_norms_kernel(const float* __restr
 
 // ---- (query, probe) pairs by list ------------------------------------------
 //
-// A counting sort without global atomics: workgroup w takes pairs
-// [w*chunk, (w+1)*chunk) of the [nq][np] probe array, counts them per list
-// in LDS and writes its row H[w][list]; pq16_offsets_kernel turns the rows
-// into each list's range and each (w, list) base; the scatter recounts in
-// LDS and places every pair at base + its LDS slot.  A pair (q, j) takes
-// part when its list is valid and j < jlim[q] (jlim null: every probe).
+// A counting sort: workgroup w takes pairs [w*chunk, (w+1)*chunk) of the
+// [nq][np] probe array.  pq16_count_kernel counts them per list in LDS and
+// adds every nonzero count to cnt[list]; pq16_offsets_kernel turns cnt into
+// each list's range of pairs (qoff) and of tiles; pq16_scatter_kernel
+// recounts in LDS, claims the workgroup's range within each list by
+// subtracting its count from cnt[list] (the value left is the range's
+// start, and the subtractions leave cnt zero for the next search), and
+// places every pair at qoff + range start + its LDS slot; it also writes
+// the list of every tile (tl), for a share of the lists.  The order of a
+// list's pairs follows the order of the atomics; the screening's results do
+// not depend on it.  A pair (q, j) takes part when its list is valid and
+// j < jlim[q] (jlim null: every probe).
 
 constexpr uint32_t kHistMax = 8192;  // lists counted in LDS (32 KiB)
-constexpr int kSortWG = 32;          // workgroups of the counting sort (at most)
+constexpr int kSortT = 1024;         // threads of a sorting workgroup
+constexpr int kSortB = 8;            // pairs a sorting thread loads at once
+constexpr int kSortWG = 256;         // sorting workgroups per stage (at most)
 constexpr uint32_t kCB = 64;         // blocks of 32 codes per screening tile
 constexpr uint32_t kXcd = 8;         // L2 domains (XCDs); workgroup b runs on XCD b % 8
 constexpr uint32_t kXcdRun = 4;      // consecutive tiles given to one XCD
@@ -257,26 +265,36 @@ struct PairSet {
   uint64_t chunk;  // pairs per sorting workgroup
 };
 
+// The lists of pairs e + i*kSortT (i < kSortB) of a workgroup's range
+// [., e1), ~0 for pairs past e1 or not taking part.  Every load is issued
+// before the first is used (indices clamped into the range, e < e1).
 // (pairs of a slice number below 2^32)
-__device__ __forceinline__ bool pair_list(const PairSet& s, uint32_t e, uint32_t& p) {
-  const uint32_t q = e / (uint32_t)s.np;
-  const uint32_t j = e - q * (uint32_t)s.np;
-  if (s.jlim && j >= s.jlim[q]) return false;
-  const int32_t v = s.probes[e];
-  if (v < 0 || (uint32_t)v >= s.nlist) return false;
-  p = (uint32_t)v;
-  return true;
+__device__ __forceinline__ void pair_lists(const PairSet& s, uint32_t e, uint32_t e1, uint32_t (&p)[kSortB]) {
+  const uint32_t np = (uint32_t)s.np;
+  int32_t v[kSortB];
+  uint32_t lim[kSortB];
+#pragma unroll
+  for (int i = 0; i < kSortB; ++i) {
+    const uint32_t ei = min(e + (uint32_t)(i * kSortT), e1 - 1);
+    v[i] = s.probes[ei];
+    lim[i] = s.jlim ? s.jlim[ei / np] : np;
+  }
+#pragma unroll
+  for (int i = 0; i < kSortB; ++i) {
+    const uint32_t ei = e + (uint32_t)(i * kSortT);
+    const uint32_t j = ei - ei / np * np;
+    p[i] = ei < e1 && j < lim[i] && v[i] >= 0 && (uint32_t)v[i] < s.nlist ? (uint32_t)v[i] : ~0u;
+  }
 }
 
 // Both stages in one launch each (grid y = stage): 0 pairs the first lists
-// (jlim), 1 every probe.  Stage st uses H + st*G*nlist, qoff and toff +
+// (jlim), 1 every probe.  Stage st uses cnt + st*nlist, qoff and toff +
 // st*(nlist+1), qlist + st*npr and tl + st*tl1.
 struct PairStages {
   PairSet s0, s1;
   uint32_t blim0, blim1;  // blocks screened per list
   uint32_t tq0, tq1;      // pairs per tile
-  uint32_t G;             // sorting workgroups per stage
-  uint32_t* H;
+  uint32_t* cnt;          // [2][nlist], zero between searches
   uint32_t* qoff;
   uint32_t* toff;
   uint2* qlist;
@@ -286,54 +304,70 @@ struct PairStages {
 
 __device__ __forceinline__ PairSet stage_set(const PairStages& ps, uint32_t st) { return st ? ps.s1 : ps.s0; }
 
-__global__ __launch_bounds__(kT) void pq16_count_kernel(PairStages ps) {
-  __shared__ uint32_t hist[kHistMax];
-  const PairSet s = stage_set(ps, blockIdx.y);
-  uint32_t* __restrict__ H = ps.H + (uint64_t)blockIdx.y * ps.G * s.nlist;
-  const uint32_t w = blockIdx.x;
-  for (uint32_t i = threadIdx.x; i < s.nlist; i += kT) hist[i] = 0;
-  __syncthreads();
-  const uint32_t n = (uint32_t)(s.nq * (uint64_t)s.np);
-  const uint32_t e1 = (uint32_t)min((uint64_t)n, (w + 1) * s.chunk);
-  for (uint32_t e = (uint32_t)(w * s.chunk) + threadIdx.x; e < e1; e += kT) {
-    uint32_t p;
-    if (pair_list(s, e, p)) atomicAdd(&hist[p], 1u);
-  }
-  __syncthreads();
-  for (uint32_t i = threadIdx.x; i < s.nlist; i += kT) H[(uint64_t)w * s.nlist + i] = hist[i];
+// The workgroup's pairs [e0, e1) of its stage.
+__device__ __forceinline__ void sort_range(const PairSet& s, uint32_t& e0, uint32_t& e1) {
+  const uint64_t n = s.nq * (uint64_t)s.np;
+  e0 = (uint32_t)min(n, blockIdx.x * s.chunk);
+  e1 = (uint32_t)min(n, (blockIdx.x + 1) * s.chunk);
 }
 
-// One workgroup of 1024 threads per stage.  cnt_p = sum over w of H[w][p]; qoff =
-// exclusive prefix of cnt; tiles_p = ceil(cnt_p / tq) * ceil(min(nb_p,
-// blim) / kCB) (nb_p = bo[p+1] - bo[p]), toff = their exclusive prefix; both
-// totals at [nlist]; tl[t] = the list of tile t.  H[w][p] is replaced by the
-// pair base of (w, p).
-__global__ __launch_bounds__(1024) void pq16_offsets_kernel(PairStages ps, const uint32_t* __restrict__ bo) {
+__global__ __launch_bounds__(kSortT) void pq16_count_kernel(PairStages ps) {
+  __shared__ uint32_t hist[kHistMax];
+  const PairSet s = stage_set(ps, blockIdx.y);
+  uint32_t* __restrict__ cnt = ps.cnt + (uint64_t)blockIdx.y * s.nlist;
+  for (uint32_t i = threadIdx.x; i < s.nlist; i += kSortT) hist[i] = 0;
+  __syncthreads();
+  uint32_t e0, e1;
+  sort_range(s, e0, e1);
+  for (uint32_t e = e0 + threadIdx.x; e < e1; e += kSortT * kSortB) {
+    uint32_t p[kSortB];
+    pair_lists(s, e, e1, p);
+#pragma unroll
+    for (int i = 0; i < kSortB; ++i)
+      if (p[i] != ~0u) atomicAdd(&hist[p[i]], 1u);
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < s.nlist; i += kSortT) {
+    const uint32_t h = hist[i];
+    if (h) atomicAdd(&cnt[i], h);
+  }
+}
+
+// One workgroup of kSortT threads per stage, thread t taking lists t +
+// u*kSortT.  qoff = exclusive prefix of cnt; tiles_p = ceil(cnt_p / tq) *
+// ceil(min(nb_p, blim) / kCB) (nb_p = bo[p+1] - bo[p]), toff = their
+// exclusive prefix; both totals at [nlist].
+__global__ __launch_bounds__(kSortT) void pq16_offsets_kernel(PairStages ps, const uint32_t* __restrict__ bo) {
+  constexpr int kU = kHistMax / kSortT;
   const uint32_t stage = blockIdx.x;
-  const uint32_t nlist = ps.s0.nlist, G = ps.G;
+  const uint32_t nlist = ps.s0.nlist;
   const uint32_t blim = stage ? ps.blim1 : ps.blim0;
   const uint32_t tq = stage ? ps.tq1 : ps.tq0;
-  uint32_t* __restrict__ H = ps.H + (uint64_t)stage * G * nlist;
+  const uint32_t* __restrict__ cnt = ps.cnt + (uint64_t)stage * nlist;
   uint32_t* __restrict__ qoff = ps.qoff + (uint64_t)stage * (nlist + 1);
   uint32_t* __restrict__ toff = ps.toff + (uint64_t)stage * (nlist + 1);
-  uint32_t* __restrict__ tl = ps.tl + stage * ps.tl1;
-  __shared__ uint32_t wq[16], wt[16];
+  __shared__ uint32_t wq[kSortT / 64], wt[kSortT / 64];
   __shared__ uint32_t carry[2];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  // every list's count and block count first
+  uint32_t c[kU], nb[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const uint32_t i = min((uint32_t)(u * kSortT + tid), nlist - 1);
+    c[u] = cnt[i];
+    nb[u] = bo[i + 1] - bo[i];
+  }
   if (tid == 0) carry[0] = carry[1] = 0;
   __syncthreads();
-  for (uint32_t base = 0; base < nlist; base += 1024) {
-    const uint32_t i = base + tid;
-    uint32_t c = 0, t = 0;
-    if (i < nlist) {
-#pragma unroll 4
-      for (uint32_t w = 0; w < G; ++w) c += H[(uint64_t)w * nlist + i];
-      const uint32_t nb = min(bo[i + 1] - bo[i], blim);
-      t = (c + tq - 1) / tq * ((nb + kCB - 1) / kCB);
-    }
-    uint32_t sc = c, st = t;  // inclusive wave scans
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    if ((uint32_t)(u * kSortT) >= nlist) break;
+    const uint32_t i = u * kSortT + tid;
+    const uint32_t cu = i < nlist ? c[u] : 0u;
+    const uint32_t t = i < nlist ? (cu + tq - 1) / tq * ((min(nb[u], blim) + kCB - 1) / kCB) : 0u;
+    uint32_t sc = cu, st = t;  // inclusive wave scans
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const uint32_t uc = (uint32_t)__shfl_up((int)sc, off);
@@ -354,18 +388,11 @@ __global__ __launch_bounds__(1024) void pq16_offsets_kernel(PairStages ps, const
       pt += wt[w];
     }
     if (i < nlist) {
-      uint32_t run = pq + sc - c;
-      qoff[i] = run;
+      qoff[i] = pq + sc - cu;
       toff[i] = pt + st - t;
-      for (uint32_t u = 0; u < t; ++u) tl[pt + st - t + u] = i;  // the list of each of its tiles
-      for (uint32_t w = 0; w < G; ++w) {
-        const uint32_t h = H[(uint64_t)w * nlist + i];
-        H[(uint64_t)w * nlist + i] = run;
-        run += h;
-      }
     }
     __syncthreads();
-    if (tid == 1023) {
+    if (tid == kSortT - 1) {
       carry[0] = pq + sc;
       carry[1] = pt + st;
     }
@@ -377,22 +404,90 @@ __global__ __launch_bounds__(1024) void pq16_offsets_kernel(PairStages ps, const
   }
 }
 
-__global__ __launch_bounds__(kT) void pq16_scatter_kernel(PairStages ps) {
+__global__ __launch_bounds__(kSortT) void pq16_scatter_kernel(PairStages ps) {
   __shared__ uint32_t hist[kHistMax];
   const PairSet s = stage_set(ps, blockIdx.y);
-  const uint32_t* __restrict__ base = ps.H + (uint64_t)blockIdx.y * ps.G * s.nlist;
+  uint32_t* __restrict__ cnt = ps.cnt + (uint64_t)blockIdx.y * s.nlist;
+  const uint32_t* __restrict__ qoff = ps.qoff + (uint64_t)blockIdx.y * (s.nlist + 1);
   uint2* __restrict__ qlist = ps.qlist + blockIdx.y * ps.npr;
-  const uint32_t w = blockIdx.x;
-  for (uint32_t i = threadIdx.x; i < s.nlist; i += kT) hist[i] = 0;
+  const uint32_t np = (uint32_t)s.np;
+  for (uint32_t i = threadIdx.x; i < s.nlist; i += kSortT) hist[i] = 0;
+  // tl[t] = the list of tile t, for the workgroup's share of the lists:
+  // lane j of wave w takes list b + j*16 + w of each run b of 1024, and all
+  // the wave's lanes write each one's tiles (the first run's tile ranges
+  // loaded now, written at the end)
+  const uint32_t* __restrict__ toff = ps.toff + (uint64_t)blockIdx.y * (s.nlist + 1);
+  const uint32_t per = (s.nlist + gridDim.x - 1) / gridDim.x;
+  const uint32_t l0 = blockIdx.x * per, l1 = min(s.nlist, l0 + per);
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t r = lane * (kSortT / 64) + (threadIdx.x >> 6);
+  uint32_t lo0 = 0, hi0 = 0;
+  if (l0 + r < l1) {
+    lo0 = toff[l0 + r];
+    hi0 = toff[l0 + r + 1];
+  }
   __syncthreads();
-  const uint32_t n = (uint32_t)(s.nq * (uint64_t)s.np);
-  const uint32_t e1 = (uint32_t)min((uint64_t)n, (w + 1) * s.chunk);
-  for (uint32_t e = (uint32_t)(w * s.chunk) + threadIdx.x; e < e1; e += kT) {
-    uint32_t p;
-    if (pair_list(s, e, p)) {
-      const uint32_t slot = atomicAdd(&hist[p], 1u);
-      const uint32_t q = e / (uint32_t)s.np;
-      qlist[base[(uint64_t)w * s.nlist + p] + slot] = make_uint2(q, e - q * (uint32_t)s.np);
+  uint32_t e0, e1;
+  sort_range(s, e0, e1);
+  // the counts (the first batch's lists kept)
+  uint32_t p0[kSortB];
+  const uint32_t f = e0 + threadIdx.x;
+  if (f < e1) {
+    pair_lists(s, f, e1, p0);
+#pragma unroll
+    for (int i = 0; i < kSortB; ++i)
+      if (p0[i] != ~0u) atomicAdd(&hist[p0[i]], 1u);
+  }
+  for (uint32_t e = f + kSortT * kSortB; e < e1; e += kSortT * kSortB) {
+    uint32_t p[kSortB];
+    pair_lists(s, e, e1, p);
+#pragma unroll
+    for (int i = 0; i < kSortB; ++i)
+      if (p[i] != ~0u) atomicAdd(&hist[p[i]], 1u);
+  }
+  __syncthreads();
+  // the workgroup's range of each list: hist becomes its next position
+  for (uint32_t i = threadIdx.x; i < s.nlist; i += kSortT) {
+    const uint32_t h = hist[i];
+    if (h) hist[i] = qoff[i] + atomicSub(&cnt[i], h) - h;
+  }
+  __syncthreads();
+  if (f < e1) {
+#pragma unroll
+    for (int i = 0; i < kSortB; ++i)
+      if (p0[i] != ~0u) {
+        const uint32_t e = f + (uint32_t)(i * kSortT);
+        const uint32_t q = e / np;
+        qlist[atomicAdd(&hist[p0[i]], 1u)] = make_uint2(q, e - q * np);
+      }
+  }
+  for (uint32_t e = f + kSortT * kSortB; e < e1; e += kSortT * kSortB) {
+    uint32_t p[kSortB];
+    pair_lists(s, e, e1, p);
+#pragma unroll
+    for (int i = 0; i < kSortB; ++i)
+      if (p[i] != ~0u) {
+        const uint32_t ei = e + (uint32_t)(i * kSortT);
+        const uint32_t q = ei / np;
+        qlist[atomicAdd(&hist[p[i]], 1u)] = make_uint2(q, ei - q * np);
+      }
+  }
+  uint32_t* __restrict__ tl = ps.tl + blockIdx.y * ps.tl1;
+  for (uint32_t b = l0; b < l1; b += kSortT) {
+    uint32_t lo = lo0, hi = hi0;
+    if (b != l0) {
+      lo = hi = 0;
+      if (b + r < l1) {
+        lo = toff[b + r];
+        hi = toff[b + r + 1];
+      }
+    }
+    for (uint64_t m = __ballot(hi != lo); m; m &= m - 1) {
+      const int l = __builtin_ctzll(m);
+      const uint32_t al = (uint32_t)__builtin_amdgcn_readlane((int)lo, l);
+      const uint32_t nl = (uint32_t)__builtin_amdgcn_readlane((int)(hi - lo), l);
+      const uint32_t li = (uint32_t)__builtin_amdgcn_readlane((int)(b + r), l);
+      for (uint32_t v = lane; v < nl; v += 64) tl[al + v] = li;
     }
   }
 }
@@ -408,24 +503,47 @@ __global__ __launch_bounds__(kT) void pq16_plan_kernel(const int32_t* __restrict
                                                        uint32_t* __restrict__ nreal, uint32_t* __restrict__ ccnt,
                                                        int* __restrict__ force, float* __restrict__ epsA,
                                                        uint32_t* __restrict__ counters) {
-  const uint64_t q = (uint64_t)blockIdx.x * kT + threadIdx.x;
+  const uint64_t q0 = (uint64_t)blockIdx.x * kT;
+  const uint64_t q = q0 + threadIdx.x;
   if (q < 4) counters[q] = 0;
+  // the workgroup's bounds start clear (coalesced)
+  const uint64_t e1 = min(nq, q0 + kT) * (uint64_t)np;
+  for (uint64_t e = q0 * np + threadIdx.x; e < e1; e += kT) epsA[e] = 0.0f;
   if (q >= nq) return;
-  ccnt[q] = 0;  // the query's counters and bounds start clear
+  ccnt[q] = 0;  // the query's counters start clear
   force[q] = 0;
-  for (int j = 0; j < np; ++j) epsA[q * np + j] = 0.0f;
+  // the first kPre probes' list lengths loaded together
+  constexpr int kPre = 4;
+  uint32_t len[kPre];
+  {
+    int32_t p[kPre];
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) p[j] = probes[q * np + min(j, np - 1)];
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+      const bool ok = p[j] >= 0 && (uint32_t)p[j] < nlist;
+      const uint32_t pc = ok ? (uint32_t)p[j] : 0u;
+      const uint32_t a0 = list_off[pc], a1 = list_off[pc + 1];
+      len[j] = ok ? a1 - a0 : 0u;  // an invalid probe: no codes
+    }
+  }
   uint64_t cum = 0, real = 0;
   uint32_t J = 0;
   for (int j = 0; j < np; ++j) {
     if (real >= (uint64_t)k || cum >= capA) break;
-    const int32_t p = probes[q * np + j];
+    uint64_t n;
+    if (j < kPre) {
+      n = len[0];
+#pragma unroll
+      for (int u = 1; u < kPre; ++u) n = j == u ? len[u] : n;
+    } else {
+      const int32_t p = probes[q * np + j];
+      n = p >= 0 && (uint32_t)p < nlist ? list_off[p + 1] - list_off[p] : 0;
+    }
     offA[q * np + j] = (uint32_t)cum;
     J = (uint32_t)j + 1;
-    if (p >= 0 && (uint32_t)p < nlist) {
-      const uint64_t len = list_off[p + 1] - list_off[p];
-      real += std::min<uint64_t>(len, capA - cum);
-      cum += (len + 31) / 32 * 32;
-    }
+    real += std::min<uint64_t>(n, capA - cum);
+    cum += (n + 31) / 32 * 32;
   }
   jlim[q] = J;
   nA[q] = (uint32_t)std::min<uint64_t>(cum, capA);
@@ -1858,6 +1976,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   if (nq == 0) return;
   const uint32_t nlist = L.nlist;
   const int np = a.np;
+  if (np < 1) throw Error(FDB_ERR_INVALID_ARGUMENT, "screened search: nprobe < 1");
   const uint32_t cap = capacity(a.k);
   const uint64_t npr = nq * (uint64_t)np;
   if (ncu_ == 0) {
@@ -1866,7 +1985,16 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
     FDB_HIP(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev));
     ncu_ = std::max(v, 1);
   }
-  H_.reserve(2ull * kSortWG * nlist);
+  if (cnt_.n < 2ull * nlist) {  // the list counts start zero; every search leaves them zero
+    cnt_.reserve(2ull * nlist);
+    cnt_clean_ = false;
+  }
+  if (!cnt_clean_) {
+    hipLaunchKernelGGL(pq16_fill_u32, dim3((unsigned)cdiv(2ull * nlist, kT)), dim3(kT), 0, s, cnt_.p,
+                       2ull * nlist, 0u);
+    FDB_HIP(hipGetLastError());
+    cnt_clean_ = true;
+  }
   qoff_.reserve(2 * (uint64_t)(nlist + 1));
   toff_.reserve(2 * (uint64_t)(nlist + 1));
   qlist_.reserve(2 * std::max<uint64_t>(npr, 1));
@@ -1892,7 +2020,8 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   FDB_HIP(hipGetLastError());
 
   // (query, probe) pairs grouped by list, stage st (0: first lists, 1: all)
-  const uint32_t G = (uint32_t)std::min<uint64_t>(std::max<uint64_t>(cdiv(npr, 8192), 1), kSortWG);
+  const uint32_t G =
+      (uint32_t)std::min<uint64_t>(std::max<uint64_t>(cdiv(npr, (uint64_t)kSortT * kSortB), 1), kSortWG);
   const uint64_t chunk = cdiv(npr, G);
   // tiles of a stage: at most (pairs / 128 + lists) pair tiles per chunk
   auto tile_bound = [&](uint32_t blim) {
@@ -1908,20 +2037,21 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   pst.blim1 = 0xFFFFFFFFu;
   pst.tq0 = kTilePairs;
   pst.tq1 = kTilePairs * stage_b_groups(L.KC);
-  pst.G = G;
-  pst.H = H_.p;
+  pst.cnt = cnt_.p;
   pst.qoff = qoff_.p;
   pst.toff = toff_.p;
   pst.qlist = qlist_.p;
   pst.tl = tl_.p;
   pst.npr = std::max<uint64_t>(npr, 1);
   pst.tl1 = tbA;
-  hipLaunchKernelGGL(pq16_count_kernel, dim3(G, 2), dim3(kT), 0, s, pst);
+  cnt_clean_ = false;  // until the scatter has run
+  hipLaunchKernelGGL(pq16_count_kernel, dim3(G, 2), dim3(kSortT), 0, s, pst);
   FDB_HIP(hipGetLastError());
-  hipLaunchKernelGGL(pq16_offsets_kernel, dim3(2), dim3(1024), 0, s, pst, L.bo.p);
+  hipLaunchKernelGGL(pq16_offsets_kernel, dim3(2), dim3(kSortT), 0, s, pst, L.bo.p);
   FDB_HIP(hipGetLastError());
-  hipLaunchKernelGGL(pq16_scatter_kernel, dim3(G, 2), dim3(kT), 0, s, pst);
+  hipLaunchKernelGGL(pq16_scatter_kernel, dim3(G, 2), dim3(kSortT), 0, s, pst);
   FDB_HIP(hipGetLastError());
+  cnt_clean_ = true;
 
   ScreenArgs sa{};
   sa.queries = a.queries;

@@ -121,7 +121,8 @@ class Pq16Searcher {
   bool timing_ = false;
   float screen_ms_ = 0.0f;
   hipEvent_t tev_[2] = {nullptr, nullptr};
-  DevBuf<uint32_t> H_, qoff_, toff_, tl_, jlim_, offA_, nA_, nreal_, ccnt_, stat_, nheavy_, order_;
+  bool cnt_clean_ = false;  // cnt_ holds zeros
+  DevBuf<uint32_t> cnt_, qoff_, toff_, tl_, jlim_, offA_, nA_, nreal_, ccnt_, stat_, nheavy_, order_;
   DevBuf<uint2> qlist_, cand_, heavy_, multi_;
   DevBuf<uint32_t> part_k_;
   DevBuf<float> epsA_, bufA_, dkA_, part_d_;
