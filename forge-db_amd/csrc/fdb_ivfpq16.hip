@@ -45,6 +45,12 @@ constexpr int kTilePairs = 128;
 // group at four.
 constexpr int stage_b_groups(int KC) { return KC <= 6 ? 2 : 1; }
 constexpr int stage_b_waves(int KC) { return KC <= 6 ? 3 : (KC <= 8 ? 4 : (KC <= 12 ? 3 : 2)); }
+// Stage B's waves per workgroup and ring stages.  Measured at 1M x 128
+// (KC 8): eight waves sharing a six- or eight-stage ring (tiles of 256
+// pairs, two workgroups per CU) took 0.195 ms against 0.175-0.185 with four
+// waves and three stages; four stages at four waves per SIMD, 0.183.
+constexpr int stage_b_wgwaves(int KC) { return (void)KC, 4; }
+constexpr int stage_b_stages(int KC) { return (void)KC, 3; }
 
 uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
@@ -72,6 +78,7 @@ __device__ __forceinline__ void sched_reads_then_mfma() {
   __builtin_amdgcn_sched_group_barrier(0x100, N, 0);  // DS reads
   __builtin_amdgcn_sched_group_barrier(0x008, N, 0);  // MFMA
 }
+
 
 // WaveTopK registers for k: ceil(k / 64) rounded up to a power of two
 int list_regs(int k) {
@@ -248,9 +255,10 @@ constexpr uint32_t kHistMax = 8192;  // lists counted in LDS (32 KiB)
 constexpr int kSortT = 1024;         // threads of a sorting workgroup
 constexpr int kSortB = 8;            // pairs a sorting thread loads at once
 constexpr int kSortWG = 256;         // sorting workgroups per stage (at most)
-constexpr uint32_t kCB = 64;         // blocks of 32 codes per screening tile
+constexpr uint32_t kCB = 64;         // blocks of 32 codes per screening tile (at most)
 constexpr uint32_t kXcd = 8;         // L2 domains (XCDs); workgroup b runs on XCD b % 8
-constexpr uint32_t kXcdRun = 4;      // consecutive tiles given to one XCD
+constexpr uint32_t kXcdRun = 4;      // consecutive tiles given to one XCD (static tiles)
+constexpr uint32_t kXcdRunDyn = 16;  // the same for dynamically taken tiles
 constexpr int kNS = 4;               // one-block stages in stage A's LDS ring
 constexpr uint32_t kLight = 256;     // candidate entries rescored by one wave (more: in parts)
 constexpr uint32_t kPart = 256;      // entries of one part of a heavy query (a workgroup)
@@ -289,17 +297,21 @@ __device__ __forceinline__ void pair_lists(const PairSet& s, uint32_t e, uint32_
 
 // Both stages in one launch each (grid y = stage): 0 pairs the first lists
 // (jlim), 1 every probe.  Stage st uses cnt + st*nlist, qoff and toff +
-// st*(nlist+1), qlist + st*npr and tl + st*tl1.
+// st*(nlist+1), qlist + st*npr and desc + st*tl1.
 struct PairStages {
   PairSet s0, s1;
   uint32_t blim0, blim1;  // blocks screened per list
   uint32_t tq0, tq1;      // pairs per tile
+  uint32_t cb0, cb1;      // blocks per tile (at most kCB)
   uint32_t* cnt;          // [2][nlist], zero between searches
   uint32_t* qoff;
   uint32_t* toff;
+  uint32_t* tcnt;         // [2][nlist] tiles of each list
+  uint32_t* tctr;         // [2][kXcd] tile counters, zeroed by the offsets kernel
   uint2* qlist;
-  uint32_t* tl;
+  uint4* desc;  // [tiles] tile descriptors (tile_work)
   uint64_t npr, tl1;
+  uint32_t sort;  // tiles in descending order of size (else in list order)
 };
 
 __device__ __forceinline__ PairSet stage_set(const PairStages& ps, uint32_t st) { return st ? ps.s1 : ps.s0; }
@@ -333,24 +345,59 @@ __global__ __launch_bounds__(kSortT) void pq16_count_kernel(PairStages ps) {
   }
 }
 
+// Exclusive prefix of v over the workgroup's threads in thread order, added
+// to carry (the running total, updated for the next call).  All threads call
+// this; ws holds kSortT / 64 words.
+__device__ __forceinline__ uint32_t block_prefix(uint32_t v, uint32_t* ws, uint32_t& carry) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t sc = v;  // inclusive wave scan
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t u = (uint32_t)__shfl_up((int)sc, off);
+    if (lane >= off) sc += u;
+  }
+  if (lane == 63) ws[wave] = sc;
+  __syncthreads();
+  uint32_t pre = carry, tot = carry;
+  for (int w = 0; w < kSortT / 64; ++w) {
+    pre += w < wave ? ws[w] : 0u;
+    tot += ws[w];
+  }
+  __syncthreads();
+  carry = tot;
+  return pre + sc - v;
+}
+
 // One workgroup of kSortT threads per stage, thread t taking lists t +
-// u*kSortT.  qoff = exclusive prefix of cnt; tiles_p = ceil(cnt_p / tq) *
-// ceil(min(nb_p, blim) / kCB) (nb_p = bo[p+1] - bo[p]), toff = their
-// exclusive prefix; both totals at [nlist].
+// u*kSortT.
+//   qoff = exclusive prefix of cnt in list order (qoff[nlist] the total).
+//   tiles_p = ceil(cnt_p / tq) * ceil(min(nb_p, blim) / cb) (nb_p = bo[p+1] -
+//   bo[p]); with sort, the tile ranges are laid out in descending order of
+//   the list's full tile (min(nb_p, blim, cb) blocks x min(groups_p, tq/32)
+//   groups of 32 pairs), so that workgroups taking tiles in order meet the
+//   longest first and the shortest last (the order within equal sizes
+//   follows the LDS atomics); else in list order.  toff[p] = the list's first
+//   tile, tcnt[p] = its tiles, toff[nlist] = the total.  The stage's tile
+//   counters are zeroed.
 __global__ __launch_bounds__(kSortT) void pq16_offsets_kernel(PairStages ps, const uint32_t* __restrict__ bo) {
   constexpr int kU = kHistMax / kSortT;
+  constexpr uint32_t kKeys = kCB * 8 + 1;  // tile sizes 0 .. 64 blocks x 8 groups
   const uint32_t stage = blockIdx.x;
   const uint32_t nlist = ps.s0.nlist;
   const uint32_t blim = stage ? ps.blim1 : ps.blim0;
   const uint32_t tq = stage ? ps.tq1 : ps.tq0;
+  const uint32_t cb = stage ? ps.cb1 : ps.cb0;
+  const bool sort = ps.sort != 0;
   const uint32_t* __restrict__ cnt = ps.cnt + (uint64_t)stage * nlist;
   uint32_t* __restrict__ qoff = ps.qoff + (uint64_t)stage * (nlist + 1);
   uint32_t* __restrict__ toff = ps.toff + (uint64_t)stage * (nlist + 1);
-  __shared__ uint32_t wq[kSortT / 64], wt[kSortT / 64];
-  __shared__ uint32_t carry[2];
+  uint32_t* __restrict__ tcnt = ps.tcnt + (uint64_t)stage * nlist;
+  __shared__ uint32_t ws[kSortT / 64];
+  __shared__ uint32_t hist[kKeys];
+  __shared__ uint32_t tbr[kHistMax];  // tiles by rank, then their prefix
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  if (tid < (int)kXcd) ps.tctr[stage * kXcd + tid] = 0u;
+  for (uint32_t i = tid; i < kKeys; i += kSortT) hist[i] = 0;
   // every list's count and block count first
   uint32_t c[kU], nb[kU];
 #pragma unroll
@@ -359,52 +406,85 @@ __global__ __launch_bounds__(kSortT) void pq16_offsets_kernel(PairStages ps, con
     c[u] = cnt[i];
     nb[u] = bo[i + 1] - bo[i];
   }
-  if (tid == 0) carry[0] = carry[1] = 0;
+  __syncthreads();
+  // pair offsets in list order; tile counts and size keys, ranked by key
+  uint32_t carry = 0, t[kU], key[kU], rin[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const uint32_t i = u * kSortT + tid;
+    const uint32_t cu = i < nlist ? c[u] : 0u;
+    const uint32_t nbl = min(nb[u], blim);
+    t[u] = (cu + tq - 1) / tq * ((nbl + cb - 1) / cb);
+    key[u] = t[u] ? min(nbl, cb) * min((cu + 31) / 32, tq / 32) : 0u;
+    if ((uint32_t)(u * kSortT) < nlist) {  // workgroup-uniform
+      const uint32_t pre = block_prefix(cu, ws, carry);
+      if (i < nlist) qoff[i] = pre;
+    }
+    rin[u] = i < nlist ? atomicAdd(&hist[key[u]], 1u) : 0u;
+  }
+  if (tid == 0) qoff[nlist] = carry;
+  __syncthreads();
+  // bucket starts in descending key order (wave 0: lane l sums keys
+  // kKeys-1-9l .. kKeys-9-9l)
+  if (tid < 64) {
+    constexpr int kPer = (kKeys + 63) / 64;
+    uint32_t sum = 0;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int kk = (int)kKeys - 1 - (tid * kPer + e);
+      sum += kk >= 0 ? hist[kk] : 0u;
+    }
+    uint32_t sc = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t u = (uint32_t)__shfl_up((int)sc, off);
+      if (tid >= off) sc += u;
+    }
+    uint32_t run = sc - sum;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int kk = (int)kKeys - 1 - (tid * kPer + e);
+      if (kk >= 0) {
+        const uint32_t h = hist[kk];
+        hist[kk] = run;
+        run += h;
+      }
+    }
+  }
+  __syncthreads();
+  uint32_t rank[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const uint32_t i = u * kSortT + tid;
+    rank[u] = i < nlist ? hist[key[u]] + rin[u] : 0u;
+    if (!sort) rank[u] = i < nlist ? i : 0u;
+    if (i < nlist) tbr[rank[u]] = t[u];
+  }
+  __syncthreads();
+  // tile offsets in rank order
+  carry = 0;
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const uint32_t r = u * kSortT + tid;
+    if ((uint32_t)(u * kSortT) < nlist) {  // workgroup-uniform
+      const uint32_t v = r < nlist ? tbr[r] : 0u;
+      const uint32_t pre = block_prefix(v, ws, carry);
+      if (r < nlist) tbr[r] = pre;
+    }
+  }
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < kU; ++u) {
-    if ((uint32_t)(u * kSortT) >= nlist) break;
     const uint32_t i = u * kSortT + tid;
-    const uint32_t cu = i < nlist ? c[u] : 0u;
-    const uint32_t t = i < nlist ? (cu + tq - 1) / tq * ((min(nb[u], blim) + kCB - 1) / kCB) : 0u;
-    uint32_t sc = cu, st = t;  // inclusive wave scans
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t uc = (uint32_t)__shfl_up((int)sc, off);
-      const uint32_t ut = (uint32_t)__shfl_up((int)st, off);
-      if (lane >= off) {
-        sc += uc;
-        st += ut;
-      }
-    }
-    if (lane == 63) {
-      wq[wave] = sc;
-      wt[wave] = st;
-    }
-    __syncthreads();
-    uint32_t pq = carry[0], pt = carry[1];
-    for (int w = 0; w < wave; ++w) {
-      pq += wq[w];
-      pt += wt[w];
-    }
     if (i < nlist) {
-      qoff[i] = pq + sc - cu;
-      toff[i] = pt + st - t;
+      toff[i] = tbr[rank[u]];
+      tcnt[i] = t[u];
     }
-    __syncthreads();
-    if (tid == kSortT - 1) {
-      carry[0] = pq + sc;
-      carry[1] = pt + st;
-    }
-    __syncthreads();
   }
-  if (tid == 0) {
-    qoff[nlist] = carry[0];
-    toff[nlist] = carry[1];
-  }
+  if (tid == 0) toff[nlist] = carry;
 }
 
-__global__ __launch_bounds__(kSortT) void pq16_scatter_kernel(PairStages ps) {
+__global__ __launch_bounds__(kSortT) void pq16_scatter_kernel(PairStages ps, const uint32_t* __restrict__ bo) {
   __shared__ uint32_t hist[kHistMax];
   const PairSet s = stage_set(ps, blockIdx.y);
   uint32_t* __restrict__ cnt = ps.cnt + (uint64_t)blockIdx.y * s.nlist;
@@ -412,11 +492,12 @@ __global__ __launch_bounds__(kSortT) void pq16_scatter_kernel(PairStages ps) {
   uint2* __restrict__ qlist = ps.qlist + blockIdx.y * ps.npr;
   const uint32_t np = (uint32_t)s.np;
   for (uint32_t i = threadIdx.x; i < s.nlist; i += kSortT) hist[i] = 0;
-  // tl[t] = the list of tile t, for the workgroup's share of the lists:
-  // lane j of wave w takes list b + j*16 + w of each run b of 1024, and all
-  // the wave's lanes write each one's tiles (the first run's tile ranges
-  // loaded now, written at the end)
+  // desc[t] = the descriptor of tile t, for the workgroup's share of the
+  // lists: lane j of wave w takes list b + j*16 + w of each run b of 1024,
+  // and all the wave's lanes write each one's tiles (the first run's tile
+  // ranges loaded now, written at the end)
   const uint32_t* __restrict__ toff = ps.toff + (uint64_t)blockIdx.y * (s.nlist + 1);
+  const uint32_t* __restrict__ tcnt = ps.tcnt + (uint64_t)blockIdx.y * s.nlist;
   const uint32_t per = (s.nlist + gridDim.x - 1) / gridDim.x;
   const uint32_t l0 = blockIdx.x * per, l1 = min(s.nlist, l0 + per);
   const uint32_t lane = threadIdx.x & 63;
@@ -424,7 +505,7 @@ __global__ __launch_bounds__(kSortT) void pq16_scatter_kernel(PairStages ps) {
   uint32_t lo0 = 0, hi0 = 0;
   if (l0 + r < l1) {
     lo0 = toff[l0 + r];
-    hi0 = toff[l0 + r + 1];
+    hi0 = lo0 + tcnt[l0 + r];
   }
   __syncthreads();
   uint32_t e0, e1;
@@ -472,14 +553,16 @@ __global__ __launch_bounds__(kSortT) void pq16_scatter_kernel(PairStages ps) {
         qlist[atomicAdd(&hist[p[i]], 1u)] = make_uint2(q, ei - q * np);
       }
   }
-  uint32_t* __restrict__ tl = ps.tl + blockIdx.y * ps.tl1;
+  uint4* __restrict__ desc = ps.desc + blockIdx.y * ps.tl1;
+  const uint32_t tq = blockIdx.y ? ps.tq1 : ps.tq0, cb = blockIdx.y ? ps.cb1 : ps.cb0;
+  const uint32_t blim = blockIdx.y ? ps.blim1 : ps.blim0;
   for (uint32_t b = l0; b < l1; b += kSortT) {
     uint32_t lo = lo0, hi = hi0;
     if (b != l0) {
       lo = hi = 0;
       if (b + r < l1) {
         lo = toff[b + r];
-        hi = toff[b + r + 1];
+        hi = lo + tcnt[b + r];
       }
     }
     for (uint64_t m = __ballot(hi != lo); m; m &= m - 1) {
@@ -487,7 +570,13 @@ __global__ __launch_bounds__(kSortT) void pq16_scatter_kernel(PairStages ps) {
       const uint32_t al = (uint32_t)__builtin_amdgcn_readlane((int)lo, l);
       const uint32_t nl = (uint32_t)__builtin_amdgcn_readlane((int)(hi - lo), l);
       const uint32_t li = (uint32_t)__builtin_amdgcn_readlane((int)(b + r), l);
-      for (uint32_t v = lane; v < nl; v += 64) tl[al + v] = li;
+      const uint32_t qb = qoff[li], qe = qoff[li + 1], b0 = bo[li];
+      const uint32_t nb = min(bo[li + 1] - b0, blim);
+      const uint32_t nqt = (qe - qb + tq - 1) / tq;
+      for (uint32_t v = lane; v < nl; v += 64) {
+        const uint32_t chunk = v / nqt, pt = v - chunk * nqt;
+        desc[al + v] = make_uint4(li | (min(cb, nb - chunk * cb) << 16), qb + pt * tq, qe, b0 + chunk * cb);
+      }
     }
   }
 }
@@ -567,9 +656,13 @@ struct ScreenArgs {
   int xexp;
   const uint32_t* qoff;
   const uint32_t* toff;
-  const uint32_t* tl;  // list of each tile
+  const uint4* desc;  // tile descriptors: list | blocks << 16, first pair, list's pair end, first block
   const uint2* qlist;
   uint32_t blim;  // blocks screened per list at most
+  uint32_t cb;    // blocks per tile (at most kCB)
+  uint32_t* tctr;  // the stage's kXcd tile counters (zero at launch)
+  uint32_t dyn;    // tiles taken from the counters (else a static stride)
+  uint32_t run;    // consecutive tiles per XCD
   // dense mode: every kept value to bufA[q][offA[q][j] + row] (< capA) and
   // the pair's bound to epsA[q][j]
   float* bufA;
@@ -600,7 +693,7 @@ __device__ __forceinline__ float add_up(float a, float b) {
 }
 
 // Tiles: list p owns toff[p] .. toff[p+1]: ceil(pairs_p / 128) pair tiles
-// (fastest) times ceil(min(blocks_p, blim) / kCB) block chunks; workgroups
+// (fastest) times ceil(min(blocks_p, blim) / cb) block chunks; workgroups
 // of four waves stride over the tiles.  In a tile, wave w takes pairs
 // [32w, 32w+32); with fewer than four groups of 32 pairs, each group has
 // split waves, which take every split-th block of the chunk.  Tiles of one
@@ -609,39 +702,70 @@ __device__ __forceinline__ float add_up(float a, float b) {
 // XCD, dispatched together, so the repeat reads hit that XCD's L2 (a
 // bijection on each round of gridDim.x tiles, a multiple of kXcd * kXcdRun).
 struct TileWork {
-  uint32_t p, chunk, q0, qend;
+  uint32_t p, nblk, babs, q0, qend;
   int split, phase;
   bool busy;   // wave-uniform: the wave has pairs
   uint32_t q1;  // a second group of 32 pairs (tiles of 256 pairs)
   bool busy1;  // wave-uniform: the wave has the second group
 };
 
-__device__ __forceinline__ uint32_t tile_slot() {
-  const uint32_t xcd = blockIdx.x % kXcd, y = blockIdx.x / kXcd;
-  return ((y / kXcdRun) * kXcd + xcd) * kXcdRun + y % kXcdRun;
+// The c-th tile of the workgroup's XCD (x = blockIdx.x % kXcd): runs of
+// `run` consecutive tiles per XCD (tiles of one list chunk are consecutive,
+// so their repeat block reads can hit that XCD's L2).
+__device__ __forceinline__ uint32_t xcd_tile(uint32_t c, uint32_t run) {
+  return ((c / run) * kXcd + blockIdx.x % kXcd) * run + c % run;
 }
 
-// TQ pairs per tile: 128, or 256 (then with five to eight groups of 32,
-// wave w also takes group w + 4).
-template <uint32_t TQ>
+// The workgroup's tile loop: body(t) for each tile it takes.  A workgroup's
+// first tile is c = blockIdx.x / kXcd of its XCD.  Static (dyn 0): then
+// every (gridDim.x / kXcd)-th of its XCD's tiles.  Dynamic (dyn 1, a grid of
+// resident workgroups): the next ones come from the XCD's counter, so
+// workgroups that finish early take more; thread 0 claims the next tile
+// while the current one runs (the atomic is older than every load of the
+// tile, so the ring's waits cover it) and one barrier per tile passes it on.
+template <class Body>
+__device__ __forceinline__ void for_tiles(uint32_t ntiles, uint32_t* __restrict__ tctr, uint32_t dyn, uint32_t run,
+                                          uint32_t* s_next, Body&& body) {
+  const uint32_t per = gridDim.x / kXcd;
+  uint32_t c = blockIdx.x / kXcd;
+  for (uint32_t t = xcd_tile(c, run); t < ntiles;) {
+    uint32_t nxt = 0;
+    if (dyn && threadIdx.x == 0) nxt = atomicAdd(&tctr[blockIdx.x % kXcd], 1u);
+    body(t);
+    if (dyn) {
+      if (threadIdx.x == 0) *s_next = nxt;
+      __syncthreads();
+      c = per + *s_next;
+    } else {
+      c += per;
+    }
+    t = xcd_tile(c, run);
+  }
+}
+
+// Tiles of TQ pairs for WV waves: wave w takes pairs [32w, 32w + 32) of the
+// tile (and group w + WV when TQ / 32 > WV, with two groups per wave); with
+// fewer groups than waves, each group has split waves, which take every
+// split-th block of the chunk.  One descriptor load gives the tile.
+template <uint32_t TQ, int WV>
 __device__ __forceinline__ TileWork tile_work(const ScreenArgs& a, uint32_t t, int wave) {
-  static_assert(TQ == 128 || TQ == 256, "tiles of 128 or 256 pairs");
+  static_assert(TQ / 32 == WV || TQ / 32 == 2 * WV, "one or two groups of 32 pairs per wave");
   TileWork w;
-  w.p = a.tl[t];
-  const uint32_t qb = a.qoff[w.p];
-  w.qend = a.qoff[w.p + 1];
-  const uint32_t nqt = (w.qend - qb + TQ - 1) / TQ;
-  const uint32_t local = t - a.toff[w.p];
-  w.chunk = local / nqt;
-  const uint32_t tq0 = qb + (local - w.chunk * nqt) * TQ;
+  const uint4 d = a.desc[t];
+  w.p = d.x & 0xFFFFu;
+  w.nblk = d.x >> 16;
+  w.babs = d.w;
+  w.qend = d.z;
+  const uint32_t tq0 = d.y;
   const uint32_t ngr = min((w.qend - tq0 + 31) / 32, TQ / 32);
-  const uint32_t ng = min(ngr, 4u);
-  w.split = 4 / (ng == 1 ? 1 : (ng == 2 ? 2 : 4));
+  const uint32_t ng = min(ngr, (uint32_t)WV);
+  const uint32_t gp = ng <= 1 ? 1u : ng <= 2 ? 2u : ng <= 4 ? 4u : 8u;  // groups rounded up to a power of 2
+  w.split = WV / (int)min(gp, (uint32_t)WV);
   w.phase = wave % w.split;
   w.q0 = tq0 + (uint32_t)(wave / w.split) * 32;
   w.busy = w.q0 < w.qend;
-  w.q1 = tq0 + (uint32_t)(wave + 4) * 32;
-  w.busy1 = ngr > 4 && w.q1 < w.qend;  // split is 1 then
+  w.q1 = tq0 + (uint32_t)(wave + WV) * 32;
+  w.busy1 = ngr > (uint32_t)WV && w.q1 < w.qend;  // split is 1 then
   return w;
 }
 
@@ -729,41 +853,43 @@ __device__ __forceinline__ void block_norms(const float* __restrict__ sx, int ha
 
 // The LDS ring of one workgroup: NS one-block stages, each the block's KC
 // A-operand chunks and its 32 norms.
-template <int KC, int NS>
+template <int KC, int NS, int WV>
 struct Ring {
   v4u blk[NS][KC * 64];
   float xn[NS][64];
-  v4u dummy[(KC + 3) / 4 * 4 > KC ? 64 : 1];
+  v4u dummy[(KC + WV - 1) / WV * WV > KC ? 64 : 1];
   float dxn[64];
 };
 
-// Streams blocks bb .. be-1 of a list (A operands at A, norms at XN)
-// through the ring by direct global-to-LDS loads; block bb + s lands in
-// stage s % NS.  Every wave issues kUW + 1 loads per block (k-chunks w,
-// w + 4, ...; wave 0 also the block's norms; spare loads re-read into a
-// dummy buffer), so waiting for all but the newest NS - 2 blocks' loads is
-// one immediate count, and a workgroup barrier then frees the previous
-// stage.  Blocks past the end re-read the last block.  step(stage, norms,
-// b) runs on the waves whose pairs take block b.  All waves call this.
-template <int KC, int NS, class Step>
-__device__ __forceinline__ void stream_blocks(Ring<KC, NS>& ring, const v4u* __restrict__ A,
-                                              const float* __restrict__ XN, uint32_t bb, uint32_t be, int wave,
-                                              int lane, const TileWork& w, Step&& step) {
-  constexpr int kUW = (KC + 3) / 4;
-  // s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
-  // at their maxima): all but the newest NS - 2 blocks' loads, and all
-  constexpr int kRingLoads = (NS - 2) * (kUW + 1);
-  constexpr int kWaitRing = (kRingLoads & 15) | ((kRingLoads >> 4) << 14) | 0x70 | 0xF00;
-  constexpr int kWaitAll = 0x70 | 0xF00;
-  const uint32_t nst = be - bb;
-  const char* __restrict__ Ab = reinterpret_cast<const char*>(A);
-  const char* __restrict__ Xb = reinterpret_cast<const char*>(XN);
-  const uint32_t lo16 = (uint32_t)lane * 16, lo4 = (uint32_t)(lane & 31) * 4;
-  auto issue = [&](int buf, uint32_t sblk) {
-    const uint32_t bl = bb + min(sblk, nst - 1);
+// Streams the nst blocks of a tile (A operands at A, norms at XN, both at
+// the tile's first block) through the ring by direct global-to-LDS loads;
+// block s lands in stage s % NS.  Every wave issues kUW + 1 loads per block
+// (k-chunks w, w + WV, ...; wave 0 also the block's norms; spare loads
+// re-read into a dummy buffer), so waiting for all but the newest NS - 2
+// blocks' loads is one immediate count (loads issued after them only make
+// it wait for more), and a workgroup barrier then frees the previous stage.
+// Blocks past the end re-read the last block.  ring_begin issues the first
+// NS - 1 blocks (before the pair operands are loaded, so that their latency
+// overlaps); ring_run streams the rest: step(stage, norms, s) runs on the
+// waves whose pairs take block s.  All waves call both.
+template <int KC, int NS, int WV>
+struct RingStream {
+  static constexpr int kUW = (KC + WV - 1) / WV;
+  Ring<KC, NS, WV>& ring;
+  const char* __restrict__ Ab;
+  const char* __restrict__ Xb;
+  uint32_t nst;
+  int wave;
+  uint32_t lo16, lo4;
+  __device__ __forceinline__ RingStream(Ring<KC, NS, WV>& r, const v4u* A, const float* XN, uint32_t n, int wv,
+                                        int lane)
+      : ring(r), Ab(reinterpret_cast<const char*>(A)), Xb(reinterpret_cast<const char*>(XN)), nst(n), wave(wv),
+        lo16((uint32_t)lane * 16), lo4((uint32_t)(lane & 31) * 4) {}
+  __device__ __forceinline__ void issue(int buf, uint32_t sblk) {
+    const uint32_t bl = min(sblk, nst - 1);
 #pragma unroll
     for (int i = 0; i < kUW; ++i) {
-      const int u = wave + 4 * i;
+      const int u = wave + WV * i;
       if (u < KC)
         lds_load16(Ab + ((uint64_t)bl * KC + u) * 1024 + lo16, &ring.blk[buf][u * 64]);
       else
@@ -773,24 +899,34 @@ __device__ __forceinline__ void stream_blocks(Ring<KC, NS>& ring, const v4u* __r
       lds_load4(Xb + (uint64_t)bl * 128 + lo4, &ring.xn[buf][0]);
     else
       lds_load4(Xb + (uint64_t)bl * 128 + lo4, &ring.dxn[0]);
-  };
+  }
+  __device__ __forceinline__ void begin() {
 #pragma unroll
-  for (int i = 0; i < NS - 1; ++i) issue(i, (uint32_t)i);
-  for (uint32_t s = 0; s < nst;) {
+    for (int i = 0; i < NS - 1; ++i) issue(i, (uint32_t)i);
+  }
+  template <class Step>
+  __device__ __forceinline__ void run(const TileWork& w, Step&& step) {
+    // s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
+    // at their maxima): all but the newest NS - 2 blocks' loads, and all
+    constexpr int kRingLoads = (NS - 2) * (kUW + 1);
+    constexpr int kWaitRing = (kRingLoads & 15) | ((kRingLoads >> 4) << 14) | 0x70 | 0xF00;
+    constexpr int kWaitAll = 0x70 | 0xF00;
+    for (uint32_t s = 0; s < nst;) {
 #pragma unroll
-    for (int buf = 0; buf < NS; ++buf) {
-      if (s < nst) {
-        wait_imm<kWaitRing>();  // this wave's loads of block s have landed
-        bare_barrier();         // everyone's have; stage (s-1) % NS is free
-        issue((buf + NS - 1) % NS, s + NS - 1);
-        if (w.busy && (int)(s % w.split) == w.phase) step(ring.blk[buf], ring.xn[buf], bb + s);
-        ++s;
+      for (int buf = 0; buf < NS; ++buf) {
+        if (s < nst) {
+          wait_imm<kWaitRing>();  // this wave's loads of block s have landed
+          bare_barrier();         // everyone's have; stage (s-1) % NS is free
+          issue((buf + NS - 1) % NS, s + NS - 1);
+          if (w.busy && (int)(s % w.split) == w.phase) step(ring.blk[buf], ring.xn[buf], s);
+          ++s;
+        }
       }
     }
+    wait_imm<kWaitAll>();  // spare loads of the ring's tail
+    bare_barrier();        // the ring is free for the next tile
   }
-  wait_imm<kWaitAll>();  // spare loads of the ring's tail
-  bare_barrier();        // the ring is free for the next tile
-}
+};
 
 // Stage A: every screened value s = fma(-2^(1-er-xexp), acc, |r|^2 + |x^|^2)
 // of the pair's first lists goes to the pair's 32-aligned range of the
@@ -799,15 +935,19 @@ __device__ __forceinline__ void stream_blocks(Ring<KC, NS>& ring, const v4u* __r
 // code 8(r/4) + 4(l/32) + r%4 of the block against pair l%32.
 template <int KC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void pq16_dense_kernel(ScreenArgs a) {
-  __shared__ Ring<KC, kNS> ring;
+  __shared__ Ring<KC, kNS, 4> ring;
   const int lane = threadIdx.x & 63;
   const int wave = wave_index();
   const int col = lane & 31;
   const int half = lane >> 5;
+  __shared__ uint32_t s_next;
   const uint32_t ntiles = a.toff[a.nlist];
-  for (uint32_t t = tile_slot(); t < ntiles; t += gridDim.x) {
-    const TileWork w = tile_work<kTilePairs>(a, t, wave);
+  for_tiles(ntiles, a.tctr, a.dyn, a.run, &s_next, [&](uint32_t t) {
+    const TileWork w = tile_work<kTilePairs, 4>(a, t, wave);
     const uint32_t p = w.p;
+    RingStream<KC, kNS, 4> rs(ring, reinterpret_cast<const v4u*>(a.data) + (uint64_t)w.babs * KC * 64,
+                              a.xnb + (uint64_t)w.babs * 32, w.nblk, wave, lane);
+    rs.begin();
     const bool qv = w.busy && w.q0 + (uint32_t)col < w.qend;
     // lanes past the tile's pairs repeat its last pair, so that every load
     // is in bounds without a branch per load (qv keeps them inactive)
@@ -822,17 +962,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
       const float rnorm = sqrtf(op.rn) * (1.0f + 0x1p-16f);
       const float X = sqrtf(__uint_as_float(a.xmax2[p])) * (1.0f + 0x1p-16f);
       o = a.offA[(uint64_t)q * a.np + j];
-      if (half == 0 && w.chunk == 0) a.epsA[(uint64_t)q * a.np + j] = pq16_eps(rnorm, X, a);
+      if (half == 0 && w.babs == a.bo[p]) a.epsA[(uint64_t)q * a.np + j] = pq16_eps(rnorm, X, a);
     }
     const float cneg = -ldexpf(1.0f, 1 - op.er - a.xexp);
     const float rn = op.rn;
-    const uint32_t b0 = a.bo[p];
-    const uint32_t nb = min(a.bo[p + 1] - b0, a.blim);
-    const uint32_t bb = w.chunk * kCB;
+    const uint32_t bb = w.babs - a.bo[p];  // the tile's first block in the list
     const uint32_t len = a.list_off[p + 1] - a.list_off[p];
-    const v4u* __restrict__ A = reinterpret_cast<const v4u*>(a.data) + (uint64_t)b0 * KC * 64;
-    stream_blocks<KC, kNS>(ring, A, a.xnb + (uint64_t)b0 * 32, bb, min(nb, bb + kCB), wave, lane, w,
-                           [&](const v4u* __restrict__ sa, const float* __restrict__ sx, uint32_t b) {
+    rs.run(w, [&](const v4u* __restrict__ sa, const float* __restrict__ sx, uint32_t sb) {
+      const uint32_t b = bb + sb;
       // every k-chunk read from LDS before the first product: one LDS
       // round trip per block instead of one per pair of products
       v4u av[KC];
@@ -861,7 +998,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
         }
       }
     });
-  }
+  });
 }
 
 // Stage B: every probed list against the query's bound.  Tiles and the
@@ -886,21 +1023,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
 // of 32 pairs per wave (tiles of 128 PG pairs): with PG 2 a list chunk of up
 // to 256 pairs is streamed through the ring once, each block multiplied
 // against both groups' operands.
-template <int KC, int NS, int W, int PG>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W))) void pq16_thresh_kernel(ScreenArgs a) {
+template <int KC, int NS, int W, int PG, int WV>
+__global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(W))) void pq16_thresh_kernel(ScreenArgs a) {
   static_assert(PG == 1 || PG == 2, "one or two groups of pairs per wave");
   constexpr uint32_t kQ = 256;  // queue entries per wave
-  __shared__ Ring<KC, NS> ring;
-  __shared__ uint32_t wq[4][kQ];
-  __shared__ uint32_t wbase[4][PG][64];  // each (group, lane)'s next position while flushing
+  __shared__ Ring<KC, NS, WV> ring;
+  __shared__ uint32_t wq[WV][kQ];
+  __shared__ uint32_t wbase[WV][PG][64];  // each (group, lane)'s next position while flushing
   const int lane = threadIdx.x & 63;
   const int wave = wave_index();
   const int col = lane & 31;
   const int half = lane >> 5;
+  __shared__ uint32_t s_next;
   const uint32_t ntiles = a.toff[a.nlist];
-  for (uint32_t t = tile_slot(); t < ntiles; t += gridDim.x) {
-    const TileWork w = tile_work<kTilePairs * PG>(a, t, wave);
+  for_tiles(ntiles, a.tctr, a.dyn, a.run, &s_next, [&](uint32_t t) {
+    const TileWork w = tile_work<32 * WV * PG, WV>(a, t, wave);
     const uint32_t p = w.p;
+    RingStream<KC, NS, WV> rs(ring, reinterpret_cast<const v4u*>(a.data) + (uint64_t)w.babs * KC * 64,
+                              a.xnb + (uint64_t)w.babs * 32, w.nblk, wave, lane);
+    rs.begin();
     const float X = sqrtf(__uint_as_float(a.xmax2[p])) * (1.0f + 0x1p-16f);
     uint32_t q[PG], j[PG];
     PairOperand<KC> op[PG];
@@ -925,9 +1066,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W))) void p
       }
       cneg[g] = -ldexpf(1.0f, 1 - op[g].er - a.xexp);
     }
-    const uint32_t b0 = a.bo[p];
-    const uint32_t nb = min(a.bo[p + 1] - b0, a.blim);
-    const uint32_t bb = w.chunk * kCB;
+    const uint32_t bb = w.babs - a.bo[p];  // the tile's first block in the list
     const uint32_t start = a.list_off[p];
     const uint32_t len = a.list_off[p + 1] - start;
     uint32_t* __restrict__ myq = wq[wave];
@@ -969,23 +1108,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W))) void p
       qn = 0;
       __builtin_amdgcn_wave_barrier();
     };
-    const v4u* __restrict__ A = reinterpret_cast<const v4u*>(a.data) + (uint64_t)b0 * KC * 64;
-    stream_blocks<KC, NS>(ring, A, a.xnb + (uint64_t)b0 * 32, bb, min(nb, bb + kCB), wave, lane, w,
-                          [&](const v4u* __restrict__ sa, const float* __restrict__ sx, uint32_t b) {
+    rs.run(w, [&](const v4u* __restrict__ sa, const float* __restrict__ sx, uint32_t sb) {
+      const uint32_t b = bb + sb;
+      // the block's k-chunks read once from LDS; with two groups each feeds
+      // both groups' products (two independent chains)
+      v4u av[KC];
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) av[kc] = sa[kc * 64 + lane];
       float xs[16];
       block_norms(sx, half, xs);
       const uint32_t rowb = b * 32 + 4 * half;
+      v16f acc[PG];
+#pragma unroll
+      for (int g = 0; g < PG; ++g) acc[g] = v16f{};
+      if (PG > 1 && w.busy1) {  // wave-uniform
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+          for (int g = 0; g < PG; ++g)
+            acc[g] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, av[kc]), op[g].bq[kc], acc[g], 0,
+                                                            0, 0);
+      } else {
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc)
+          acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, av[kc]), op[0].bq[kc], acc[0], 0, 0,
+                                                          0);
+      }
 #pragma unroll
       for (int g = 0; g < PG; ++g) {
         if (g > 0 && !w.busy1) break;  // wave-uniform
-        v16f acc = {};
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc)
-          acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, sa[kc * 64 + lane]), op[g].bq[kc],
-                                                       acc, 0, 0, 0);
         float s[16];
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr) s[rr] = __builtin_fmaf(cneg[g], acc[rr], xs[rr]);
+        for (int rr = 0; rr < 16; ++rr) s[rr] = __builtin_fmaf(cneg[g], acc[g][rr], xs[rr]);
         const float m0 = fminf(fminf(s[0], s[1]), s[2]);
         const float m1 = fminf(fminf(s[3], s[4]), s[5]);
         const float m2 = fminf(fminf(s[6], s[7]), s[8]);
@@ -1018,13 +1172,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W))) void p
       }
     });
     if (qn > 0) flush();
-  }
+  });
 }
 
 // Stage B's kernel for KC k-chunks
 template <int KC>
 void (*thresh_kernel())(ScreenArgs) {
-  return pq16_thresh_kernel<KC, 3, stage_b_waves(KC), stage_b_groups(KC)>;
+  return pq16_thresh_kernel<KC, stage_b_stages(KC), stage_b_waves(KC), stage_b_groups(KC), stage_b_wgwaves(KC)>;
 }
 
 // One wave per query: dkA = (k-th smallest kept screened value) + the
@@ -1997,6 +2151,8 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   }
   qoff_.reserve(2 * (uint64_t)(nlist + 1));
   toff_.reserve(2 * (uint64_t)(nlist + 1));
+  tcnt_.reserve(2ull * nlist);
+  tctr_.reserve(2 * kXcd);
   qlist_.reserve(2 * std::max<uint64_t>(npr, 1));
   jlim_.reserve(nq);
   offA_.reserve(npr);
@@ -2024,11 +2180,12 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
       (uint32_t)std::min<uint64_t>(std::max<uint64_t>(cdiv(npr, (uint64_t)kSortT * kSortB), 1), kSortWG);
   const uint64_t chunk = cdiv(npr, G);
   // tiles of a stage: at most (pairs / 128 + lists) pair tiles per chunk
-  auto tile_bound = [&](uint32_t blim) {
-    return (cdiv(npr, kTilePairs) + nlist) * cdiv(std::min<uint64_t>(L.max_blocks, blim), kCB);
+  const uint32_t cbB = kCB;
+  auto tile_bound = [&](uint32_t blim, uint32_t cb) {
+    return (cdiv(npr, kTilePairs) + nlist) * cdiv(std::min<uint64_t>(L.max_blocks, blim), cb);
   };
-  const uint64_t tbA = tile_bound(capA / 32), tbB = tile_bound(0xFFFFFFFFu);
-  tl_.reserve(std::max<uint64_t>(tbA + tbB, 1));
+  const uint64_t tbA = tile_bound(capA / 32, kCB), tbB = tile_bound(0xFFFFFFFFu, cbB);
+  desc_.reserve(std::max<uint64_t>(tbA + tbB, 1));
   // both stages' pairs grouped by list: 0 the first lists, 1 every probe
   PairStages pst{};
   pst.s0 = PairSet{a.probes, nq, np, jlim_.p, nlist, chunk};
@@ -2036,12 +2193,25 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   pst.blim0 = capA / 32;
   pst.blim1 = 0xFFFFFFFFu;
   pst.tq0 = kTilePairs;
-  pst.tq1 = kTilePairs * stage_b_groups(L.KC);
+  const int wvB = stage_b_wgwaves(L.KC);
+  // Large indexes (tens of tiles per resident workgroup) take their tiles
+  // from per-XCD counters in descending order of size, so that the last
+  // tiles are short.  Measured at 10M x 96 codes (nlist 4096, nprobe 64):
+  // stage B 1.56-1.60 ms against 1.81 with the static stride; at 1M x 128
+  // (nlist 1024, nprobe 16; ~3 tiles per workgroup) the static stride over
+  // tiles in list order was faster (0.175 against 0.185 ms).
+  const bool dyn = L.nblocks >= 512ull * (uint64_t)ncu_;
+  pst.sort = dyn ? 1u : 0u;
+  pst.tq1 = 32 * wvB * stage_b_groups(L.KC);
+  pst.cb0 = kCB;
+  pst.cb1 = cbB;
   pst.cnt = cnt_.p;
   pst.qoff = qoff_.p;
   pst.toff = toff_.p;
+  pst.tcnt = tcnt_.p;
+  pst.tctr = tctr_.p;
   pst.qlist = qlist_.p;
-  pst.tl = tl_.p;
+  pst.desc = desc_.p;
   pst.npr = std::max<uint64_t>(npr, 1);
   pst.tl1 = tbA;
   cnt_clean_ = false;  // until the scatter has run
@@ -2049,7 +2219,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   FDB_HIP(hipGetLastError());
   hipLaunchKernelGGL(pq16_offsets_kernel, dim3(2), dim3(kSortT), 0, s, pst, L.bo.p);
   FDB_HIP(hipGetLastError());
-  hipLaunchKernelGGL(pq16_scatter_kernel, dim3(G, 2), dim3(kSortT), 0, s, pst);
+  hipLaunchKernelGGL(pq16_scatter_kernel, dim3(G, 2), dim3(kSortT), 0, s, pst, L.bo.p);
   FDB_HIP(hipGetLastError());
   cnt_clean_ = true;
 
@@ -2090,16 +2260,31 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
 #undef FDB_KC
   }
   if (!dense) throw Error(FDB_ERR_HIP, "no screening kernel for this dimension");
-  // workgroups stride over the tiles; a multiple of kXcd * kXcdRun
-  const unsigned grid = (unsigned)std::max<uint64_t>(cdiv(8 * (uint64_t)ncu_, kXcd * kXcdRun), 1) * kXcd * kXcdRun;
+  // Dynamic tiles: one resident round of workgroups (a multiple of kXcd),
+  // which then take tiles from their XCD's counter.  Static: eight
+  // workgroups per CU striding over the tiles (a multiple of kXcd * run).
+  auto grid_of = [&](void (*kern)(ScreenArgs), int threads) {
+    if (!dyn) return (unsigned)(std::max<uint64_t>(cdiv(8 * (uint64_t)ncu_, kXcd * kXcdRun), 1) * kXcd * kXcdRun);
+    for (const auto& g : grids_)
+      if (g.first == reinterpret_cast<const void*>(kern)) return g.second;
+    int per = 0;
+    FDB_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kern, threads, 0));
+    const unsigned g = (unsigned)(std::max<uint64_t>(cdiv((uint64_t)std::max(per, 1) * ncu_, kXcd), 1) * kXcd);
+    grids_.emplace_back(reinterpret_cast<const void*>(kern), g);
+    return g;
+  };
 
   // 1. the first lists of each query, every screened value kept; d_k bound
   sa.qoff = qoff_.p;
   sa.toff = toff_.p;
-  sa.tl = tl_.p;
+  sa.desc = desc_.p;
   sa.qlist = qlist_.p;
   sa.blim = capA / 32;
-  hipLaunchKernelGGL(dense, dim3(grid), dim3(256), 0, s, sa);
+  sa.cb = kCB;
+  sa.tctr = tctr_.p;
+  sa.dyn = dyn ? 1u : 0u;
+  sa.run = dyn ? kXcdRunDyn : kXcdRun;
+  hipLaunchKernelGGL(dense, dim3(grid_of(dense, 256)), dim3(256), 0, s, sa);
   FDB_HIP(hipGetLastError());
   const int R = list_regs(a.k);
   switch (R) {
@@ -2118,11 +2303,14 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   // 2. every probed list against the bound
   sa.qoff = qoff_.p + (nlist + 1);
   sa.toff = toff_.p + (nlist + 1);
-  sa.tl = tl_.p + tbA;
+  sa.desc = desc_.p + tbA;
   sa.qlist = qlist_.p + std::max<uint64_t>(npr, 1);
   sa.blim = 0xFFFFFFFFu;
+  sa.cb = cbB;
+  sa.tctr = tctr_.p + kXcd;
+  const unsigned gridB = grid_of(thresh, 64 * wvB);
   if (timing_) FDB_HIP(hipEventRecord(tev_[0], s));
-  hipLaunchKernelGGL(thresh, dim3(grid), dim3(256), 0, s, sa);
+  hipLaunchKernelGGL(thresh, dim3(gridB), dim3(64 * wvB), 0, s, sa);
   FDB_HIP(hipGetLastError());
   if (timing_) {
     FDB_HIP(hipEventRecord(tev_[1], s));

@@ -25,6 +25,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <utility>
 #include <vector>
 
 #include "fdb_host.hpp"
@@ -116,14 +117,16 @@ class Pq16Searcher {
  private:
   void flush_stats(hipStream_t s);
   int ncu_ = 0;
+  std::vector<std::pair<const void*, unsigned>> grids_;  // screening kernel -> its resident grid
   bool clear_ = true;        // the next count replaces stat_
   uint64_t pending_nq_ = 0;  // queries of the last slice, not yet counted
   bool timing_ = false;
   float screen_ms_ = 0.0f;
   hipEvent_t tev_[2] = {nullptr, nullptr};
   bool cnt_clean_ = false;  // cnt_ holds zeros
-  DevBuf<uint32_t> cnt_, qoff_, toff_, tl_, jlim_, offA_, nA_, nreal_, ccnt_, stat_, nheavy_, order_;
+  DevBuf<uint32_t> cnt_, qoff_, toff_, tcnt_, tctr_, jlim_, offA_, nA_, nreal_, ccnt_, stat_, nheavy_, order_;
   DevBuf<uint2> qlist_, cand_, heavy_, multi_;
+  DevBuf<uint4> desc_;  // tile descriptors of both stages
   DevBuf<uint32_t> part_k_;
   DevBuf<float> epsA_, bufA_, dkA_, part_d_;
   DevBuf<int> force_, flags_;
