@@ -197,10 +197,11 @@ def w_name(w):
 
 def thresh_kernel_name(dim):
     """The threshold screening kernel (stage B) an IVF-PQ shape runs:
-    <k-chunks, ring stages, waves per SIMD, groups of 32 pairs per wave>."""
+    <k-chunks, ring stages, waves per SIMD, groups of 32 pairs per wave,
+    waves per workgroup>."""
     kc = (dim + 15) // 16
     waves = 3 if kc <= 6 else (4 if kc <= 8 else (3 if kc <= 12 else 2))
-    return f"pq16_thresh_kernel<{kc}, 3, {waves}, {2 if kc <= 6 else 1}>"
+    return f"pq16_thresh_kernel<{kc}, 3, {waves}, {2 if kc <= 6 else 1}, 4>"
 
 
 def latency_leg(index, oracle, queries, k, reps):
