@@ -1292,8 +1292,7 @@ struct RescoreArgs16 {
   const float* codebooks;
   const float* cb4;  // codebooks with codewords padded to a multiple of 4 floats
   int nlist;
-  int cached;        // residuals of every probe in LDS (the parts of heavy queries)
-  int cached_light;  // the same for each wave's query in the one-wave rescoring
+  int cached;        // residuals of every probe in LDS
   const uint8_t* codes;
   const uint64_t* ids;
   const uint32_t* ccnt;
@@ -1670,15 +1669,10 @@ __global__ __launch_bounds__(kT) void pq16_classify_kernel(const uint32_t* __res
 }
 
 // One wave per query (have: the wave has one): a query of at most kLight
-// candidate entries scored and selected as in pq16_rescore_heavy.  With
-// cached_light, the wave first writes its query's residuals r_j = q - c_(probe
-// j) to its share of the dynamic LDS ([np][D] per wave), so that a candidate
-// reads its residual from LDS instead of gathering its centroid row (the same
-// fp32 differences, so the same entries).  Every wave of the workgroup calls
-// it (one workgroup barrier).
+// candidate entries scored and selected as in pq16_rescore_heavy.  Every wave
+// of the workgroup calls it (one workgroup barrier).
 template <int R, int DS, int MM>
 __device__ __forceinline__ void pq16_rescore_light(const RescoreArgs16& a, uint64_t q, bool have) {
-  extern __shared__ float rcl[];  // [kT / 64][np][D] when cached_light
   __shared__ float qsm[kT / 64][256];
   __shared__ uint2 queue[kT / 64][64];
   __shared__ uint2 xent[kT / 64][64];
@@ -1687,18 +1681,8 @@ __device__ __forceinline__ void pq16_rescore_light(const RescoreArgs16& a, uint6
   const int wave = wave_index();
   const uint32_t cnt = have ? a.ccnt[q] : 0u;
   const int D = a.D;
-  const bool cached = DS >= 0 && a.cached_light;
-  float* __restrict__ rw = rcl + (uint64_t)wave * a.np * D;
-  if (have) {
+  if (have)
     for (int d = lane; d < D; d += 64) qsm[wave][d] = a.queries[q * D + d];
-    if (cached)
-      for (int e = lane; e < a.np * D; e += 64) {
-        const int j = e / D;
-        const int d = e - j * D;
-        const int32_t p = a.probes[q * a.np + j];
-        rw[e] = (p >= 0 && p < a.nlist) ? a.queries[q * D + d] - a.centroids[(uint64_t)p * D + d] : 0.0f;
-      }
-  }
   __syncthreads();
   if (!have) return;
   const float* __restrict__ qs = qsm[wave];
@@ -1720,18 +1704,11 @@ __device__ __forceinline__ void pq16_rescore_light(const RescoreArgs16& a, uint6
           d = row_dist(a, qs, key);
         } else {
           const CodeRow<MM> code(a.codes + (uint64_t)key * M);
-          if (cached) {
-            const float* __restrict__ rr = rw + jj * D;
-            d = adc_order(M, a.order, [&](int m) {
-              return entry_cached<DS>(rr + m * dsub, a.cb4 + ((uint64_t)m * 256 + code[m]) * ds4, dsub);
-            });
-          } else {
-            const float* __restrict__ cen = a.centroids + (uint64_t)a.probes[q * a.np + jj] * D;
-            d = adc_order(M, a.order, [&](int m) {
-              return entry_direct<DS>(qs + m * dsub, cen + m * dsub, a.cb4 + ((uint64_t)m * 256 + code[m]) * ds4,
-                                      dsub);
-            });
-          }
+          const float* __restrict__ cen = a.centroids + (uint64_t)a.probes[q * a.np + jj] * D;
+          d = adc_order(M, a.order, [&](int m) {
+            return entry_direct<DS>(qs + m * dsub, cen + m * dsub, a.cb4 + ((uint64_t)m * 256 + code[m]) * ds4,
+                                    dsub);
+          });
         }
       }
       tk.offer_queued(d, key, has, queue[wave], qn);
@@ -2384,10 +2361,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   r.cb4 = L.cb4.p;
   r.nlist = (int)nlist;
   r.cached = !a.rows && (uint64_t)np * L.D * sizeof(float) <= 32 * 1024;
-  // one-wave queries: every wave's residuals, when they fit 32 KiB
-  r.cached_light = !a.rows && (uint64_t)(kT / 64) * np * L.D * sizeof(float) <= 32 * 1024;
-  const size_t lds = std::max(sizeof(float) * ((size_t)L.D + (r.cached ? (size_t)np * L.D : 0)),
-                              r.cached_light ? sizeof(float) * (kT / 64) * (size_t)np * L.D : (size_t)0);
+  const size_t lds = sizeof(float) * ((size_t)L.D + (r.cached ? (size_t)np * L.D : 0));
   const int ds = (L.dsub == 3 || L.dsub == 4 || L.dsub == 8) ? L.dsub : 0;
   void (*rk)(RescoreArgs16, uint64_t, uint32_t) = nullptr;
 #define FDB_RS(n)                                                                       \
