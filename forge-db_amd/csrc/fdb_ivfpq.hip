@@ -650,7 +650,7 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
   const int smode = search_mode_.load(std::memory_order_relaxed);
   const uint64_t scanned = host_.nlist ? host_.ids.size() * np / host_.nlist : 0;
   bool screen = smode != 1 && !rerank && !trunc && live == nullptr && a.lut_mode == 0 && np >= 2 &&
-                host_.M * host_.dsub <= 256 && (smode == 2 || nq * scanned >= kPq16MinWork);
+                host_.M * host_.dsub <= 256 && (smode >= 2 || nq * scanned >= kPq16MinWork);
   if (screen && pq16_dirty_) {
     pq16_.build(codebooks_.p, codes_.p, off_.p, host_.offsets, host_.nlist, (int)host_.M, (int)host_.dsub, s);
     pq16_dirty_ = false;
@@ -665,6 +665,7 @@ void IvfPqIndex::run(const float* d_qs, uint64_t nq, uint32_t k, uint32_t np, in
     for (uint64_t q0 = 0; q0 < nq; q0 += sl) {
       const uint64_t m = std::min<uint64_t>(sl, nq - q0);
       Pq16SearchArgs sa{};
+      sa.tiles = smode == 3 ? 1 : -1;
       sa.queries = d_qs + q0 * D;
       sa.nq = m;
       sa.probes = probes_.p + q0 * np;

@@ -46,9 +46,10 @@ class IvfPqIndex {
 
   // 0 = automatic (fp16 screening with exact rescoring for large plain
   // batches, fdb_ivfpq16.hpp), 1 = exact scan only, 2 = screening wherever
-  // it applies; the results are the same
+  // it applies, 3 = as 2 with size-sorted tiles from per-XCD counters
+  // whatever the index size; the results are the same
   bool set_search_mode(int m) {
-    if (m < 0 || m > 2) return false;
+    if (m < 0 || m > 3) return false;
     search_mode_.store(m, std::memory_order_relaxed);
     return true;
   }

@@ -2200,7 +2200,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   // stage B 1.56-1.60 ms against 1.81 with the static stride; at 1M x 128
   // (nlist 1024, nprobe 16; ~3 tiles per workgroup) the static stride over
   // tiles in list order was faster (0.175 against 0.185 ms).
-  const bool dyn = L.nblocks >= 512ull * (uint64_t)ncu_;
+  const bool dyn = a.tiles >= 0 ? a.tiles == 1 : L.nblocks >= 512ull * (uint64_t)ncu_;
   pst.sort = dyn ? 1u : 0u;
   pst.tq1 = 32 * wvB * stage_b_groups(L.KC);
   pst.cb0 = kCB;

@@ -78,6 +78,10 @@ struct Pq16SearchArgs {
   // Euclidean metric); codebooks and codes are unused.
   const float* rows = nullptr;
   int sqrt_out = 0;
+  // Work schedule: -1 by index size (tiles sorted by size and taken from
+  // per-XCD counters when the index has at least 512 blocks per CU), 0 a
+  // static stride over tiles in list order, 1 sorted tiles from counters.
+  int tiles = -1;
   uint64_t* out_ids;
   float* out_d;
   uint32_t* out_counts;

@@ -30,7 +30,7 @@ LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libforgedb_hip.so")
 
 __all__ = [
     "DistanceMetric", "ForgeDbError", "IVFPQIndex", "BruteForceIndex", "IVFIndex",
-    "IVFPQ_AUTO", "IVFPQ_EXACT", "IVFPQ_SCREEN",
+    "IVFPQ_AUTO", "IVFPQ_EXACT", "IVFPQ_SCREEN", "IVFPQ_SCREEN_SORTED",
     "load_library", "LIB_PATH",
     "EXPORTED_SYMBOLS",
 ]
@@ -64,7 +64,7 @@ EXPORTED_SYMBOLS = (
 LUT_EXACT, LUT_FAST = 0, 1
 BF_AUTO, BF_EXACT, BF_SCREEN, BF_SCREEN_F32 = 0, 1, 2, 3
 IVF_AUTO, IVF_EXACT, IVF_SCREEN_LISTS = 0, 1, 2
-IVFPQ_AUTO, IVFPQ_EXACT, IVFPQ_SCREEN = 0, 1, 2
+IVFPQ_AUTO, IVFPQ_EXACT, IVFPQ_SCREEN, IVFPQ_SCREEN_SORTED = 0, 1, 2, 3
 COARSE_AUTO, COARSE_EXACT, COARSE_SCREEN = 0, 1, 2
 
 
@@ -309,7 +309,9 @@ class IVFPQIndex:
     def set_search_mode(self, mode: int) -> None:
         """IVFPQ_AUTO (default: half-precision screening with exact rescoring
         for large plain batches), IVFPQ_EXACT (table scan only) or
-        IVFPQ_SCREEN (screening wherever it applies); same results."""
+        IVFPQ_SCREEN (screening wherever it applies) or IVFPQ_SCREEN_SORTED
+        (screening with the size-sorted tile schedule of large indexes,
+        whatever the size); same results."""
         _check(self._lib, self._lib.fdb_ivfpq_set_search_mode(self._h, int(mode)))
 
     def last_screen_stats(self, stream: int = 0):

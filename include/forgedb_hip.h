@@ -151,13 +151,16 @@ FDB_API fdb_status fdb_ivfpq_set_coarse_mode(fdb_ivfpq* index, uint32_t mode);
  *     or residuals out of half-precision range, are rescanned exactly.
  *   FDB_IVFPQ_EXACT: the table scan for every query.
  *   FDB_IVFPQ_SCREEN: screening wherever it applies, whatever the size.
+ *   FDB_IVFPQ_SCREEN_SORTED: as FDB_IVFPQ_SCREEN, with the work schedule
+ *     that large indexes take by themselves (tiles ordered by size, taken
+ *     from per-XCD counters) whatever the index size; the same results.
  * fdb_ivfpq_last_screen_stats reports, for the last batch, the queries
  * rescanned exactly and the candidates rescored (waits for hip_stream; NULL
  * = the handle's stream); fdb_ivfpq_last_search_path 0 (table scan) or 2
  * (screening).  The decoded codes take 2 * roundup(dim, 16) bytes per code
  * of device memory, built at the first screened search after the lists
  * change. */
-enum { FDB_IVFPQ_AUTO = 0, FDB_IVFPQ_EXACT = 1, FDB_IVFPQ_SCREEN = 2 };
+enum { FDB_IVFPQ_AUTO = 0, FDB_IVFPQ_EXACT = 1, FDB_IVFPQ_SCREEN = 2, FDB_IVFPQ_SCREEN_SORTED = 3 };
 FDB_API fdb_status fdb_ivfpq_set_search_mode(fdb_ivfpq* index, uint32_t mode);
 FDB_API fdb_status fdb_ivfpq_last_screen_stats(fdb_ivfpq* index, void* hip_stream, uint64_t* fallbacks,
                                                uint64_t* candidates);

@@ -9,7 +9,8 @@ import pytest
 
 import refcpu
 
-from forgedb import IVFPQ_AUTO, IVFPQ_EXACT, IVFPQ_SCREEN, DistanceMetric, ForgeDbError, IVFPQIndex, datagen
+from forgedb import (IVFPQ_AUTO, IVFPQ_EXACT, IVFPQ_SCREEN, IVFPQ_SCREEN_SORTED, DistanceMetric, ForgeDbError,
+                     IVFPQIndex, datagen)
 
 pytestmark = pytest.mark.gpu
 
@@ -31,8 +32,8 @@ def same(a, b, label):
         assert np.all(gi[q, c:] == NO_ID)
 
 
-def screened(gx, queries, k, label):
-    gx.set_search_mode(IVFPQ_SCREEN)
+def screened(gx, queries, k, label, mode=IVFPQ_SCREEN):
+    gx.set_search_mode(mode)
     out = gx.batch_search_arrays(queries, k)
     assert gx.last_search_path() == 2, label
     fb, cand = gx.last_screen_stats()
@@ -55,6 +56,51 @@ def test_screen_parity(small_ivfpq, nprobe, k):
     gx.set_search_mode(IVFPQ_EXACT)
     same(got, gx.batch_search_arrays(q, k), f"screen np{nprobe} k{k} vs table scan")
     assert gx.last_search_path() == 0
+
+
+@pytest.mark.parametrize("nprobe,k", [(2, 10), (16, 10), (16, 100), (64, 1000)])
+def test_screen_sorted_schedule(small_ivfpq, nprobe, k):
+    """The work schedule of large indexes (tiles ordered by size, taken from
+    per-XCD counters by a grid of resident workgroups) on the small index:
+    the same results as the table scan and the oracle."""
+    print(f"screened batch, sorted tiles, nprobe={nprobe} k={k} (20k x 128, nlist 64, M 16)", flush=True)
+    gx = gpu_index(small_ivfpq["art"])
+    ox = small_ivfpq["oracle"]
+    gx.set_nprobe(nprobe)
+    ox.set_nprobe(nprobe)
+    q = small_ivfpq["queries"]
+    got, _ = screened(gx, q, k, f"sorted np{nprobe} k{k}", IVFPQ_SCREEN_SORTED)
+    same(got, ox.batch_search(q, k), f"sorted np{nprobe} k{k} vs oracle")
+    gx.set_search_mode(IVFPQ_SCREEN)
+    same(got, gx.batch_search_arrays(q, k), f"sorted np{nprobe} k{k} vs static tiles")
+
+
+@pytest.mark.parametrize("dim,M", [(96, 32), (128, 16), (20, 5)])
+def test_screen_sorted_skewed_lists(dim, M):
+    """Sorted tiles on skewed lists: most vectors in one list (several
+    64-block chunks and pair tiles), many lists holding a few codes or none,
+    so the size keys span their whole range and fewer tiles than workgroups
+    exist for some stages."""
+    print(f"sorted tiles, skewed lists dim={dim} M={M}", flush=True)
+    rng = np.random.default_rng(dim + M)
+    nlist = 48
+    centres = rng.normal(0.0, 6.0, size=(nlist, dim)).astype(np.float32)
+    # 70% of the points around centre 0, the rest spread thinly over a few
+    # centres; lists 40.. get nothing beyond what k-means gives them
+    n = 9000
+    pick = np.where(rng.random(n) < 0.7, 0, rng.integers(1, 12, size=n))
+    base = (centres[pick] + rng.normal(0.0, 1.0, size=(n, dim))).astype(np.float32)
+    ox = refcpu.IvfPq.build(base, nlist=nlist, M=M, seed=2)
+    gx = gpu_index(ox.export())
+    q = (centres[np.where(rng.random(300) < 0.8, 0, rng.integers(0, nlist, size=300))]
+         + rng.normal(0.0, 1.0, size=(300, dim))).astype(np.float32)
+    for nprobe, k in ((2, 10), (8, 100), (nlist, 7)):
+        gx.set_nprobe(nprobe)
+        ox.set_nprobe(nprobe)
+        got, _ = screened(gx, q, k, f"skewed d{dim} np{nprobe}", IVFPQ_SCREEN_SORTED)
+        same(got, ox.batch_search(q, k), f"skewed sorted d{dim} M{M} np{nprobe} k{k} vs oracle")
+        gx.set_search_mode(IVFPQ_EXACT)
+        same(got, gx.batch_search_arrays(q, k), f"skewed sorted d{dim} M{M} np{nprobe} k{k} vs table scan")
 
 
 @pytest.mark.parametrize("dim,M,nlist", [(96, 32, 32), (128, 8, 16), (16, 4, 8), (48, 12, 12), (20, 5, 6),
