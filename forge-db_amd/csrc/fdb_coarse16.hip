@@ -5,8 +5,11 @@
 //                      values compare above every finite one)
 // c16_blocks_kernel    fp16 A-operand blocks of 32 centroids and their
 //                      norms, laid out per half-lane
-// coarse16_kernel      4 waves per 32 queries: the bound pass, the
-//                      candidate pass, exact rescoring and selection
+// coarse16_kernel      4 waves per 32 queries: the bound pass and the
+//                      candidate pass; each query's candidates to a list
+// coarse16_rescore_kernel
+//                      a wave per query: exact rescoring of its candidates
+//                      and selection (many more workgroups than tiles)
 #include "fdb_coarse16.hpp"
 
 #include <algorithm>
@@ -107,6 +110,8 @@ struct C16Args {
   int32_t* probes;
   float* dists;
   int* flags;
+  uint32_t* cand;  // [nq][cap] screened candidates (centroid indices)
+  uint32_t* ncand; // [nq] their count (0 for a flagged query)
 };
 
 // Sorted insertion of v into the m smallest kept in t[0..M) ascending.
@@ -169,7 +174,7 @@ __global__ __launch_bounds__(kCT) __attribute__((amdgpu_waves_per_eu(2))) void c
   __shared__ float s_qn[32], s_T[32];
   __shared__ int s_eq[32];
   __shared__ uint32_t s_cnt[32], s_pre[33];
-  __shared__ uint8_t s_pair[32 * kMaxCap];  // query of each rescored pair
+  __shared__ uint8_t s_pair[M == 16 ? 1 : 32 * kMaxCap];  // query of each rescored pair (in-kernel rescoring)
   float* __restrict__ qs = reinterpret_cast<float*>(lds);
   uint2* __restrict__ cand = reinterpret_cast<uint2*>(lds + 32 * LQS);
   float* __restrict__ mins = reinterpret_cast<float*>(cand);
@@ -409,121 +414,254 @@ __global__ __launch_bounds__(kCT) __attribute__((amdgpu_waves_per_eu(2))) void c
   });
   __syncthreads();
 
-  // a query is served here when it was screened and its candidates fit;
-  // the others are flagged for the exact kernel
-  if (tid < 32) {
-    const uint32_t n = s_cnt[tid];
-    const bool ok = tid < nqt && s_T[tid] != -f_inf() && n >= (uint32_t)a.np && n <= (uint32_t)cap;
-    if (tid < nqt) a.flags[q0 + tid] = ok ? 0 : 1;
-    const uint32_t own = ok ? n : 0u;
-    uint32_t inc = own;
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) {
-      const uint32_t v = (uint32_t)__shfl_up((int)inc, off);
-      if (lane >= off) inc += v;
+  if constexpr (M == 16) {
+    // np > 32: the candidates go to coarse16_rescore_kernel (many more
+    // workgroups than tiles for the larger rescoring and selection)
+    // a query is served when it was screened and its candidates fit; the
+    // others are flagged for the exact kernel.  The served queries' candidate
+    // lists go to the rescoring kernel.
+    {
+      constexpr int TPQ = kCT / 32;
+      const int qi = tid / TPQ, sub = tid % TPQ;
+      const uint32_t n = s_cnt[qi];
+      const bool ok = qi < nqt && s_T[qi] != -f_inf() && n >= (uint32_t)a.np && n <= (uint32_t)cap;
+      if (qi < nqt) {
+        if (sub == 0) {
+          a.flags[q0 + qi] = ok ? 0 : 1;
+          a.ncand[q0 + qi] = ok ? n : 0u;
+        }
+        if (ok)
+          for (uint32_t j = (uint32_t)sub; j < n; j += TPQ) a.cand[(q0 + qi) * (uint64_t)cap + j] = cand[qi * cap + j].x;
+      }
     }
-    s_pre[tid + 1] = inc;
-    if (tid == 0) s_pre[0] = 0;
-    if (!ok) s_cnt[tid] = 0;
-    // slots up to the next multiple of 16 hold a key above every candidate
-    // (distance bits 0xFFFFFFFF are a NaN, which no distance is)
-    if (ok)
-      for (uint32_t j = n; j < (n + 15) / 16 * 16; ++j) cand[tid * cap + j] = make_uint2(0xFFFFFFFFu, 0xFFFFFFFFu);
-  }
-  __syncthreads();
-  {
-    constexpr int TPQ = kCT / 32;
-    const int qi = tid / TPQ;
-    const uint32_t b0 = s_pre[qi], n = s_pre[qi + 1] - b0;
-    for (uint32_t j = (uint32_t)(tid % TPQ); j < n; j += TPQ) s_pair[b0 + j] = (uint8_t)qi;
-  }
-  __syncthreads();
+    return;
+  } else {
+    // a query is served here when it was screened and its candidates fit;
+    // the others are flagged for the exact kernel
+    if (tid < 32) {
+      const uint32_t n = s_cnt[tid];
+      const bool ok = tid < nqt && s_T[tid] != -f_inf() && n >= (uint32_t)a.np && n <= (uint32_t)cap;
+      if (tid < nqt) a.flags[q0 + tid] = ok ? 0 : 1;
+      const uint32_t own = ok ? n : 0u;
+      uint32_t inc = own;
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) {
+        const uint32_t v = (uint32_t)__shfl_up((int)inc, off);
+        if (lane >= off) inc += v;
+      }
+      s_pre[tid + 1] = inc;
+      if (tid == 0) s_pre[0] = 0;
+      if (!ok) s_cnt[tid] = 0;
+      // slots up to the next multiple of 16 hold a key above every candidate
+      // (distance bits 0xFFFFFFFF are a NaN, which no distance is)
+      if (ok)
+        for (uint32_t j = n; j < (n + 15) / 16 * 16; ++j) cand[tid * cap + j] = make_uint2(0xFFFFFFFFu, 0xFFFFFFFFu);
+    }
+    __syncthreads();
+    {
+      constexpr int TPQ = kCT / 32;
+      const int qi = tid / TPQ;
+      const uint32_t b0 = s_pre[qi], n = s_pre[qi + 1] - b0;
+      for (uint32_t j = (uint32_t)(tid % TPQ); j < n; j += TPQ) s_pair[b0 + j] = (uint8_t)qi;
+    }
+    __syncthreads();
 
-  // rescoring: the exact distance of every (query, candidate) pair in the
-  // reference's order, two threads a pair: thread h holds the FMA lanes
-  // 4h .. 4h+3 over the 8-float chunks; lanes summed 0..7 in order, then
-  // the scalar tail
-  const uint32_t total = __builtin_amdgcn_readfirstlane(s_pre[32]);
-  const int d8 = a.dim / 8;
-  const int h = tid & 1;
-  for (uint32_t i = (uint32_t)(tid >> 1); i < total; i += kCT / 2) {
-    const int qi = s_pair[i];
-    const uint32_t slot = i - s_pre[qi];
-    const float* __restrict__ cr = a.centroids + (uint64_t)cand[qi * cap + slot].x * a.dim;
-    const float* __restrict__ qr = qs + qi * LQS;
-    float l0 = 0.0f, l1 = 0.0f, l2 = 0.0f, l3 = 0.0f;
-    // the row's chunks loaded 16 at a time (d8 <= 2 KC), then the lanes
-    constexpr int G = 2 * KC < 16 ? 2 * KC : 16;
+    // rescoring: the exact distance of every (query, candidate) pair in the
+    // reference's order, two threads a pair: thread h holds the FMA lanes
+    // 4h .. 4h+3 over the 8-float chunks; lanes summed 0..7 in order, then
+    // the scalar tail
+    const uint32_t total = __builtin_amdgcn_readfirstlane(s_pre[32]);
+    const int d8 = a.dim / 8;
+    const int h = tid & 1;
+    for (uint32_t i = (uint32_t)(tid >> 1); i < total; i += kCT / 2) {
+      const int qi = s_pair[i];
+      const uint32_t slot = i - s_pre[qi];
+      const float* __restrict__ cr = a.centroids + (uint64_t)cand[qi * cap + slot].x * a.dim;
+      const float* __restrict__ qr = qs + qi * LQS;
+      float l0 = 0.0f, l1 = 0.0f, l2 = 0.0f, l3 = 0.0f;
+      // the row's chunks loaded 16 at a time (d8 <= 2 KC), then the lanes
+      constexpr int G = 2 * KC < 16 ? 2 * KC : 16;
 #pragma unroll
-    for (int j0 = 0; j0 < 2 * KC; j0 += G) {
-      v4f x[G];
+      for (int j0 = 0; j0 < 2 * KC; j0 += G) {
+        v4f x[G];
 #pragma unroll
-      for (int j = 0; j < G; ++j)
-        if (j0 + j < d8) {
-          const float* __restrict__ c8 = cr + 8 * (j0 + j) + 4 * h;
-          if (a.vec) {
-            x[j] = *reinterpret_cast<const v4f*>(c8);
-          } else {
-            x[j].x = c8[0];
-            x[j].y = c8[1];
-            x[j].z = c8[2];
-            x[j].w = c8[3];
+        for (int j = 0; j < G; ++j)
+          if (j0 + j < d8) {
+            const float* __restrict__ c8 = cr + 8 * (j0 + j) + 4 * h;
+            if (a.vec) {
+              x[j] = *reinterpret_cast<const v4f*>(c8);
+            } else {
+              x[j].x = c8[0];
+              x[j].y = c8[1];
+              x[j].z = c8[2];
+              x[j].w = c8[3];
+            }
+          }
+#pragma unroll
+        for (int j = 0; j < G; ++j)
+          if (j0 + j < d8) {
+            const v4f y = *reinterpret_cast<const v4f*>(qr + 8 * (j0 + j) + 4 * h);
+            const float e0 = y.x - x[j].x, e1 = y.y - x[j].y, e2 = y.z - x[j].z, e3 = y.w - x[j].w;
+            l0 = __builtin_fmaf(e0, e0, l0);
+            l1 = __builtin_fmaf(e1, e1, l1);
+            l2 = __builtin_fmaf(e2, e2, l2);
+            l3 = __builtin_fmaf(e3, e3, l3);
+          }
+      }
+      const float lo = ((l0 + l1) + l2) + l3;
+      const float from_lo = __shfl(lo, lane & ~1);
+      if (h == 1) {
+        float tot = (((from_lo + l0) + l1) + l2) + l3;
+        for (int d = 8 * d8; d < a.dim; ++d) {
+          const float e = qr[d] - cr[d];
+          tot = tot + e * e;
+        }
+        cand[qi * cap + slot].y = __float_as_uint(tot);
+      }
+    }
+    __syncthreads();
+
+    // selection: a served query's candidate of rank r by (distance, centroid
+    // index) goes to probe slot r < np (distances are >= +0, so their bits
+    // order as the values do).  Wave w takes queries 8w .. 8w+7; lane l ranks
+    // candidate r0 + l against all, read sixteen at a time (every lane the
+    // same address; the padding keys never count) and compared from
+    // registers.
+    for (int t = 0; t < 32 / kW; ++t) {
+      const int qi = wave * (32 / kW) + t;
+      const uint32_t n = __builtin_amdgcn_readfirstlane(s_cnt[qi]);
+      const uint4* __restrict__ cq2 = reinterpret_cast<const uint4*>(cand + qi * cap);
+      const uint64_t qq = q0 + (uint64_t)qi;
+      for (uint32_t r0 = 0; r0 < n; r0 += 64) {
+        const uint32_t j = r0 + (uint32_t)lane;
+        const uint2 me = j < n ? cand[qi * cap + j] : make_uint2(0xFFFFFFFFu, 0xFFFFFFFFu);
+        const uint64_t key = ((uint64_t)me.y << 32) | me.x;
+        uint32_t rank = 0;
+        for (uint32_t c0 = 0; c0 < n; c0 += 16) {
+          uint4 w[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) w[i] = cq2[c0 / 2 + i];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            rank += ((((uint64_t)w[i].y << 32) | w[i].x) < key) ? 1u : 0u;
+            rank += ((((uint64_t)w[i].w << 32) | w[i].z) < key) ? 1u : 0u;
           }
         }
-#pragma unroll
-      for (int j = 0; j < G; ++j)
-        if (j0 + j < d8) {
-          const v4f y = *reinterpret_cast<const v4f*>(qr + 8 * (j0 + j) + 4 * h);
-          const float e0 = y.x - x[j].x, e1 = y.y - x[j].y, e2 = y.z - x[j].z, e3 = y.w - x[j].w;
-          l0 = __builtin_fmaf(e0, e0, l0);
-          l1 = __builtin_fmaf(e1, e1, l1);
-          l2 = __builtin_fmaf(e2, e2, l2);
-          l3 = __builtin_fmaf(e3, e3, l3);
+        if (j < n && rank < (uint32_t)a.np) {
+          a.probes[qq * a.np + rank] = (int32_t)me.x;
+          if (a.dists) a.dists[qq * a.np + rank] = __uint_as_float(me.y);
         }
-    }
-    const float lo = ((l0 + l1) + l2) + l3;
-    const float from_lo = __shfl(lo, lane & ~1);
-    if (h == 1) {
-      float tot = (((from_lo + l0) + l1) + l2) + l3;
-      for (int d = 8 * d8; d < a.dim; ++d) {
-        const float e = qr[d] - cr[d];
-        tot = tot + e * e;
       }
-      cand[qi * cap + slot].y = __float_as_uint(tot);
     }
   }
-  __syncthreads();
+}
 
-  // selection: a served query's candidate of rank r by (distance, centroid
-  // index) goes to probe slot r < np (distances are >= +0, so their bits
-  // order as the values do).  Wave w takes queries 8w .. 8w+7; lane l ranks
-  // candidate r0 + l against all, read sixteen at a time (every lane the
-  // same address; the padding keys never count) and compared from
-  // registers.
-  for (int t = 0; t < 32 / kW; ++t) {
-    const int qi = wave * (32 / kW) + t;
-    const uint32_t n = __builtin_amdgcn_readfirstlane(s_cnt[qi]);
-    const uint4* __restrict__ cq2 = reinterpret_cast<const uint4*>(cand + qi * cap);
-    const uint64_t qq = q0 + (uint64_t)qi;
-    for (uint32_t r0 = 0; r0 < n; r0 += 64) {
-      const uint32_t j = r0 + (uint32_t)lane;
-      const uint2 me = j < n ? cand[qi * cap + j] : make_uint2(0xFFFFFFFFu, 0xFFFFFFFFu);
-      const uint64_t key = ((uint64_t)me.y << 32) | me.x;
-      uint32_t rank = 0;
-      for (uint32_t c0 = 0; c0 < n; c0 += 16) {
-        uint4 w[8];
+// One wave per screened query: the exact distance of each candidate in the
+// reference's order (a lane per candidate: FMA lanes 0..7 over the 8-float
+// chunks, lanes summed 0..7 in order, then the scalar tail), then each
+// candidate's rank by (distance bits, centroid index) gives its probe slot
+// (distances are >= +0, so their bits order as the values do).  Queries
+// flagged by the screening kernel are left to the exact kernel.
+__global__ __launch_bounds__(kT) void coarse16_rescore_kernel(C16Args a) {
+  __shared__ __align__(16) float qrow[kT / 64][256];
+  __shared__ uint2 keys[kT / 64][kMaxCap];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const uint64_t q = (uint64_t)blockIdx.x * (kT / 64) + wave;
+  if (q >= a.nq) return;
+  const uint32_t n = a.ncand[q];
+  if (n == 0) return;  // flagged (its flag is set): the exact kernel serves it
+  const int dim = a.dim;
+  float* __restrict__ qr = qrow[wave];
+  for (int d = lane; d < dim; d += 64) qr[d] = a.queries[q * (uint64_t)dim + d];
+  __builtin_amdgcn_wave_barrier();
+  const int d8 = dim / 8;
+  for (uint32_t c0 = 0; c0 < n; c0 += 64) {
+    const uint32_t c = c0 + (uint32_t)lane;
+    const bool has = c < n;
+    const uint32_t id = has ? a.cand[q * (uint64_t)a.cap + c] : 0u;
+    const float* __restrict__ cr = a.centroids + (uint64_t)id * dim;
+    float l[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w[i] = cq2[c0 / 2 + i];
+    for (int t = 0; t < 8; ++t) l[t] = 0.0f;
+    // chunks of 8 floats: groups of four chunks (32 floats), the next
+    // group's loads issued before the current group's products, then the
+    // chunks left one at a time
+    auto acc = [&](const v4f* x, int j0) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          rank += ((((uint64_t)w[i].y << 32) | w[i].x) < key) ? 1u : 0u;
-          rank += ((((uint64_t)w[i].w << 32) | w[i].z) < key) ? 1u : 0u;
+      for (int u = 0; u < 8; ++u) {
+        const v4f y = *reinterpret_cast<const v4f*>(qr + 8 * j0 + 4 * u);
+        const int t0 = 4 * (u & 1);
+        const float e0 = y.x - x[u].x, e1 = y.y - x[u].y, e2 = y.z - x[u].z, e3 = y.w - x[u].w;
+        l[t0] = __builtin_fmaf(e0, e0, l[t0]);
+        l[t0 + 1] = __builtin_fmaf(e1, e1, l[t0 + 1]);
+        l[t0 + 2] = __builtin_fmaf(e2, e2, l[t0 + 2]);
+        l[t0 + 3] = __builtin_fmaf(e3, e3, l[t0 + 3]);
+      }
+    };
+    auto load4 = [&](v4f* x, int j0) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = *reinterpret_cast<const v4f*>(cr + 8 * j0 + 4 * u);
+    };
+    int j = 0;
+    if (a.vec) {
+      const int ng = d8 / 4;
+      v4f xa[8], xb[8];
+      if (ng > 0) load4(xa, 0);
+      for (int g = 0; g < ng; g += 2) {
+        if (g + 1 < ng) load4(xb, 4 * (g + 1));
+        acc(xa, 4 * g);
+        if (g + 1 < ng) {
+          if (g + 2 < ng) load4(xa, 4 * (g + 2));
+          acc(xb, 4 * (g + 1));
         }
       }
-      if (j < n && rank < (uint32_t)a.np) {
-        a.probes[qq * a.np + rank] = (int32_t)me.x;
-        if (a.dists) a.dists[qq * a.np + rank] = __uint_as_float(me.y);
+      j = 4 * ng;
+      for (; j < d8; ++j) {
+        const v4f x0 = *reinterpret_cast<const v4f*>(cr + 8 * j);
+        const v4f x1 = *reinterpret_cast<const v4f*>(cr + 8 * j + 4);
+        const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const float e = qr[8 * j + t] - x[t];
+          l[t] = __builtin_fmaf(e, e, l[t]);
+        }
       }
+    }
+    for (; j < d8; ++j) {
+      float x[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) x[t] = cr[8 * j + t];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const float e = qr[8 * j + t] - x[t];
+        l[t] = __builtin_fmaf(e, e, l[t]);
+      }
+    }
+    float tot = l[0];
+#pragma unroll
+    for (int t = 1; t < 8; ++t) tot = tot + l[t];
+    for (int d = 8 * d8; d < dim; ++d) {
+      const float e = qr[d] - cr[d];
+      tot = tot + e * e;
+    }
+    if (has) keys[wave][c] = make_uint2(id, __float_as_uint(tot));  // c < n <= cap <= kMaxCap
+  }
+  __builtin_amdgcn_wave_barrier();
+  // ranks: every candidate against all n, read as LDS broadcasts
+  const uint2* __restrict__ kw = keys[wave];
+  for (uint32_t c0 = 0; c0 < n; c0 += 64) {
+    const uint32_t c = c0 + (uint32_t)lane;
+    const uint2 me = c < n ? kw[c] : make_uint2(0u, 0u);
+    const uint64_t key = ((uint64_t)me.y << 32) | me.x;
+    uint32_t rank = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+      const uint2 o = kw[i];
+      rank += ((((uint64_t)o.y << 32) | o.x) < key) ? 1u : 0u;
+    }
+    if (c < n && rank < (uint32_t)a.np) {
+      a.probes[q * a.np + rank] = (int32_t)me.x;
+      if (a.dists) a.dists[q * a.np + rank] = __uint_as_float(me.y);
     }
   }
 }
@@ -600,6 +738,10 @@ void Coarse16::select(const float* d_qs, uint64_t nq, uint32_t np, const float* 
   a.probes = probes;
   a.dists = dists;
   a.flags = flags;
+  cand_.reserve(nq * (uint64_t)a.cap);
+  ncand_.reserve(nq);
+  a.cand = cand_.p;
+  a.ncand = ncand_.p;
   const size_t lds = (size_t)32 * (16 * KC_ + 4) * 4 + (size_t)32 * a.cap * 8;
   const bool m16 = np > 32;  // 8 M >= np kept minima per query
   // the kept minima ([32][8 M + 4] floats) are held in the candidate slots
@@ -618,6 +760,10 @@ void Coarse16::select(const float* d_qs, uint64_t nq, uint32_t np, const float* 
   FDB_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
   hipLaunchKernelGGL(fn, dim3((unsigned)cdiv(nq, 32)), dim3(kCT), lds, s, a);
   FDB_HIP(hipGetLastError());
+  if (m16) {
+    hipLaunchKernelGGL(coarse16_rescore_kernel, dim3((unsigned)cdiv(nq, kT / 64)), dim3(kT), 0, s, a);
+    FDB_HIP(hipGetLastError());
+  }
 }
 
 }  // namespace fdb

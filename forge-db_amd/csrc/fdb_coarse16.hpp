@@ -62,6 +62,7 @@ class Coarse16 {
   DevBuf<uint4> blocks_;  // [nblk][KC][64] A operands
   DevBuf<float> cnp_;     // [nblk][2][16]: each half-lane's 16 |c|^2 (+inf past nlist)
   DevBuf<uint32_t> stats_;
+  DevBuf<uint32_t> cand_, ncand_;  // [nq][cap] screened candidates and their counts (per call)
 };
 
 }  // namespace fdb
