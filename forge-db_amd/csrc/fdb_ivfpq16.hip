@@ -255,7 +255,9 @@ constexpr uint32_t kHistMax = 8192;  // lists counted in LDS (32 KiB)
 constexpr int kSortT = 1024;         // threads of a sorting workgroup
 constexpr int kSortB = 8;            // pairs a sorting thread loads at once
 constexpr int kSortWG = 256;         // sorting workgroups per stage (at most)
-constexpr uint32_t kCB = 64;         // blocks of 32 codes per screening tile (at most)
+constexpr uint32_t kCB = 64;         // blocks of 32 codes per screening tile
+constexpr uint32_t kCBDyn = 256;     // the same for size-sorted tiles taken from counters
+constexpr uint32_t kCBMax = 256;     // at most (8 bits of a candidate entry)
 constexpr uint32_t kXcd = 8;         // L2 domains (XCDs); workgroup b runs on XCD b % 8
 constexpr uint32_t kXcdRun = 4;      // consecutive tiles given to one XCD (static tiles)
 constexpr uint32_t kXcdRunDyn = 16;  // the same for dynamically taken tiles
@@ -302,7 +304,7 @@ struct PairStages {
   PairSet s0, s1;
   uint32_t blim0, blim1;  // blocks screened per list
   uint32_t tq0, tq1;      // pairs per tile
-  uint32_t cb0, cb1;      // blocks per tile (at most kCB)
+  uint32_t cb0, cb1;      // blocks per tile (at most kCBMax)
   uint32_t* cnt;          // [2][nlist], zero between searches
   uint32_t* qoff;
   uint32_t* toff;
@@ -381,7 +383,7 @@ __device__ __forceinline__ uint32_t block_prefix(uint32_t v, uint32_t* ws, uint3
 //   counters are zeroed.
 __global__ __launch_bounds__(kSortT) void pq16_offsets_kernel(PairStages ps, const uint32_t* __restrict__ bo) {
   constexpr int kU = kHistMax / kSortT;
-  constexpr uint32_t kKeys = kCB * 8 + 1;  // tile sizes 0 .. 64 blocks x 8 groups
+  constexpr uint32_t kKeys = kCBMax * 8 + 1;  // tile sizes 0 .. 256 blocks x 8 groups
   const uint32_t stage = blockIdx.x;
   const uint32_t nlist = ps.s0.nlist;
   const uint32_t blim = stage ? ps.blim1 : ps.blim0;
@@ -659,7 +661,7 @@ struct ScreenArgs {
   const uint4* desc;  // tile descriptors: list | blocks << 16, first pair, list's pair end, first block
   const uint2* qlist;
   uint32_t blim;  // blocks screened per list at most
-  uint32_t cb;    // blocks per tile (at most kCB)
+  uint32_t cb;    // blocks per tile (at most kCBMax)
   uint32_t* tctr;  // the stage's kXcd tile counters (zero at launch)
   uint32_t dyn;    // tiles taken from the counters (else a static stride)
   uint32_t run;    // consecutive tiles per XCD
@@ -1011,7 +1013,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
 //   the list's end have |x^|^2 = +inf, so s' = +inf; they are masked
 //   explicitly only where T' is +inf.
 //   Candidates: a lane with a passing row appends one 32-bit entry (row
-//   mask | block in the chunk << 16 | lane << 22) to its wave's LDS queue
+//   mask | block in the chunk << 16 | lane << 24 | group << 30) to its wave's LDS queue
 //   at the rank ballot and mbcnt give it: no atomics while blocks stream,
 //   so the ring's loads stay in flight (an atomic with return waits for
 //   every outstanding load).  At the end of the tile (or when the queue is
@@ -1089,8 +1091,8 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(W))) vo
       for (uint32_t i0 = 0; i0 < qn; i0 += 64) {
         const uint32_t i = i0 + (uint32_t)lane;
         const uint32_t ent = i < qn ? myq[i] : 0u;
-        const int owner = (int)((ent >> 22) & 63);
-        const int g = PG > 1 ? (int)((ent >> 28) & 1) : 0;
+        const int owner = (int)((ent >> 24) & 63);
+        const int g = PG > 1 ? (int)((ent >> 30) & 1) : 0;
         uint32_t oq = (uint32_t)__shfl((int)q[0], owner), oj = (uint32_t)__shfl((int)j[0], owner);
         if constexpr (PG > 1) {
           const uint32_t oq1 = (uint32_t)__shfl((int)q[PG - 1], owner), oj1 = (uint32_t)__shfl((int)j[PG - 1], owner);
@@ -1100,7 +1102,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(W))) vo
         if (i < qn) {
           const uint32_t pos = atomicAdd(&wbase[wave][g][owner], 1u);
           if (pos < a.cap) {
-            const uint32_t rowb = (bb + ((ent >> 16) & 63)) * 32 + 4 * (uint32_t)(owner >> 5);
+            const uint32_t rowb = (bb + ((ent >> 16) & 255)) * 32 + 4 * (uint32_t)(owner >> 5);
             a.cand[(uint64_t)oq * a.cap + pos] = make_uint2(start + rowb, (oj << 16) | (ent & 0xFFFFu));
           }
         }
@@ -1164,7 +1166,7 @@ __global__ __launch_bounds__(64 * WV) __attribute__((amdgpu_waves_per_eu(W))) vo
         if (passm != 0) {
           const uint32_t rank =
               __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-          myq[qn + rank] = passm | ((b - bb) << 16) | ((uint32_t)lane << 22) | ((uint32_t)g << 28);
+          myq[qn + rank] = passm | ((b - bb) << 16) | ((uint32_t)lane << 24) | ((uint32_t)g << 30);
           ++cnt[g];
         }
         qn += (uint32_t)__popcll(bal);
@@ -2180,7 +2182,15 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
       (uint32_t)std::min<uint64_t>(std::max<uint64_t>(cdiv(npr, (uint64_t)kSortT * kSortB), 1), kSortWG);
   const uint64_t chunk = cdiv(npr, G);
   // tiles of a stage: at most (pairs / 128 + lists) pair tiles per chunk
-  const uint32_t cbB = kCB;
+  // Large indexes (tens of tiles per resident workgroup) take their tiles
+  // from per-XCD counters in descending order of size, so that the last
+  // tiles are short.  Measured at 10M x 96 codes (nlist 4096, nprobe 64):
+  // stage B 1.56-1.60 ms against 1.81 with the static stride; at 1M x 128
+  // (nlist 1024, nprobe 16; ~3 tiles per workgroup) the static stride over
+  // tiles in list order was faster (0.175 against 0.185 ms).  Sorted tiles
+  // hold up to kCBDyn blocks: fewer tiles, so less of the per-tile setup.
+  const bool dyn = a.tiles >= 0 ? a.tiles == 1 : L.nblocks >= 512ull * (uint64_t)ncu_;
+  const uint32_t cbB = dyn ? kCBDyn : kCB;
   auto tile_bound = [&](uint32_t blim, uint32_t cb) {
     return (cdiv(npr, kTilePairs) + nlist) * cdiv(std::min<uint64_t>(L.max_blocks, blim), cb);
   };
@@ -2194,13 +2204,6 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   pst.blim1 = 0xFFFFFFFFu;
   pst.tq0 = kTilePairs;
   const int wvB = stage_b_wgwaves(L.KC);
-  // Large indexes (tens of tiles per resident workgroup) take their tiles
-  // from per-XCD counters in descending order of size, so that the last
-  // tiles are short.  Measured at 10M x 96 codes (nlist 4096, nprobe 64):
-  // stage B 1.56-1.60 ms against 1.81 with the static stride; at 1M x 128
-  // (nlist 1024, nprobe 16; ~3 tiles per workgroup) the static stride over
-  // tiles in list order was faster (0.175 against 0.185 ms).
-  const bool dyn = a.tiles >= 0 ? a.tiles == 1 : L.nblocks >= 512ull * (uint64_t)ncu_;
   pst.sort = dyn ? 1u : 0u;
   pst.tq1 = 32 * wvB * stage_b_groups(L.KC);
   pst.cb0 = kCB;
