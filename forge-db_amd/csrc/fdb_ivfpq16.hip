@@ -2191,10 +2191,11 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   // hold up to kCBDyn blocks: fewer tiles, so less of the per-tile setup.
   const bool dyn = a.tiles >= 0 ? a.tiles == 1 : L.nblocks >= 512ull * (uint64_t)ncu_;
   const uint32_t cbB = dyn ? kCBDyn : kCB;
+  const uint32_t cbA = dyn ? kCBDyn : kCB;
   auto tile_bound = [&](uint32_t blim, uint32_t cb) {
     return (cdiv(npr, kTilePairs) + nlist) * cdiv(std::min<uint64_t>(L.max_blocks, blim), cb);
   };
-  const uint64_t tbA = tile_bound(capA / 32, kCB), tbB = tile_bound(0xFFFFFFFFu, cbB);
+  const uint64_t tbA = tile_bound(capA / 32, cbA), tbB = tile_bound(0xFFFFFFFFu, cbB);
   desc_.reserve(std::max<uint64_t>(tbA + tbB, 1));
   // both stages' pairs grouped by list: 0 the first lists, 1 every probe
   PairStages pst{};
@@ -2206,7 +2207,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   const int wvB = stage_b_wgwaves(L.KC);
   pst.sort = dyn ? 1u : 0u;
   pst.tq1 = 32 * wvB * stage_b_groups(L.KC);
-  pst.cb0 = kCB;
+  pst.cb0 = cbA;
   pst.cb1 = cbB;
   pst.cnt = cnt_.p;
   pst.qoff = qoff_.p;
@@ -2283,7 +2284,7 @@ void Pq16Searcher::search(const Pq16Lists& L, const Pq16SearchArgs& a, hipStream
   sa.desc = desc_.p;
   sa.qlist = qlist_.p;
   sa.blim = capA / 32;
-  sa.cb = kCB;
+  sa.cb = cbA;
   sa.tctr = tctr_.p;
   sa.dyn = dyn ? 1u : 0u;
   sa.run = dyn ? kXcdRunDyn : kXcdRun;
