@@ -65,10 +65,12 @@ __global__ __launch_bounds__(kThreads) void coarse_select_kernel(
   const int d8 = D8T ? D8T : dim / 8;
   if (only) {
     // only the workgroups holding a flagged query run; the others' lists
-    // are already written (and would be the same)
-    bool any = false;
-    for (int i = 0; i < kCoarseQB; ++i) any = any || (q0 + i < nq && only[q0 + i] != 0);
-    if (!any) return;
+    // are already written (and would be the same).  Lane i < kCoarseQB of
+    // each wave reads query i's flag: one load and a ballot, not a chain of
+    // loads.
+    static_assert(kCoarseQB <= 64, "a wave reads the workgroup's flags");
+    const bool f = lane < kCoarseQB && q0 + lane < nq && only[q0 + lane] != 0;
+    if (__ballot(f) == 0) return;
   }
 
   for (int e = tid; e < kCoarseQB * dim; e += kThreads) {
