@@ -1211,30 +1211,34 @@ __global__ __launch_bounds__(64) void pq16_select_kernel(const float* __restrict
   const f4* __restrict__ v = reinterpret_cast<const f4*>(bufA + q * capA);
   const uint32_t n4 = (n + 3) / 4;  // n is a multiple of 32 or capA
   const f4 none = {f_inf(), f_inf(), f_inf(), f_inf()};
-  // k <= 64 (k <= 128): each lane's smallest value (two smallest) goes in
+  // k <= 64 (k <= 128): each lane's smallest value (four smallest) goes in
   // first; the k-th smallest of those bounds the k-th overall, so that few of
   // the others get past the list's threshold (one merge instead of one per
   // 64 early values, and few insertions after it).  Every value is offered
   // once either way.
-  uint32_t skip = kNoPos, skip2 = kNoPos;
-  if constexpr (R <= 2) {
-    float mn = f_inf(), mn2 = f_inf();
+  constexpr int S = R == 1 ? 1 : (R == 2 ? 4 : 0);  // seeds per lane
+  uint32_t si[S > 0 ? S : 1];
+#pragma unroll
+  for (int j = 0; j < (S > 0 ? S : 1); ++j) si[j] = kNoPos;
+  if constexpr (S > 0) {
+    float ms[S];
+#pragma unroll
+    for (int j = 0; j < S; ++j) ms[j] = f_inf();
+    // sorted insertion of (x, i) into the lane's S smallest
     auto seed = [&](float x, uint32_t i) {
-      if constexpr (R == 2) {
-        if (x < mn2) {
-          if (x < mn) {
-            mn2 = mn;
-            skip2 = skip;
-            mn = x;
-            skip = i;
-          } else {
-            mn2 = x;
-            skip2 = i;
-          }
+#pragma unroll
+      for (int j = S - 1; j > 0; --j) {
+        if (x < ms[j - 1]) {
+          ms[j] = ms[j - 1];
+          si[j] = si[j - 1];
+        } else if (x < ms[j]) {
+          ms[j] = x;
+          si[j] = i;
         }
-      } else if (x < mn) {
-        mn = x;
-        skip = i;
+      }
+      if (x < ms[0]) {
+        ms[0] = x;
+        si[0] = i;
       }
     };
 #pragma unroll 1
@@ -1247,20 +1251,26 @@ __global__ __launch_bounds__(64) void pq16_select_kernel(const float* __restrict
       seed(w.z, i + 2);
       seed(w.w, i + 3);
     }
-    tk.offer_queued(mn, skip, mn < f_inf(), queue, qn);
-    if constexpr (R == 2) tk.offer_queued(mn2, skip2, mn2 < f_inf(), queue, qn);
+#pragma unroll
+    for (int j = 0; j < S; ++j) tk.offer_queued(ms[j], si[j], ms[j] < f_inf(), queue, qn);
     tk.flush(queue, qn);
   }
+  auto seeded = [&](uint32_t i) {
+    bool r = false;
+#pragma unroll
+    for (int j = 0; j < (S > 0 ? S : 1); ++j) r = r || i == si[j];
+    return r;
+  };
   f4 w = (uint32_t)lane < n4 ? v[lane] : none;
 #pragma unroll 1
   for (uint32_t i0 = 0; i0 < n4; i0 += 64) {
     const uint32_t inext = i0 + 64 + (uint32_t)lane;
     const f4 wn = inext < n4 ? v[inext] : none;  // the next values in flight
     const uint32_t i = 4 * (i0 + (uint32_t)lane);
-    tk.offer_queued(w.x, i, w.x < f_inf() && i != skip && i != skip2, queue, qn);
-    tk.offer_queued(w.y, i + 1, w.y < f_inf() && i + 1 != skip && i + 1 != skip2, queue, qn);
-    tk.offer_queued(w.z, i + 2, w.z < f_inf() && i + 2 != skip && i + 2 != skip2, queue, qn);
-    tk.offer_queued(w.w, i + 3, w.w < f_inf() && i + 3 != skip && i + 3 != skip2, queue, qn);
+    tk.offer_queued(w.x, i, w.x < f_inf() && !seeded(i), queue, qn);
+    tk.offer_queued(w.y, i + 1, w.y < f_inf() && !seeded(i + 1), queue, qn);
+    tk.offer_queued(w.z, i + 2, w.z < f_inf() && !seeded(i + 2), queue, qn);
+    tk.offer_queued(w.w, i + 3, w.w < f_inf() && !seeded(i + 3), queue, qn);
     w = wn;
   }
   tk.flush(queue, qn);
