@@ -399,7 +399,10 @@ __global__ __launch_bounds__(kSortT) void pq16_offsets_kernel(PairStages ps, con
   __shared__ uint32_t tbr[kHistMax];  // tiles by rank, then their prefix
   const int tid = threadIdx.x;
   if (tid < (int)kXcd) ps.tctr[stage * kXcd + tid] = 0u;
-  for (uint32_t i = tid; i < kKeys; i += kSortT) hist[i] = 0;
+  // (the histogram ranks the lists by tile size; unsorted, a list's rank is
+  // its index and the histogram is skipped)
+  if (sort)
+    for (uint32_t i = tid; i < kKeys; i += kSortT) hist[i] = 0;
   // every list's count and block count first
   uint32_t c[kU], nb[kU];
 #pragma unroll
@@ -422,13 +425,13 @@ __global__ __launch_bounds__(kSortT) void pq16_offsets_kernel(PairStages ps, con
       const uint32_t pre = block_prefix(cu, ws, carry);
       if (i < nlist) qoff[i] = pre;
     }
-    rin[u] = i < nlist ? atomicAdd(&hist[key[u]], 1u) : 0u;
+    rin[u] = sort && i < nlist ? atomicAdd(&hist[key[u]], 1u) : 0u;
   }
   if (tid == 0) qoff[nlist] = carry;
   __syncthreads();
   // bucket starts in descending key order (wave 0: lane l sums keys
   // kKeys-1-9l .. kKeys-9-9l)
-  if (tid < 64) {
+  if (sort && tid < 64) {
     constexpr int kPer = (kKeys + 63) / 64;
     uint32_t sum = 0;
 #pragma unroll
@@ -458,8 +461,7 @@ __global__ __launch_bounds__(kSortT) void pq16_offsets_kernel(PairStages ps, con
 #pragma unroll
   for (int u = 0; u < kU; ++u) {
     const uint32_t i = u * kSortT + tid;
-    rank[u] = i < nlist ? hist[key[u]] + rin[u] : 0u;
-    if (!sort) rank[u] = i < nlist ? i : 0u;
+    rank[u] = i >= nlist ? 0u : sort ? hist[key[u]] + rin[u] : i;
     if (i < nlist) tbr[rank[u]] = t[u];
   }
   __syncthreads();
